@@ -1,0 +1,236 @@
+#!/usr/bin/env python3
+"""FP8 GEMM throughput on one MI355X (BASELINE.json metric).
+
+    python bench.py [--steps K] [--warmup W] [--shape M,N,K] [--variant auto]
+
+A step is one GEMM launch (C = sa*sb * A . B_T^T, e4m3 in, fp32 accumulate,
+bf16 out) through the C ABI on inputs already resident in HBM.  Default
+workload: M = N = K = 8192, normal(0, 1) e4m3
+inputs, per-tensor scales uniform in [0.5, 2], rotating A/B sets totalling at
+least 512 MiB so consecutive launches do not hit in the 256 MB MALL (the
+reference's bench.cpp:24 does the same).
+
+Prints ONE JSON line on stdout (rank 0, N = 1):
+  value      whole-job TFLOP/s = 2*M*N*K*steps / wall time of the timed loop
+  roofline   the GEMM kernel's average duration from HIP events recorded on
+             its own stream around every timed launch -> achieved TFLOP/s
+             against the 5.0 PFLOP/s dense-FP8 MFMA peak; `traffic` (HBM bytes
+             per launch) comes from the committed rocprofv3 FETCH_SIZE /
+             WRITE_SIZE summary for this workload when one exists
+  cpu_baseline  the reference's CPU GEMM (test.cpp:19-30, built from its
+             sources into oracle/_ref) -- or the oracle port of it when that
+             build is absent -- timed on a row slab of the same workload
+Diagnostics go to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP8_TFLOPS = 5000.0      # MI355X dense FP8 MFMA peak (published)
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E (published)
+ROTATE_BYTES = 512 << 20      # bench.cpp:24
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--shape", default="8192,8192,8192",
+                    help="M,N,K of the timed GEMM")
+    ap.add_argument("--variant", default="auto")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target CPU time of the cpu_baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def traffic_for(workload: str, variant: str):
+    """HBM bytes per launch from the committed rocprof summary, if any."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            table = json.load(f)
+        ent = table.get(workload, {}).get(variant)
+        return None if ent is None else ent.get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(A_host, B_host, M, N, K, target_s):
+    """Time the reference CPU GEMM on rows [0, R) of the workload."""
+    import numpy as np
+    from oracle import pyoracle as po
+    kind = "reference"
+    try:
+        ref = po.RefLib()
+        fn = ref.gemm_cpu
+
+        def run(rows):
+            return fn(np.ascontiguousarray(A_host[:rows]), B_host)
+        try:
+            omp = ctypes.CDLL("/opt/rocm/llvm/lib/libomp.so")
+            cores = int(omp.omp_get_max_threads())
+        except OSError:
+            cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count()))
+        what = "reference gemm_cpu (test.cpp:19-30) built from its sources"
+    except (FileNotFoundError, OSError):
+        kind = "port"
+        o = po.get()
+
+        def run(rows):
+            return o.gemm(np.ascontiguousarray(A_host[:rows]), B_host,
+                          faithful=True)
+        cores = o.num_threads()
+        what = "oracle port of gemm_cpu (oracle/oracle.c hg_gemm_ref)"
+    rows = 8
+    t0 = time.perf_counter()
+    run(rows)
+    t = time.perf_counter() - t0
+    rows = int(max(8, min(M, rows * target_s / max(t, 1e-3))))
+    t0 = time.perf_counter()
+    run(rows)
+    t = time.perf_counter() - t0
+    tflops = 2.0 * rows * N * K / t / 1e12
+    return {
+        "value": round(tflops, 6), "unit": "TFLOP/s", "cores": cores,
+        "kind": kind,
+        "sample": (f"rows 0..{rows - 1} of the {M}x{N}x{K} workload "
+                   f"({rows}x{N}x{K}, {t:.1f} s, {what}); TFLOP/s of the "
+                   f"slab, which equals the full-size rate (cost is linear "
+                   f"in M)"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} "
+              "is not supported (the GEMM shards by M or N with no exchange; "
+              "see DESIGN.md).", file=sys.stderr)
+        return 2
+    import numpy as np
+    import torch
+
+    import hipgemm_amd as hg
+
+    M, N, K = (int(x) for x in args.shape.split(","))
+    variant = hg.VARIANTS.get(args.variant)
+    if variant is None:
+        raise SystemExit(f"unknown variant {args.variant}")
+    vname = hg.variant_name(hg.select_variant(M, N, K) if variant == 0
+                            else variant)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    hg.lib()
+
+    per_set = M * K + N * K
+    nsets = max(1, math.ceil(ROTATE_BYTES / per_set))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2024)
+    As, Bs = [], []
+    for _ in range(nsets):
+        As.append(torch.randn((M, K), generator=gen, device=dev)
+                  .clamp_(-448, 448).to(torch.float8_e4m3fn))
+        Bs.append(torch.randn((N, K), generator=gen, device=dev)
+                  .clamp_(-448, 448).to(torch.float8_e4m3fn))
+    sa = (torch.rand(1, generator=gen, device=dev) * 1.5 + 0.5)
+    sb = (torch.rand(1, generator=gen, device=dev) * 1.5 + 0.5)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    torch.cuda.synchronize()
+    log(f"bench: {M}x{N}x{K} variant={vname} rotating_sets={nsets} "
+        f"steps={args.steps} warmup={args.warmup}")
+
+    def launch(i):
+        hg.fp8_gemm_bf16(As[i % nsets], Bs[i % nsets], sa, sb, out,
+                         variant=variant, stream=stream)
+
+    for i in range(args.warmup):
+        launch(i)
+    torch.cuda.synchronize()
+
+    ev = [(torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        launch(args.warmup + i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_ms = np.array([a.elapsed_time(b) for a, b in ev])
+
+    flop = 2.0 * M * N * K
+    ms_per_step = wall * 1e3 / args.steps
+    value = flop / (ms_per_step * 1e-3) / 1e12
+    avg_ms = float(kern_ms.mean())
+    achieved = flop / (avg_ms * 1e-3) / 1e12
+    log(f"bench: kernel ms avg={avg_ms:.4f} median={np.median(kern_ms):.4f} "
+        f"best={kern_ms.min():.4f} -> {achieved:.1f} TFLOP/s avg, "
+        f"{flop / (kern_ms.min() * 1e-3) / 1e12:.1f} best; wall/step "
+        f"{ms_per_step:.4f} ms")
+
+    workload = f"fp8_gemm_{M}x{N}x{K}"
+    result = {
+        "metric": "FP8 GEMM TFLOP/s at M=N=K=8192 (% of dense FP8 peak)",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3",
+        "data": "synthetic",
+        "config": {
+            "workload": workload,
+            "M": M, "N": N, "K": K,
+            "inputs": "normal(0,1) clipped +-448 -> e4m3, per-tensor fp32 "
+                      "scales U[0.5,2)",
+            "accumulate": "fp32", "output": "bf16",
+            "variant": vname, "rotating_sets": nsets,
+            "pct_of_peak": round(100.0 * value / PEAK_FP8_TFLOPS, 2),
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": PEAK_FP8_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
+            "traffic": traffic_for(workload, vname),
+            "kernel_ms_avg": round(avg_ms, 5),
+            "kernel_ms_best": round(float(kern_ms.min()), 5),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        A_host = As[0].view(torch.uint8).cpu().numpy()
+        B_host = Bs[0].view(torch.uint8).cpu().numpy()
+        result["cpu_baseline"] = cpu_baseline(A_host, B_host, M, N, K,
+                                              args.cpu_seconds)
+        log(f"bench: cpu_baseline {result['cpu_baseline']}")
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

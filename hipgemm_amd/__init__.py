@@ -1,0 +1,242 @@
+"""hipgemm_amd -- MI355X (gfx950) FP8 e4m3 GEMM with bf16 output.
+
+Host side of the library.  The compute path is libhipgemm.so (hand-written
+HIP kernels for CDNA4 behind the C ABI of include/hipgemm.h); this module
+binds that ABI with ctypes and, for convenience, accepts torch tensors, whose
+device memory and current stream it passes through as plain pointers.
+
+There is no CPU or library fallback: if libhipgemm.so is missing or fails to
+load, every entry point raises HipGemmError.
+
+Reference (nirw4nna/hipgemm) interface mirrored here:
+  fp8_gemm_4wave_256x256x128(A, B_T, C)  -- the kernel of fp8_4wave.hpp:334-338
+      as launched at test.cpp:79 / bench.cpp:78: C (M x N bf16) = A (M x K
+      e4m3) . B_T (N x K e4m3)^T.
+  fp8_gemm_bf16(...)                      -- the same with runtime strides,
+      per-tensor scales, a stream and a schedule choice (C ABI
+      hipgemm_fp8_gemm_bf16).
+Argument errors raise HipGemmError (the C ABI returns hipErrorInvalidValue);
+the reference has no error path (fp8_4wave.hpp has no shape checks).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from typing import Optional
+
+__all__ = [
+    "HipGemmError", "lib", "lib_path", "fp8_gemm_bf16", "fp8_gemm",
+    "fp8_gemm_4wave_256x256x128", "gemm_raw", "select_variant",
+    "variant_name", "version", "tile_order", "lds_slot", "VARIANTS",
+    "declared_symbols",
+]
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_ROOT = os.path.dirname(_HERE)
+_LIB_PATH = os.path.join(_HERE, "libhipgemm.so")
+_HEADER = os.path.join(_ROOT, "include", "hipgemm.h")
+
+VARIANTS = {"auto": 0, "4wave": 1}
+
+hipSuccess = 0
+hipErrorInvalidValue = 1
+
+
+class HipGemmError(RuntimeError):
+    """Raised for a missing library, bad arguments or a failed launch."""
+
+    def __init__(self, msg: str, code: int = -1):
+        super().__init__(msg)
+        self.code = code
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib_path() -> str:
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    """Load libhipgemm.so (once).  Raises HipGemmError if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIB_PATH):
+        raise HipGemmError(
+            f"{_LIB_PATH} is not built; run `python -m hipgemm_amd.build` "
+            "(or __graft_entry__.build()).  There is no fallback path.")
+    try:
+        L = ctypes.CDLL(_LIB_PATH)
+    except OSError as e:  # pragma: no cover - depends on the machine
+        raise HipGemmError(f"cannot load {_LIB_PATH}: {e}") from e
+    vp, ci = ctypes.c_void_p, ctypes.c_int
+    L.hipgemm_fp8_gemm_bf16.argtypes = [vp, vp, vp, ci, ci, ci, ci, ci, ci,
+                                        vp, vp, ci, vp]
+    L.hipgemm_fp8_gemm_bf16.restype = ci
+    L.hipgemm_fp8_gemm_4wave_256x256x128.argtypes = [vp, vp, vp, ci, ci, ci,
+                                                     vp]
+    L.hipgemm_fp8_gemm_4wave_256x256x128.restype = ci
+    L.hipgemm_select_variant.argtypes = [ci, ci, ci]
+    L.hipgemm_select_variant.restype = ci
+    L.hipgemm_variant_name.argtypes = [ci]
+    L.hipgemm_variant_name.restype = ctypes.c_char_p
+    L.hipgemm_version.argtypes = []
+    L.hipgemm_version.restype = ci
+    L.hipgemm_tile_order.argtypes = [ci, ci, ci, ci, vp, vp, ci]
+    L.hipgemm_tile_order.restype = ci
+    L.hipgemm_lds_slot.argtypes = [ci, ci]
+    L.hipgemm_lds_slot.restype = ci
+    _lib = L
+    return L
+
+
+def declared_symbols() -> list:
+    """Function names declared in include/hipgemm.h."""
+    with open(_HEADER) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hipgemm_[a-z0-9_]+)\s*\(", text)))
+
+
+def _check(code: int, what: str) -> None:
+    if code != hipSuccess:
+        raise HipGemmError(f"{what} failed with hipError {code}", code)
+
+
+def gemm_raw(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int,
+             lda: int, ldb: int, ldc: int, scale_a_ptr: int = 0,
+             scale_b_ptr: int = 0, variant: int = 0, stream: int = 0) -> int:
+    """Call hipgemm_fp8_gemm_bf16 on raw device pointers; returns hipError_t."""
+    return int(lib().hipgemm_fp8_gemm_bf16(
+        a_ptr or None, b_ptr or None, c_ptr or None, M, N, K, lda, ldb, ldc,
+        scale_a_ptr or None, scale_b_ptr or None, variant, stream or None))
+
+
+def select_variant(M: int, N: int, K: int) -> int:
+    return int(lib().hipgemm_select_variant(M, N, K))
+
+
+def variant_name(v: int) -> Optional[str]:
+    r = lib().hipgemm_variant_name(v)
+    return r.decode() if r is not None else None
+
+
+def version() -> int:
+    return int(lib().hipgemm_version())
+
+
+def tile_order(grid: int, tiles_m: int, tiles_n: int, group_m: int = 0):
+    """(tile_m, tile_n) lists in the order the kernel's workgroups visit
+    tiles (host-side view, no GPU)."""
+    cap = tiles_m * tiles_n
+    tm = (ctypes.c_int * cap)()
+    tn = (ctypes.c_int * cap)()
+    n = lib().hipgemm_tile_order(grid, tiles_m, tiles_n, group_m,
+                                 ctypes.cast(tm, ctypes.c_void_p),
+                                 ctypes.cast(tn, ctypes.c_void_p), cap)
+    return list(tm[:n]), list(tn[:n])
+
+
+def lds_slot(row: int, chunk: int) -> int:
+    return int(lib().hipgemm_lds_slot(row, chunk))
+
+
+# -- torch convenience layer ----------------------------------------------
+
+
+def _torch():
+    import torch  # noqa: WPS433 - torch is optional for the raw ABI
+    return torch
+
+
+def _as_bytes_2d(t, name):
+    torch = _torch()
+    if t.dim() != 2:
+        raise HipGemmError(f"{name} must be 2-D, got {tuple(t.shape)}",
+                           hipErrorInvalidValue)
+    if t.dtype not in (torch.uint8, torch.float8_e4m3fn):
+        raise HipGemmError(f"{name} must be float8_e4m3fn or uint8 bytes, got "
+                           f"{t.dtype}", hipErrorInvalidValue)
+    if not t.is_cuda:
+        raise HipGemmError(f"{name} must be a device tensor",
+                           hipErrorInvalidValue)
+    if t.stride(1) != 1:
+        raise HipGemmError(f"{name} must have unit stride along K",
+                           hipErrorInvalidValue)
+    return t
+
+
+def _scale_ptr(s, name):
+    if s is None:
+        return 0
+    torch = _torch()
+    if not (isinstance(s, torch.Tensor) and s.is_cuda and
+            s.dtype == torch.float32 and s.numel() == 1):
+        raise HipGemmError(f"{name} must be a 1-element float32 device tensor",
+                           hipErrorInvalidValue)
+    return s.data_ptr()
+
+
+def fp8_gemm_bf16(a, b_t, scale_a=None, scale_b=None, out=None,
+                  variant: int = 0, stream=None):
+    """out[M, N] (bf16) = scale_a * scale_b * a[M, K] @ b_t[N, K].T.
+
+    a, b_t: device tensors of dtype float8_e4m3fn (or uint8 holding e4m3
+    bytes) with unit stride along K.  scale_a / scale_b: optional 1-element
+    float32 device tensors.  out: optional bf16 device tensor with unit column
+    stride; allocated if None.  Runs on `stream` (a torch.cuda.Stream) or the
+    current stream.
+    """
+    torch = _torch()
+    a = _as_bytes_2d(a, "a")
+    b_t = _as_bytes_2d(b_t, "b_t")
+    M, K = a.shape
+    N, K2 = b_t.shape
+    if K2 != K:
+        raise HipGemmError(f"K mismatch: a has {K}, b_t has {K2}",
+                           hipErrorInvalidValue)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    elif (out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or
+          (M > 0 and N > 0 and out.stride(1) != 1)):
+        raise HipGemmError("out must be a (M, N) bfloat16 tensor with unit "
+                           "column stride", hipErrorInvalidValue)
+    if stream is None:
+        stream = torch.cuda.current_stream(a.device)
+    lda = a.stride(0) if (M > 1 and K > 0) else max(K, 16)
+    ldb = b_t.stride(0) if (N > 1 and K > 0) else max(K, 16)
+    ldc = out.stride(0) if M > 1 else max(N, 1)
+    code = gemm_raw(a.data_ptr(), b_t.data_ptr(), out.data_ptr(), M, N, K,
+                    lda, ldb, ldc, _scale_ptr(scale_a, "scale_a"),
+                    _scale_ptr(scale_b, "scale_b"), variant,
+                    stream.cuda_stream)
+    _check(code, "hipgemm_fp8_gemm_bf16")
+    return out
+
+
+fp8_gemm = fp8_gemm_bf16
+
+
+def fp8_gemm_4wave_256x256x128(A, B_T, C, stream=None):
+    """Mirror of the reference launch (test.cpp:79): C = A @ B_T.T with packed
+    strides (lda = ldb = K, ldc = N), no scales, the 4-wave schedule."""
+    torch = _torch()
+    A = _as_bytes_2d(A, "A")
+    B_T = _as_bytes_2d(B_T, "B_T")
+    M, K = A.shape
+    N = B_T.shape[0]
+    if not (A.is_contiguous() and B_T.is_contiguous() and C.is_contiguous()):
+        raise HipGemmError("A, B_T and C must be contiguous",
+                           hipErrorInvalidValue)
+    if C.dtype != torch.bfloat16 or tuple(C.shape) != (M, N):
+        raise HipGemmError("C must be a contiguous (M, N) bfloat16 tensor",
+                           hipErrorInvalidValue)
+    if stream is None:
+        stream = torch.cuda.current_stream(A.device)
+    code = int(lib().hipgemm_fp8_gemm_4wave_256x256x128(
+        A.data_ptr(), B_T.data_ptr(), C.data_ptr(), M, N, K,
+        stream.cuda_stream or None))
+    _check(code, "hipgemm_fp8_gemm_4wave_256x256x128")
+    return C

@@ -1,0 +1,113 @@
+/*
+ * hipgemm -- C ABI of the MI355X (gfx950) FP8 GEMM.
+ *
+ *   C[M x N] = bf16_rne( (scale_a * scale_b) * sum_k A[m, k] * B_T[n, k] )
+ *
+ * A is M x K, row-major, e4m3 (OCP E4M3FN, one byte), row stride lda bytes.
+ * B_T is N x K, row-major (K contiguous), e4m3, row stride ldb bytes.
+ * C is M x N, row-major, bf16, row stride ldc elements.
+ * Accumulation is fp32.  scale_a / scale_b are DEVICE pointers to one fp32
+ * each (per-tensor scales), or NULL for 1.0; the product scale_a * scale_b is
+ * formed in fp32 and applied to the fp32 accumulator before rounding.
+ *
+ * The reference (nirw4nna/hipgemm) exposes only a C++ kernel template,
+ * fp8_gemm_4wave_256x256x128<M, N, K>(A, B_T, C) (fp8_4wave.hpp:334-338),
+ * launched by its callers as <<<(M*N)/65536, 256>>> on the null stream
+ * (test.cpp:79, bench.cpp:55, bench.cpp:78).  That surface is kept in
+ * include/hipgemm/fp8_gemm.hpp; these entry points are the plain-pointer
+ * boundary over it.  Plain pointers and sizes only.
+ *
+ * Errors: every entry point returns a hipError_t and never exits the
+ * process.  Argument errors return hipErrorInvalidValue before any HIP call,
+ * so they can be checked on a machine without a GPU.  Requirements:
+ *   M, N, K >= 0;  C non-NULL, 2-byte aligned, ldc >= N;
+ *   A, B_T non-NULL and 16-byte aligned;  K % 16 == 0;
+ *   lda >= K, ldb >= K, lda % 16 == 0, ldb % 16 == 0, lda, ldb <= 2^23.
+ * M == 0 or N == 0 is a no-op (nothing is checked or written).  K == 0
+ * writes bf16(0 * scale) everywhere and neither reads nor checks A, B_T,
+ * lda, ldb.
+ * Nothing outside the M x N window of C is written.
+ *
+ * Threading: no global mutable state; calls on different streams may run
+ * concurrently as long as their C windows do not overlap.
+ */
+#ifndef HIPGEMM_H
+#define HIPGEMM_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HIPGEMM_VERSION 100 /* 1.0.0 */
+
+/* Schedules.  AUTO picks by shape (hipgemm_select_variant). */
+enum {
+  HIPGEMM_VARIANT_AUTO = 0,
+  /* 256 threads (4 waves, one per SIMD), 256 x 256 tile, 4-stage LDS ring,
+   * v_mfma_f32_32x32x64_f8f6f4.  The schedule behind the drop-in template. */
+  HIPGEMM_VARIANT_4WAVE = 1,
+  HIPGEMM_VARIANT_COUNT = 2
+};
+
+/*
+ * Runtime-shape GEMM with scales and a stream.
+ * Replaces: fp8_gemm_4wave_256x256x128<M, N, K><<<(M*N)/65536, 256>>>(A, B_T,
+ * C) (fp8_4wave.hpp:334-338, launched at test.cpp:79 and bench.cpp:78), whose
+ * shapes are template constants, strides fixed at lda = ldb = K, ldc = N, with
+ * no scales and the null stream.
+ */
+hipError_t hipgemm_fp8_gemm_bf16(const void *A, const void *B_T, void *C,
+                                 int M, int N, int K, int lda, int ldb,
+                                 int ldc, const float *scale_a,
+                                 const float *scale_b, int variant,
+                                 hipStream_t stream);
+
+/*
+ * The reference launch with runtime shapes: packed strides (lda = ldb = K,
+ * ldc = N), no scales, the 4-wave schedule.
+ * Replaces: fp8_gemm_4wave_256x256x128<M, N, K><<<(M*N)/65536, 256>>>(A, B_T,
+ * C) at test.cpp:79 and bench.cpp:55/78.
+ */
+hipError_t hipgemm_fp8_gemm_4wave_256x256x128(const void *A, const void *B_T,
+                                              void *C, int M, int N, int K,
+                                              hipStream_t stream);
+
+/* Variant AUTO resolves to for this shape (no GPU needed). No reference
+ * counterpart (the reference has one schedule). */
+int hipgemm_select_variant(int M, int N, int K);
+
+/* Human-readable variant name, or NULL.  No reference counterpart. */
+const char *hipgemm_variant_name(int variant);
+
+/* HIPGEMM_VERSION of the built library.  No reference counterpart. */
+int hipgemm_version(void);
+
+/*
+ * Host-side view of the workgroup -> output-tile order a launch of `grid`
+ * workgroups uses over a tiles_m x tiles_n tile grid: fills tile_m[i],
+ * tile_n[i] for the i-th tile processed (workgroup-major: the tiles of
+ * workgroup b are b's first, second, ... tile).  Returns the number of
+ * entries written (at most cap).  For tests of the order's bijectivity; no
+ * GPU needed.  group_m <= 0 selects the library default.  Replaces the
+ * in-kernel remap at fp8_4wave.hpp:357-377 (not callable there).
+ */
+int hipgemm_tile_order(int grid, int tiles_m, int tiles_n, int group_m,
+                       int *tile_m, int *tile_n, int cap);
+
+/*
+ * Host-side view of the LDS tile layout: the 16-byte slot (0..3) at which
+ * K-chunk `chunk` (0..3) of tile row `row` sits inside its 64-byte LDS row.
+ * For tests of the bank-conflict-freedom of the layout; no GPU needed.
+ * Returns -1 for out-of-range arguments.  Replaces the swizzle helpers at
+ * fp8_4wave.hpp:136-177 (not callable there).
+ */
+int hipgemm_lds_slot(int row, int chunk);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HIPGEMM_H */

@@ -1,0 +1,124 @@
+// hipgemm -- gfx950 (CDNA4) device primitives.
+//
+// Everything here is a thin, named wrapper over one hardware facility:
+//   * buffer resources (V#) with hardware range checking, so out-of-range
+//     lanes read zero instead of faulting (ragged tiles, K tails);
+//   * direct global->LDS DMA (buffer_load_dwordx4 ... lds), 16 bytes per lane,
+//     written to LDS at M0 + 16*lane;
+//   * v_mfma_f32_32x32x64_f8f6f4 / v_mfma_f32_16x16x128_f8f6f4 with OCP e4m3
+//     operands (cbsz = blgp = 0) and fp32 accumulators;
+//   * explicit s_waitcnt / s_barrier / s_setprio placement;
+//   * v_cvt_pk_bf16_f32 (round-to-nearest-even fp32 -> bf16).
+//
+// Reference counterparts (nirw4nna/hipgemm): fp8_4wave.hpp:53-59 (MFMA
+// wrapper), :80-100 (raw.buffer.load.lds and the buffer resource), :214-217
+// (bf16 conversion, truncating there; RNE here).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace hipgemm {
+namespace detail {
+
+using i32x4 = int __attribute__((ext_vector_type(4)));
+using i32x8 = int __attribute__((ext_vector_type(8)));
+using u32x2 = unsigned __attribute__((ext_vector_type(2)));
+using f32x2 = float __attribute__((ext_vector_type(2)));
+using f32x4 = float __attribute__((ext_vector_type(4)));
+using f32x16 = float __attribute__((ext_vector_type(16)));
+using bf16x2_t = __bf16 __attribute__((ext_vector_type(2)));
+
+// LDS (address space 3) byte pointer.
+using lds_u8 = __attribute__((address_space(3))) uint8_t;
+
+constexpr int kWave = 64;
+
+// Word 3 of a gfx9 buffer resource: DATA_FORMAT (bits 18:15) = 4 (32-bit),
+// everything else zero -- no swizzle, no add-tid, stride 0 (raw buffer), so
+// the hardware range check is a plain byte-offset test against num_records.
+constexpr int kBufferWord3 = 0x00020000;
+
+// Any per-lane offset at or above this is out of range for every buffer we
+// build (num_records is always < 2^31): such a lane reads zero.
+constexpr uint32_t kOobOffset = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
+                                                           uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)bytes, kBufferWord3);
+}
+
+// 16 bytes per lane, global (rsrc + voffset + soffset) -> LDS
+// (lds_wave_base + 16 * lane).  lds_wave_base must be wave-uniform.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc,
+                                      lds_u8* lds_wave_base, uint32_t voffset,
+                                      uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rsrc, (__attribute__((address_space(3))) void*)lds_wave_base, 16,
+      (int)voffset, (int)soffset, 0, 0);
+}
+
+__device__ __forceinline__ i32x4 lds_read16(const lds_u8* p) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) i32x4*>(p);
+}
+
+__device__ __forceinline__ void lds_write8(lds_u8* p, u32x2 v) {
+  *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(p) = v;
+}
+
+__device__ __forceinline__ i32x8 join(i32x4 lo, i32x4 hi) {
+  return i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+}
+
+// D[32x32] += X[32x64] . Y[32x64]^T, e4m3 x e4m3 -> fp32.  Lane l carries
+// row l%32 of X (and of Y) and 32 of its 64 K-bytes.
+__device__ __forceinline__ f32x16 mfma_32x32x64(i32x8 x, i32x8 y, f32x16 acc) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(x, y, acc, 0, 0, 0, 0,
+                                                         0, 0);
+}
+
+// D[16x16] += X[16x128] . Y[16x128]^T, e4m3 x e4m3 -> fp32.
+__device__ __forceinline__ f32x4 mfma_16x16x128(i32x8 x, i32x8 y, f32x4 acc) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(x, y, acc, 0, 0, 0, 0,
+                                                          0, 0);
+}
+
+// Two fp32 -> packed bf16x2, round-to-nearest-even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2_t v = __builtin_convertvector(f32x2{lo, hi}, bf16x2_t);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Scalar wave index (a compile-time-unknown but wave-uniform value kept in an
+// SGPR, so LDS DMA destinations built from it need no readfirstlane).
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+}
+__device__ __forceinline__ int lane_id() { return threadIdx.x % kWave; }
+
+// Explicit counters.  The compiler does not order LDS reads after LDS-DMA
+// writes, so every stage hand-off below is an explicit vmcnt wait + barrier.
+// The "memory" clobbers keep the compiler from moving loads or stores across.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_lgkmcnt() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ void sched_fence() {
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+}  // namespace detail
+}  // namespace hipgemm

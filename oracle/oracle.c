@@ -1,0 +1,311 @@
+/*
+ * hipgemm oracle -- CPU restatement of the reference FP8 GEMM path.
+ * TEST INFRASTRUCTURE ONLY (see oracle.h for the contract and what pins each
+ * function).  Reference citations are file:line into nirw4nna/hipgemm.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static inline uint32_t f32_bits(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  return u;
+}
+static inline float bits_f32(uint32_t u) {
+  float x;
+  memcpy(&x, &u, 4);
+  return x;
+}
+
+/* ------------------------------------------------------------------------ */
+/* OCP E4M3FN ("fp8" of fp8_4wave.hpp:15).  1 sign, 4 exponent (bias 7), 3   */
+/* mantissa bits; exponent field 0 is subnormal (m * 2^-9); S.1111.111 is    */
+/* NaN; there is no infinity; the largest finite magnitude is 1.75*2^8=448.  */
+/* ------------------------------------------------------------------------ */
+float hg_e4m3_to_f32(uint8_t v) {
+  const int e = (v >> 3) & 15, m = v & 7;
+  float mag;
+  if (e == 15 && m == 7)
+    mag = NAN;
+  else if (e == 0)
+    mag = ldexpf((float)m, -9);
+  else
+    mag = ldexpf((float)(8 + m), e - 10);
+  return (v & 0x80) ? -mag : mag;
+}
+
+/* Round-to-nearest-even onto the e4m3 grid with saturation to +-448, the
+ * behaviour of the __hip_fp8_e4m3(float) constructor the reference uses
+ * (utils.hpp:32): its default is __HIP_SATFINITE, Inf and NaN both become
+ * NaN (0x7f | sign), magnitudes above 448 become 448.  Method: scale by the
+ * grid quantum of x's binade (a power of two, so exact), round to an integer
+ * with rintf (RNE in the default rounding mode), then re-encode the value. */
+uint8_t hg_f32_to_e4m3(float x) {
+  const uint32_t u = f32_bits(x);
+  const uint8_t sign = (uint8_t)((u >> 24) & 0x80);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a >= 0x7f800000u) return sign | 0x7f;   /* Inf, NaN -> NaN          */
+  if (a > 0x43e00000u) return sign | 0x7e;    /* |x| > 448 -> 448         */
+  const float ax = bits_f32(a);
+  int e2;
+  (void)frexpf(ax, &e2);                      /* ax = f * 2^e2, f in [.5,1) */
+  int E = e2 - 1;                             /* ax in [2^E, 2^(E+1))       */
+  if (a == 0 || E < -6) E = -6;               /* subnormal quantum 2^-9     */
+  const int qexp = E - 3;                     /* 3 mantissa bits            */
+  const float n = rintf(ldexpf(ax, -qexp));   /* integer multiple of quantum */
+  if (n == 0.0f) return sign;
+  const float v = ldexpf(n, qexp);            /* exact, <= 448              */
+  if (v < 0.015625f)                          /* < 2^-6: subnormal          */
+    return sign | (uint8_t)ldexpf(v, 9);
+  int ve;
+  (void)frexpf(v, &ve);
+  const int Ev = ve - 1;                      /* may be E+1 after rounding  */
+  const int mant = (int)ldexpf(v, 3 - Ev) - 8;
+  return sign | (uint8_t)(((Ev + 7) << 3) | mant);
+}
+
+/* bf16 = upper half of an fp32 with round-to-nearest-even on the dropped
+ * half (what __hip_bfloat16(float), test.cpp:27, does on the host); NaN is
+ * kept NaN with the quiet bit set. */
+uint16_t hg_f32_to_bf16(float x) {
+  uint32_t u = f32_bits(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+float hg_bf16_to_f32(uint16_t v) { return bits_f32((uint32_t)v << 16); }
+
+void hg_f32_to_e4m3_n(const float *x, uint8_t *out, size_t n) {
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i) out[i] = hg_f32_to_e4m3(x[i]);
+}
+void hg_e4m3_to_f32_n(const uint8_t *x, float *out, size_t n) {
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i) out[i] = hg_e4m3_to_f32(x[i]);
+}
+void hg_f32_to_bf16_n(const float *x, uint16_t *out, size_t n) {
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i) out[i] = hg_f32_to_bf16(x[i]);
+}
+void hg_bf16_to_f32_n(const uint16_t *x, float *out, size_t n) {
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i) out[i] = hg_bf16_to_f32(x[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Seeded generators (the build's own; the reference only has utils.hpp's    */
+/* mt19937 normal(-1,1), restated separately in reftest_rng.cpp).            */
+/* Counter-based: element i = mix(mix(seed) + (i+1) * golden) with the       */
+/* SplitMix64 finaliser (Steele, Lea & Flood, OOPSLA 2014).                  */
+/* ------------------------------------------------------------------------ */
+static inline uint64_t splitmix_mix(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+uint64_t hg_rand64(uint64_t seed, uint64_t index) {
+  return splitmix_mix(splitmix_mix(seed) + (index + 1) * 0x9e3779b97f4a7c15ull);
+}
+
+static inline double u01_open(uint32_t r) { /* (0, 1) */
+  return ((double)r + 0.5) * (1.0 / 4294967296.0);
+}
+
+static inline float draw(uint64_t seed, uint64_t i, int dist, double p0,
+                         double p1) {
+  const uint64_t h = hg_rand64(seed, i);
+  if (dist == HG_DIST_UNIFORM) {
+    const double u = (double)(h >> 40) * (1.0 / 16777216.0); /* [0,1), 2^-24 */
+    return (float)(p0 + (p1 - p0) * u);
+  }
+  /* Box-Muller, cosine branch (Box & Muller 1958). */
+  const double u1 = u01_open((uint32_t)(h >> 32));
+  const double u2 = (double)(uint32_t)h * (1.0 / 4294967296.0);
+  const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+  double x = p0 + p1 * z;
+  if (x > 448.0) x = 448.0;
+  if (x < -448.0) x = -448.0;
+  return (float)x;
+}
+
+void hg_fill_e4m3(uint8_t *out, size_t n, uint64_t seed, int dist, double p0,
+                  double p1) {
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i)
+    out[i] = hg_f32_to_e4m3(draw(seed, (uint64_t)i, dist, p0, p1));
+}
+
+float hg_draw_scale(uint64_t seed, double lo, double hi) {
+  return draw(seed ^ 0x5ca1e5ca1e5ca1e5ull, 0, HG_DIST_UNIFORM, lo, hi);
+}
+
+/* ------------------------------------------------------------------------ */
+/* GEMM                                                                      */
+/* ------------------------------------------------------------------------ */
+static float g_e4m3_lut[256];
+static int g_lut_ready = 0;
+
+static void lut_init(void) {
+  if (g_lut_ready) return;
+#pragma omp critical(hg_lut)
+  {
+    if (!g_lut_ready) {
+      for (int i = 0; i < 256; ++i) g_e4m3_lut[i] = hg_e4m3_to_f32((uint8_t)i);
+      g_lut_ready = 1;
+    }
+  }
+}
+
+static inline uint16_t epilogue(float acc, float s) {
+  return hg_f32_to_bf16(acc * s);
+}
+
+/* test.cpp:19-30, plus the per-tensor scale extension.  Loop order, the
+ * OpenMP collapse(2) over (row, col) and the scalar fp32 K sum follow the
+ * reference; the e4m3 decode goes through a 256-entry table holding the same
+ * values the HIP header's operator float returns. */
+void hg_gemm_ref(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
+                 int N, int K, int lda, int ldb, int ldc, float scale_a,
+                 float scale_b) {
+  lut_init();
+  const float s = scale_a * scale_b;
+#pragma omp parallel for collapse(2)
+  for (int row = 0; row < M; ++row) {
+    for (int col = 0; col < N; ++col) {
+      float acc = 0.0f;
+      for (int k = 0; k < K; ++k)
+        acc += g_e4m3_lut[A[(size_t)row * lda + k]] *
+               g_e4m3_lut[B_T[(size_t)col * ldb + k]];
+      C[(size_t)row * ldc + col] = epilogue(acc, s);
+    }
+  }
+}
+
+/* B_T decoded and transposed to Bt[K][N] fp32. */
+static float *decode_bt(const uint8_t *B_T, int N, int K, int ldb) {
+  float *Bt = (float *)malloc((size_t)K * N * sizeof(float));
+  if (!Bt) return NULL;
+  lut_init();
+#pragma omp parallel for schedule(static)
+  for (int kb = 0; kb < K; kb += 64) {
+    const int ke = kb + 64 < K ? kb + 64 : K;
+    for (int n = 0; n < N; ++n)
+      for (int k = kb; k < ke; ++k)
+        Bt[(size_t)k * N + n] = g_e4m3_lut[B_T[(size_t)n * ldb + k]];
+  }
+  return Bt;
+}
+
+#define RB 8   /* rows per block    */
+#define CB 128 /* columns per block */
+
+/* acc[r][j] for rows rows[0..nr) and columns [n0, n0+nc): per output the K
+ * sum runs k = 0, 1, ..., K-1 in fp32, as in the reference. */
+static void block_acc(const uint8_t *A, const float *Bt, const int *rows,
+                      int nr, int n0, int nc, int N, int K, int lda,
+                      float acc[RB][CB]) {
+  const uint8_t *arow[RB];
+  for (int r = 0; r < RB; ++r) {
+    arow[r] = A + (size_t)rows[r < nr ? r : 0] * lda;
+    for (int j = 0; j < CB; ++j) acc[r][j] = 0.0f;
+  }
+  for (int k = 0; k < K; ++k) {
+    const float *b = Bt + (size_t)k * N + n0;
+    for (int r = 0; r < RB; ++r) {
+      const float a = g_e4m3_lut[arow[r][k]];
+      float *ac = acc[r];
+      if (nc == CB) {
+#pragma omp simd
+        for (int j = 0; j < CB; ++j) ac[j] += a * b[j];
+      } else {
+        for (int j = 0; j < nc; ++j) ac[j] += a * b[j];
+      }
+    }
+  }
+}
+
+static void rows_impl(const uint8_t *A, const float *Bt, const int *rows,
+                      int nrows, int N, int K, int lda, void *out, int ldo,
+                      int mode, float s) {
+  const int nrb = (nrows + RB - 1) / RB, ncb = (N + CB - 1) / CB;
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+  for (int rb = 0; rb < nrb; ++rb) {
+    for (int cb = 0; cb < ncb; ++cb) {
+      float acc[RB][CB] __attribute__((aligned(64)));
+      const int r0 = rb * RB, n0 = cb * CB;
+      const int nr = nrows - r0 < RB ? nrows - r0 : RB;
+      const int nc = N - n0 < CB ? N - n0 : CB;
+      block_acc(A, Bt, rows + r0, nr, n0, nc, N, K, lda, acc);
+      for (int r = 0; r < nr; ++r)
+        for (int j = 0; j < nc; ++j) {
+          const size_t o = (size_t)(r0 + r) * ldo + n0 + j;
+          if (mode == 0)
+            ((uint16_t *)out)[o] = epilogue(acc[r][j], s);
+          else
+            ((float *)out)[o] = acc[r][j];
+        }
+    }
+  }
+}
+
+void hg_gemm_fast(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
+                  int N, int K, int lda, int ldb, int ldc, float scale_a,
+                  float scale_b) {
+  float *Bt = decode_bt(B_T, N, K, ldb);
+  int *rows = (int *)malloc((size_t)(M > 0 ? M : 1) * sizeof(int));
+  if (!Bt || !rows) abort();
+  for (int i = 0; i < M; ++i) rows[i] = i;
+  rows_impl(A, Bt, rows, M, N, K, lda, C, ldc, 0, scale_a * scale_b);
+  free(rows);
+  free(Bt);
+}
+
+void hg_gemm_rows(const uint8_t *A, const uint8_t *B_T, uint16_t *C_rows,
+                  const int *rows, int nrows, int N, int K, int lda, int ldb,
+                  float scale_a, float scale_b) {
+  float *Bt = decode_bt(B_T, N, K, ldb);
+  if (!Bt) abort();
+  rows_impl(A, Bt, rows, nrows, N, K, lda, C_rows, N, 0, scale_a * scale_b);
+  free(Bt);
+}
+
+void hg_gemm_rows_acc(const uint8_t *A, const uint8_t *B_T, float *acc_rows,
+                      const int *rows, int nrows, int N, int K, int lda,
+                      int ldb) {
+  float *Bt = decode_bt(B_T, N, K, ldb);
+  if (!Bt) abort();
+  rows_impl(A, Bt, rows, nrows, N, K, lda, acc_rows, N, 1, 1.0f);
+  free(Bt);
+}
+
+void hg_gemm_rows_f64(const uint8_t *A, const uint8_t *B_T, double *acc_rows,
+                      const int *rows, int nrows, int N, int K, int lda,
+                      int ldb) {
+  lut_init();
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int r = 0; r < nrows; ++r)
+    for (int n = 0; n < N; ++n) {
+      const uint8_t *a = A + (size_t)rows[r] * lda;
+      const uint8_t *b = B_T + (size_t)n * ldb;
+      double acc = 0.0;
+      for (int k = 0; k < K; ++k)
+        acc += (double)g_e4m3_lut[a[k]] * (double)g_e4m3_lut[b[k]];
+      acc_rows[(size_t)r * N + n] = acc;
+    }
+}
+
+int hg_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}

@@ -1,0 +1,107 @@
+/*
+ * hipgemm oracle -- CPU restatement of the reference FP8 GEMM path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (the hipgemm_amd package,
+ * libhipgemm.so, include/) may include, link or call this code.  Only tests/,
+ * __graft_entry__.smoke() and the cpu_baseline leg of bench.py use it, and only
+ * as the checker.
+ *
+ * Reference being restated (nirw4nna/hipgemm):
+ *   test.cpp:19-30   gemm_cpu: per output, fp32 sequential-K sum of
+ *                    float(A[row*K+k]) * float(B[col*K+k]), then bf16(acc) (RNE)
+ *   utils.hpp:27-34  init_random: mt19937(seed), normal_distribution<float>(-1,1),
+ *                    cast to fp8 (e4m3, RNE, satfinite)
+ *   fp8_4wave.hpp:15-16  fp8 = __hip_fp8_e4m3 (OCP E4M3FN), bf16 = __hip_bfloat16
+ *
+ * Extension the reference does not have: per-tensor fp32 scales applied as
+ *   C = bf16_rne(acc * (scale_a * scale_b)), every step in fp32.
+ * With scale_a = scale_b = 1 this is bit-identical to gemm_cpu.
+ *
+ * Pinning (what checks each function; see tests/test_oracle.py):
+ *   hg_f32_to_e4m3 / hg_e4m3_to_f32 : exhaustive 2^32 sweep against the HIP
+ *       header conversion (__hip_fp8_e4m3 ctor / operator float), plus OCP
+ *       closed-form values.
+ *   hg_f32_to_bf16                  : exhaustive sweep against HIP's
+ *       __hip_bfloat16(float) (static_cast<__bf16>), plus closed forms.
+ *   hg_gemm_ref / hg_gemm_fast / hg_gemm_rows : bit-exact against the
+ *       reference's own gemm_cpu compiled from its sources (oracle/_ref),
+ *       brute-force fp64 on tiny shapes, one-hot / permutation / all-ones
+ *       closed forms.
+ *   hg_fill_e4m3 (REFTEST mode)     : bit-exact against the reference's
+ *       init_random compiled from its sources (oracle/_ref).
+ *   hg_fill_e4m3 (UNIFORM / NORMAL) : the build's own seeded generators (the
+ *       reference has no such generator); pinned by committed golden hashes
+ *       and distribution-moment checks.
+ */
+#ifndef HIPGEMM_ORACLE_H
+#define HIPGEMM_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- element codecs ---------------------------------------------------- */
+uint8_t hg_f32_to_e4m3(float x);      /* RNE, satfinite, Inf/NaN -> NaN    */
+float hg_e4m3_to_f32(uint8_t v);      /* exact                              */
+uint16_t hg_f32_to_bf16(float x);     /* RNE, NaN -> quiet NaN              */
+float hg_bf16_to_f32(uint16_t v);     /* exact                              */
+
+void hg_f32_to_e4m3_n(const float *x, uint8_t *out, size_t n);
+void hg_e4m3_to_f32_n(const uint8_t *x, float *out, size_t n);
+void hg_f32_to_bf16_n(const float *x, uint16_t *out, size_t n);
+void hg_bf16_to_f32_n(const uint16_t *x, float *out, size_t n);
+
+/* ---- seeded generators -------------------------------------------------- */
+enum {
+  HG_DIST_UNIFORM = 0, /* p0 + (p1 - p0) * u, u in [0,1)                     */
+  HG_DIST_NORMAL = 1,  /* mean p0, std p1 (Box-Muller), clipped to +-448      */
+};
+uint64_t hg_rand64(uint64_t seed, uint64_t index);
+/* Fill n e4m3 bytes; element i depends only on (seed, i) so the fill is
+ * order-independent and parallel. */
+void hg_fill_e4m3(uint8_t *out, size_t n, uint64_t seed, int dist, double p0,
+                  double p1);
+/* One fp32 scale drawn uniform in [lo, hi). */
+float hg_draw_scale(uint64_t seed, double lo, double hi);
+/* Reference-test mode: reproduces utils.hpp:27-34 (mt19937 + libstdc++
+ * normal_distribution<float>(-1, 1)), implemented in reftest_rng.cpp. */
+void hg_fill_e4m3_reftest(uint8_t *out, size_t n, uint64_t seed);
+
+/* ---- GEMM --------------------------------------------------------------- */
+/* C[M x N] (bf16 bits, ldc) = bf16(scale_a*scale_b * A[M x K] . B_T[N x K]^T)
+ * A row-major (lda), B_T row-major N x K (ldb).  Faithful restatement of
+ * test.cpp:19-30: OpenMP over outputs, scalar sequential-K fp32 sum. */
+void hg_gemm_ref(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
+                 int N, int K, int lda, int ldb, int ldc, float scale_a,
+                 float scale_b);
+/* Bit-identical to hg_gemm_ref (per-output sequential K order is kept; the
+ * e4m3 x e4m3 products are exact in fp32, so vectorising across outputs does
+ * not change any sum).  Blocked and SIMD across output columns. */
+void hg_gemm_fast(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
+                  int N, int K, int lda, int ldb, int ldc, float scale_a,
+                  float scale_b);
+/* Same as hg_gemm_fast for the listed rows only: output row r of C_rows
+ * (row-major, ld = N) is row rows[r] of the full product. */
+void hg_gemm_rows(const uint8_t *A, const uint8_t *B_T, uint16_t *C_rows,
+                  const int *rows, int nrows, int N, int K, int lda, int ldb,
+                  float scale_a, float scale_b);
+/* fp32 accumulators (before scale and rounding) for the listed rows. */
+void hg_gemm_rows_acc(const uint8_t *A, const uint8_t *B_T, float *acc_rows,
+                      const int *rows, int nrows, int N, int K, int lda,
+                      int ldb);
+/* Exact (fp64) accumulators for the listed rows; used to separate CPU and
+ * GPU rounding when reporting error statistics. */
+void hg_gemm_rows_f64(const uint8_t *A, const uint8_t *B_T, double *acc_rows,
+                      const int *rows, int nrows, int N, int K, int lda,
+                      int ldb);
+
+/* Threads OpenMP will use (for reporting cpu_baseline.cores). */
+int hg_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,261 @@
+"""ctypes bindings for the hipgemm CPU oracle.
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of bench.py, always as the checker.  The product
+package ``hipgemm_amd`` never imports this module.
+
+Libraries (built by ``oracle/Makefile``):
+  liboracle.so        C restatement of the reference path (oracle.c,
+                      reftest_rng.cpp); see oracle.h for what pins each part.
+  libpin_hipconv.so   HIP-header conversions, for the exhaustive codec pin.
+  _ref/libref_test.so the reference's own test.cpp (gemm_cpu, init_random,
+                      validate_matrix) built from its sources; optional.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+UNIFORM = 0
+NORMAL = 1
+
+_c_u8p = ctypes.POINTER(ctypes.c_uint8)
+_vp = ctypes.c_void_p
+
+
+def _ptr(a: np.ndarray) -> ctypes.c_void_p:
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+class Oracle:
+    """Thin wrapper over liboracle.so."""
+
+    def __init__(self, path: Optional[str] = None):
+        path = path or os.path.join(HERE, "liboracle.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(
+                f"{path} missing: build it with `make -C oracle` "
+                "(or __graft_entry__.build())")
+        self.lib = L = ctypes.CDLL(path)
+        L.hg_f32_to_e4m3.restype = ctypes.c_uint8
+        L.hg_f32_to_e4m3.argtypes = [ctypes.c_float]
+        L.hg_e4m3_to_f32.restype = ctypes.c_float
+        L.hg_e4m3_to_f32.argtypes = [ctypes.c_uint8]
+        L.hg_f32_to_bf16.restype = ctypes.c_uint16
+        L.hg_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.hg_bf16_to_f32.restype = ctypes.c_float
+        L.hg_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        for name in ("hg_f32_to_e4m3_n", "hg_e4m3_to_f32_n",
+                     "hg_f32_to_bf16_n", "hg_bf16_to_f32_n"):
+            getattr(L, name).argtypes = [_vp, _vp, ctypes.c_size_t]
+            getattr(L, name).restype = None
+        L.hg_rand64.restype = ctypes.c_uint64
+        L.hg_rand64.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+        L.hg_fill_e4m3.argtypes = [_vp, ctypes.c_size_t, ctypes.c_uint64,
+                                   ctypes.c_int, ctypes.c_double,
+                                   ctypes.c_double]
+        L.hg_fill_e4m3.restype = None
+        L.hg_fill_e4m3_reftest.argtypes = [_vp, ctypes.c_size_t,
+                                           ctypes.c_uint64]
+        L.hg_fill_e4m3_reftest.restype = None
+        L.hg_draw_scale.restype = ctypes.c_float
+        L.hg_draw_scale.argtypes = [ctypes.c_uint64, ctypes.c_double,
+                                    ctypes.c_double]
+        gemm_args = [_vp, _vp, _vp] + [ctypes.c_int] * 6 + [ctypes.c_float] * 2
+        for name in ("hg_gemm_ref", "hg_gemm_fast"):
+            getattr(L, name).argtypes = gemm_args
+            getattr(L, name).restype = None
+        L.hg_gemm_rows.argtypes = [_vp, _vp, _vp, _vp] + [ctypes.c_int] * 5 + \
+            [ctypes.c_float] * 2
+        L.hg_gemm_rows.restype = None
+        for name in ("hg_gemm_rows_acc", "hg_gemm_rows_f64"):
+            getattr(L, name).argtypes = [_vp, _vp, _vp, _vp] + [ctypes.c_int] * 5
+            getattr(L, name).restype = None
+        L.hg_num_threads.restype = ctypes.c_int
+
+    # -- codecs ------------------------------------------------------------
+    def f32_to_e4m3(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty(x.shape, np.uint8)
+        self.lib.hg_f32_to_e4m3_n(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def e4m3_to_f32(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.uint8)
+        out = np.empty(x.shape, np.float32)
+        self.lib.hg_e4m3_to_f32_n(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def f32_to_bf16(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty(x.shape, np.uint16)
+        self.lib.hg_f32_to_bf16_n(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def bf16_to_f32(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.uint16)
+        out = np.empty(x.shape, np.float32)
+        self.lib.hg_bf16_to_f32_n(_ptr(x), _ptr(out), x.size)
+        return out
+
+    # -- generators --------------------------------------------------------
+    def fill(self, shape: Sequence[int], seed: int, dist: int = UNIFORM,
+             p0: float = -1.0, p1: float = 1.0) -> np.ndarray:
+        out = np.empty(tuple(shape), np.uint8)
+        self.lib.hg_fill_e4m3(_ptr(out), out.size, seed, dist, p0, p1)
+        return out
+
+    def fill_reftest(self, shape: Sequence[int], seed: int) -> np.ndarray:
+        out = np.empty(tuple(shape), np.uint8)
+        self.lib.hg_fill_e4m3_reftest(_ptr(out), out.size, seed)
+        return out
+
+    def draw_scale(self, seed: int, lo: float = 0.5, hi: float = 2.0) -> float:
+        return float(self.lib.hg_draw_scale(seed, lo, hi))
+
+    # -- GEMM --------------------------------------------------------------
+    @staticmethod
+    def _check(A, B, M, N, K, lda, ldb):
+        assert A.dtype == np.uint8 and B.dtype == np.uint8
+        assert A.size >= (M - 1) * lda + K if M > 0 else True
+        assert B.size >= (N - 1) * ldb + K if N > 0 else True
+
+    def gemm(self, A: np.ndarray, B: np.ndarray, scale_a: float = 1.0,
+             scale_b: float = 1.0, faithful: bool = False) -> np.ndarray:
+        """bf16 bits of scale_a*scale_b * A @ B.T, A: M x K, B: N x K."""
+        A = np.ascontiguousarray(A)
+        B = np.ascontiguousarray(B)
+        M, K = A.shape
+        N = B.shape[0]
+        assert B.shape[1] == K
+        C = np.empty((M, N), np.uint16)
+        fn = self.lib.hg_gemm_ref if faithful else self.lib.hg_gemm_fast
+        fn(_ptr(A), _ptr(B), _ptr(C), M, N, K, K, K, N, scale_a, scale_b)
+        return C
+
+    def gemm_rows(self, A: np.ndarray, B: np.ndarray, rows: Sequence[int],
+                  scale_a: float = 1.0, scale_b: float = 1.0) -> np.ndarray:
+        A = np.ascontiguousarray(A)
+        B = np.ascontiguousarray(B)
+        K = A.shape[1]
+        N = B.shape[0]
+        r = np.ascontiguousarray(np.asarray(rows, dtype=np.int32))
+        assert r.size == 0 or (r.min() >= 0 and r.max() < A.shape[0])
+        C = np.empty((r.size, N), np.uint16)
+        self.lib.hg_gemm_rows(_ptr(A), _ptr(B), _ptr(C), _ptr(r), r.size, N, K,
+                              K, K, scale_a, scale_b)
+        return C
+
+    def gemm_rows_acc(self, A, B, rows) -> np.ndarray:
+        A = np.ascontiguousarray(A)
+        B = np.ascontiguousarray(B)
+        r = np.ascontiguousarray(np.asarray(rows, dtype=np.int32))
+        out = np.empty((r.size, B.shape[0]), np.float32)
+        self.lib.hg_gemm_rows_acc(_ptr(A), _ptr(B), _ptr(out), _ptr(r), r.size,
+                                  B.shape[0], A.shape[1], A.shape[1],
+                                  A.shape[1])
+        return out
+
+    def gemm_rows_f64(self, A, B, rows) -> np.ndarray:
+        A = np.ascontiguousarray(A)
+        B = np.ascontiguousarray(B)
+        r = np.ascontiguousarray(np.asarray(rows, dtype=np.int32))
+        out = np.empty((r.size, B.shape[0]), np.float64)
+        self.lib.hg_gemm_rows_f64(_ptr(A), _ptr(B), _ptr(out), _ptr(r), r.size,
+                                  B.shape[0], A.shape[1], A.shape[1],
+                                  A.shape[1])
+        return out
+
+    def num_threads(self) -> int:
+        return int(self.lib.hg_num_threads())
+
+
+class HipConvPin:
+    """HIP-header host conversions (libpin_hipconv.so)."""
+
+    def __init__(self, path: Optional[str] = None):
+        path = path or os.path.join(HERE, "libpin_hipconv.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        self.lib = L = ctypes.CDLL(path)
+        L.hg_pin_hip_f32_to_e4m3.restype = ctypes.c_uint8
+        L.hg_pin_hip_f32_to_e4m3.argtypes = [ctypes.c_float]
+        L.hg_pin_hip_e4m3_to_f32.restype = ctypes.c_float
+        L.hg_pin_hip_e4m3_to_f32.argtypes = [ctypes.c_uint8]
+        L.hg_pin_hip_f32_to_bf16.restype = ctypes.c_uint16
+        L.hg_pin_hip_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.hg_pin_sweep.restype = ctypes.c_uint64
+        L.hg_pin_sweep.argtypes = [ctypes.c_int, ctypes.c_uint64,
+                                   ctypes.c_uint64, _vp, ctypes.c_uint64,
+                                   ctypes.POINTER(ctypes.c_uint64)]
+
+    def sweep(self, what: int, lo: int = 0, hi: int = 1 << 32, cap: int = 64):
+        bad = np.zeros(cap, np.uint32)
+        tiny = ctypes.c_uint64(0)
+        n = self.lib.hg_pin_sweep(what, lo, hi, _ptr(bad), cap,
+                                  ctypes.byref(tiny))
+        return int(n), bad[: min(int(n), cap)], int(tiny.value)
+
+
+class RefLib:
+    """The reference's own host functions, compiled from its sources into
+    oracle/_ref/libref_test.so by ``make -C oracle ref``.  Absent on machines
+    where the reference sources were not available at build time."""
+
+    SYMS = {
+        "gemm_cpu": "_Z8gemm_cpuP14__hip_fp8_e4m3S0_P14__hip_bfloat16iii",
+        "init_random": "_Z11init_randomP14__hip_fp8_e4m3mm",
+        "validate_matrix": "_Z15validate_matrixP14__hip_bfloat16S0_ii",
+    }
+
+    def __init__(self, path: Optional[str] = None):
+        path = path or os.path.join(HERE, "_ref", "libref_test.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        self.lib = ctypes.CDLL(path)
+        self.gemm_cpu_fn = getattr(self.lib, self.SYMS["gemm_cpu"])
+        self.gemm_cpu_fn.argtypes = [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int]
+        self.gemm_cpu_fn.restype = None
+        self.init_random_fn = getattr(self.lib, self.SYMS["init_random"])
+        self.init_random_fn.argtypes = [_vp, ctypes.c_size_t, ctypes.c_size_t]
+        self.init_random_fn.restype = None
+        self.validate_fn = getattr(self.lib, self.SYMS["validate_matrix"])
+        self.validate_fn.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int]
+        self.validate_fn.restype = ctypes.c_bool
+
+    @staticmethod
+    def available(path: Optional[str] = None) -> bool:
+        return os.path.exists(path or os.path.join(HERE, "_ref",
+                                                   "libref_test.so"))
+
+    def gemm_cpu(self, A: np.ndarray, B: np.ndarray) -> np.ndarray:
+        """test.cpp:19-30 on contiguous A (M x K), B (N x K); bf16 bits."""
+        A = np.ascontiguousarray(A, dtype=np.uint8)
+        B = np.ascontiguousarray(B, dtype=np.uint8)
+        M, K = A.shape
+        N = B.shape[0]
+        C = np.empty((M, N), np.uint16)
+        self.gemm_cpu_fn(_ptr(A), _ptr(B), _ptr(C), M, N, K)
+        return C
+
+    def init_random(self, n: int, seed: int) -> np.ndarray:
+        out = np.empty(n, np.uint8)
+        self.init_random_fn(_ptr(out), n, seed)
+        return out
+
+
+_oracle: Optional[Oracle] = None
+
+
+def get() -> Oracle:
+    global _oracle
+    if _oracle is None:
+        _oracle = Oracle()
+    return _oracle

@@ -1,0 +1,109 @@
+"""The C ABI library: loads, exports every declared symbol, validates
+arguments before touching the GPU.  Runs without a GPU."""
+import ctypes
+import os
+import subprocess
+import sys
+
+import pytest
+
+import hipgemm_amd as hg
+
+INVALID = 1  # hipErrorInvalidValue
+FAKE = 1 << 20  # aligned fake device address; never dereferenced here
+
+
+def test_library_loads_and_exports_header_symbols():
+    L = hg.lib()
+    syms = hg.declared_symbols()
+    assert "hipgemm_fp8_gemm_bf16" in syms
+    assert "hipgemm_fp8_gemm_4wave_256x256x128" in syms
+    for s in syms:
+        assert hasattr(L, s), s
+    out = subprocess.run(["nm", "-D", "--defined-only", hg.lib_path()],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = [s for s in syms if s not in exported]
+    assert not missing, missing
+
+
+def test_version_and_variants():
+    assert hg.version() == 100
+    assert hg.variant_name(0) == "auto"
+    assert hg.variant_name(1).startswith("4wave")
+    assert hg.variant_name(99) is None
+    assert hg.select_variant(8192, 8192, 8192) in (1,)
+
+
+@pytest.mark.parametrize("args", [
+    dict(A=0),                         # null A
+    dict(B=0),                         # null B_T
+    dict(C=0),                         # null C
+    dict(M=-1), dict(N=-5), dict(K=-16),
+    dict(K=40, lda=48, ldb=48),        # K % 16 != 0
+    dict(lda=48),                      # lda < K
+    dict(ldb=48),                      # ldb < K
+    dict(lda=72),                      # lda % 16 != 0
+    dict(ldc=63),                      # ldc < N
+    dict(A=FAKE + 8),                  # A not 16-byte aligned
+    dict(B=FAKE + 4),                  # B_T not 16-byte aligned
+    dict(C=FAKE + 1),                  # C not 2-byte aligned
+    dict(lda=(1 << 23) + 16),          # lda too large for 32-bit offsets
+    dict(variant=7), dict(variant=-1),
+])
+def test_argument_validation(args):
+    p = dict(A=FAKE, B=FAKE, C=FAKE, M=64, N=64, K=64, lda=64, ldb=64, ldc=64,
+             variant=0)
+    p.update(args)
+    code = hg.gemm_raw(p["A"], p["B"], p["C"], p["M"], p["N"], p["K"],
+                       p["lda"], p["ldb"], p["ldc"], 0, 0, p["variant"], 0)
+    assert code == INVALID
+
+
+def test_empty_problem_is_a_noop():
+    assert hg.gemm_raw(0, 0, 0, 0, 64, 64, 64, 64, 64) == 0
+    assert hg.gemm_raw(0, 0, 0, 64, 0, 64, 64, 64, 64) == 0
+
+
+def test_k_zero_needs_only_c():
+    # K == 0 does not read A / B_T, so they may be NULL; C is still checked.
+    assert hg.gemm_raw(0, 0, 0, 64, 64, 0, 0, 0, 64) == INVALID
+    assert hg.gemm_raw(0, 0, FAKE + 1, 64, 64, 0, 0, 0, 64) == INVALID
+    assert hg.gemm_raw(0, 0, FAKE, 64, 64, 0, 0, 0, 63) == INVALID
+
+
+def test_dropin_entry_validates_too():
+    L = hg.lib()
+    assert L.hipgemm_fp8_gemm_4wave_256x256x128(None, None, None, 64, 64, 64,
+                                                None) == INVALID
+    assert L.hipgemm_fp8_gemm_4wave_256x256x128(FAKE, FAKE, FAKE, 64, 64, 40,
+                                                None) == INVALID
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    code = (
+        "import hipgemm_amd as h\n"
+        "h._LIB_PATH = '/nonexistent/libhipgemm.so'\n"
+        "try:\n"
+        "    h.lib()\n"
+        "except h.HipGemmError as e:\n"
+        "    print('raised', e)\n"
+        "else:\n"
+        "    raise SystemExit('no error')\n")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", code], cwd=root,
+                       capture_output=True, text=True)
+    assert r.returncode == 0 and "raised" in r.stdout, r.stderr
+
+
+def test_product_does_not_import_oracle():
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    pkg = os.path.join(root, "hipgemm_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".cpp", ".hpp", ".h")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in text.replace("oracle/", ""), f
+    for dirpath, _, files in os.walk(os.path.join(root, "include")):
+        for f in files:
+            assert "oracle" not in open(os.path.join(dirpath, f)).read(), f

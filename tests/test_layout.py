@@ -1,0 +1,94 @@
+"""LDS layout and workgroup->tile order, through the built library (no GPU).
+
+The kernel's LDS tile rows are 64 bytes (four 16-byte slots).  hipgemm_lds_slot
+exposes the slot of (row, K-chunk); these tests check the properties the
+kernel relies on rather than restating the formula:
+  * each row's chunk->slot map is a permutation (DMA lands every chunk once);
+  * MFMA operand fetches (ds_read_b128, 16 consecutive rows at one chunk per
+    16-lane group, fragment bases at multiples of 32 rows) hit 16 distinct
+    16-byte bank groups per 256 bytes, and each 8-lane half hits 8 distinct
+    groups per 128 bytes -- conflict-free under either LDS width;
+  * the tile order visits every tile exactly once for any grid size.
+"""
+import itertools
+
+import numpy as np
+import pytest
+
+import hipgemm_amd as hg
+
+
+def slot(r, c):
+    s = hg.lds_slot(r, c)
+    assert 0 <= s < 4
+    return s
+
+
+def test_slot_is_permutation_per_row():
+    for r in range(512):
+        assert sorted(slot(r, c) for c in range(4)) == [0, 1, 2, 3], r
+    assert hg.lds_slot(-1, 0) == -1 and hg.lds_slot(0, 4) == -1
+
+
+def test_slot_depends_on_row_mod_16_only():
+    for r in range(256):
+        for c in range(4):
+            assert slot(r, c) == slot(r % 16, c)
+
+
+@pytest.mark.parametrize("base", [0, 32, 64, 96, 128, 160, 192, 224])
+def test_operand_fetch_bank_conflict_free(base):
+    # lane l of an MFMA fragment fetch reads row base + l%32 at chunk
+    # 2*(l//32) + t, t in {0, 1}; hardware serves 16 (or 8) lanes at a time.
+    for t in (0, 1):
+        addrs = [(base + l % 32) * 64 + slot(base + l % 32, 2 * (l // 32) + t) * 16
+                 for l in range(64)]
+        for g0 in range(0, 64, 16):
+            grp = addrs[g0:g0 + 16]
+            assert len({(a % 256) // 16 for a in grp}) == 16, (base, t, g0)
+        for g0 in range(0, 64, 8):
+            grp = addrs[g0:g0 + 8]
+            assert len({(a % 128) // 16 for a in grp}) == 8, (base, t, g0)
+
+
+def test_dma_fill_covers_every_chunk_once():
+    # DMA lane l of the instruction for rows [R0, R0+16) fetches chunk
+    # (l%4) ^ xor(row) into slot l%4 of row R0 + l//4; i.e. slot s of row r
+    # holds chunk c with lds_slot(r, c) == s.  Every (row, chunk) lands once.
+    for R0 in (0, 16, 240):
+        seen = set()
+        for l in range(64):
+            r, s = R0 + l // 4, l % 4
+            c = [c for c in range(4) if slot(r, c) == s]
+            assert len(c) == 1
+            seen.add((r, c[0]))
+        assert len(seen) == 64
+
+
+GRIDS = [(1, 1, 1), (4, 2, 2), (305, 16, 20), (320, 16, 20), (256, 16, 20),
+         (1024, 32, 32), (3584, 32, 112), (7, 3, 5), (9, 3, 3), (64, 4, 4),
+         (13, 1, 40), (100, 40, 1), (255, 17, 15)]
+
+
+@pytest.mark.parametrize("grid,tm,tn", GRIDS)
+def test_tile_order_bijective(grid, tm, tn):
+    for gm in (0, 1, 3, 4, 8):
+        ms, ns = hg.tile_order(grid, tm, tn, gm)
+        assert len(ms) == tm * tn
+        pairs = set(zip(ms, ns))
+        assert pairs == set(itertools.product(range(tm), range(tn))), (grid, gm)
+
+
+def test_tile_order_xcd_blocks_are_compact():
+    # 8192^3: 32 x 32 tiles, one tile per workgroup.  Workgroup b runs on XCD
+    # b % 8; the 32 workgroups an XCD holds at once (one per CU) should form a
+    # compact block of tiles (few distinct A row-panels and B column-panels).
+    grid = 1024
+    ms, ns = hg.tile_order(grid, 32, 32)
+    first = {}
+    for b in range(grid):
+        first[b] = (ms[b], ns[b])
+    for x in range(8):
+        wave0 = [first[b] for b in range(x, grid, 8)][:32]
+        assert len({m for m, _ in wave0}) <= 4
+        assert len({n for _, n in wave0}) <= 8

@@ -1,0 +1,247 @@
+"""Pins for the CPU oracle (oracle/): the checker every parity test relies on.
+
+Each oracle function is checked against something independent of it:
+  * codecs: exhaustive 2^32 sweeps against the HIP header conversions the
+    reference calls (utils.hpp:32, test.cpp:25/27), plus OCP closed forms;
+  * reference-test generator: bit-exact against init_random (utils.hpp:27-34)
+    compiled from the reference sources (oracle/_ref);
+  * GEMM: bit-exact against gemm_cpu (test.cpp:19-30) compiled from the
+    reference sources, exact fp64 brute force where fp32 sums are exact,
+    permutation / all-ones / zero closed forms, and committed golden vectors;
+  * own generators: committed golden hashes and distribution moments.
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import pyoracle as po
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def bits_f32(u):
+    return np.array([u], dtype=np.uint32).view(np.float32)[0]
+
+
+# ---------------------------------------------------------------- codecs ---
+
+def test_e4m3_encode_exhaustive_vs_hip_header():
+    pin = po.HipConvPin()
+    n, bad, tiny = pin.sweep(0)
+    assert n == 0, [hex(b) for b in bad]
+    assert tiny > 0  # the |x| < 2^-69 range was compared to signed zero
+
+
+def test_bf16_encode_exhaustive_vs_hip_header():
+    pin = po.HipConvPin()
+    n, bad, _ = pin.sweep(1)
+    assert n == 0, [hex(b) for b in bad]
+
+
+def test_e4m3_decode_all_codes_vs_hip_header(oracle):
+    pin = po.HipConvPin()
+    for b in range(256):
+        x = oracle.lib.hg_e4m3_to_f32(b)
+        y = pin.lib.hg_pin_hip_e4m3_to_f32(b)
+        assert (np.isnan(x) and np.isnan(y)) or (x == y and
+                                                 np.signbit(x) == np.signbit(y)), b
+
+
+def test_e4m3_closed_forms(oracle):
+    dec, enc = oracle.lib.hg_e4m3_to_f32, oracle.lib.hg_f32_to_e4m3
+    assert dec(0x38) == 1.0 and dec(0xB8) == -1.0
+    assert dec(0x7E) == 448.0 and dec(0xFE) == -448.0
+    assert dec(0x01) == 2.0 ** -9 and dec(0x08) == 2.0 ** -6
+    assert dec(0x07) == 7 * 2.0 ** -9
+    assert np.isnan(dec(0x7F)) and np.isnan(dec(0xFF))
+    assert dec(0x80) == 0.0 and np.signbit(dec(0x80))
+    # every finite code round-trips
+    for b in range(256):
+        if b & 0x7F != 0x7F:
+            assert enc(dec(b)) == b, hex(b)
+    assert enc(449.0) == 0x7E and enc(1e30) == 0x7E and enc(-1e30) == 0xFE
+    assert enc(float("inf")) == 0x7F and enc(float("-inf")) == 0xFF
+    assert enc(float("nan")) & 0x7F == 0x7F
+    assert enc(2.0 ** -10) == 0x00            # tie -> even (zero)
+    assert enc(1.5 * 2.0 ** -10) == 0x01      # above the tie
+    assert enc(1.0625) == 0x38                # tie 1.0 / 1.125 -> even
+    assert enc(1.1875) == 0x3A                # tie 1.125 / 1.25 -> even
+    assert enc(-0.0) == 0x80
+
+
+def test_bf16_closed_forms(oracle):
+    f = oracle.lib.hg_f32_to_bf16
+    assert f(1.0) == 0x3F80 and f(-2.0) == 0xC000
+    assert f(1.0 + 2.0 ** -8) == 0x3F80          # tie -> even
+    assert f(1.0 + 3 * 2.0 ** -8) == 0x3F82      # tie -> even (up)
+    assert f(1.0 + 2.0 ** -8 + 2.0 ** -20) == 0x3F81
+    assert f(3.4e38) == 0x7F80                   # rounds up to +inf
+    assert f(float("inf")) == 0x7F80
+    nanb = f(float("nan"))
+    assert (nanb & 0x7F80) == 0x7F80 and (nanb & 0x7F) != 0
+
+
+# ------------------------------------------------------------ generators ---
+
+def test_reftest_generator_matches_reference_init_random(oracle):
+    if not po.RefLib.available():
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    ref = po.RefLib()
+    for seed in (0, 1, 2, 123):
+        n = 50_000 + seed
+        assert np.array_equal(ref.init_random(n, seed),
+                              oracle.fill_reftest((n,), seed)), seed
+
+
+def test_generator_golden_hashes(oracle):
+    with open(os.path.join(GOLDEN, "generators.json")) as f:
+        gold = json.load(f)
+    for case in gold["cases"]:
+        if case["dist"] == "reftest":
+            a = oracle.fill_reftest((case["n"],), case["seed"])
+        else:
+            d = po.UNIFORM if case["dist"] == "uniform" else po.NORMAL
+            a = oracle.fill((case["n"],), case["seed"], d, case["p0"], case["p1"])
+        assert hashlib.sha256(a.tobytes()).hexdigest() == case["sha256"], case
+    for case in gold["scales"]:
+        assert oracle.draw_scale(case["seed"]) == case["value"]
+
+
+def test_generator_moments(oracle):
+    n = 1 << 20
+    u = oracle.e4m3_to_f32(oracle.fill((n,), 11, po.UNIFORM, -1.0, 1.0))
+    assert abs(u.mean()) < 5e-3 and abs(u.var() - 1 / 3) < 5e-3
+    assert u.min() >= -1.0 and u.max() <= 1.0
+    z = oracle.e4m3_to_f32(oracle.fill((n,), 12, po.NORMAL, 0.0, 1.0))
+    assert abs(z.mean()) < 5e-3 and abs(z.std() - 1.0) < 1e-2
+    h = oracle.e4m3_to_f32(oracle.fill((n,), 13, po.NORMAL, 0.0, 0.5))
+    assert abs(h.std() - 0.5) < 5e-3
+    # different seeds, different streams; same seed, same stream
+    assert not np.array_equal(oracle.fill((4096,), 1), oracle.fill((4096,), 2))
+    assert np.array_equal(oracle.fill((4096,), 3), oracle.fill((4096,), 3))
+    s = [oracle.draw_scale(k) for k in range(64)]
+    assert min(s) >= 0.5 and max(s) < 2.0 and len(set(s)) > 60
+
+
+# ------------------------------------------------------------------ GEMM ---
+
+def _inputs(oracle, M, N, K, seed=1, dist=po.NORMAL, p0=0.0, p1=1.0):
+    return (oracle.fill((M, K), 2 * seed, dist, p0, p1),
+            oracle.fill((N, K), 2 * seed + 1, dist, p0, p1))
+
+
+@pytest.mark.parametrize("shape", [(64, 48, 96), (33, 17, 160), (1, 1, 16),
+                                   (128, 96, 512), (7, 130, 48)])
+def test_gemm_matches_reference_gemm_cpu(oracle, shape):
+    if not po.RefLib.available():
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    ref = po.RefLib()
+    M, N, K = shape
+    for dist, p0, p1 in ((po.NORMAL, 0.0, 1.0), (po.UNIFORM, -1.0, 1.0)):
+        A, B = _inputs(oracle, M, N, K, 3, dist, p0, p1)
+        want = ref.gemm_cpu(A, B)
+        assert np.array_equal(oracle.gemm(A, B, faithful=True), want)
+        assert np.array_equal(oracle.gemm(A, B), want)
+
+
+def test_gemm_reftest_inputs_match_reference(oracle):
+    """The reference's own test inputs (utils.hpp:27-34), A != B."""
+    if not po.RefLib.available():
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    ref = po.RefLib()
+    M = N = K = 256
+    A = ref.init_random(M * K, 0).reshape(M, K)
+    B = ref.init_random(N * K, 1).reshape(N, K)
+    assert np.array_equal(oracle.gemm(A, B), ref.gemm_cpu(A, B))
+
+
+def test_gemm_exact_bruteforce_fp64(oracle):
+    """U[-1,1] e4m3 values are multiples of 2^-9, so products are multiples of
+    2^-18; with |partial sums| < 2^6 every fp32 sum is exact and the oracle
+    must equal bf16(exact fp64 sum) bit for bit."""
+    M, N, K = 40, 56, 256
+    A, B = _inputs(oracle, M, N, K, 5, po.UNIFORM, -1.0, 1.0)
+    a = oracle.e4m3_to_f32(A).astype(np.float64)
+    b = oracle.e4m3_to_f32(B).astype(np.float64)
+    exact = a @ b.T
+    partial = np.abs(np.cumsum(a[:, None, :] * b[None, :, :], axis=2)).max()
+    assert partial < 64.0
+    want = oracle.f32_to_bf16(exact.astype(np.float32))
+    assert np.array_equal(oracle.gemm(A, B), want)
+    # and the transposed product is a different matrix (orientation is pinned)
+    assert not np.array_equal(oracle.gemm(B, A), want[:N, :M])
+
+
+def test_gemm_closed_forms(oracle):
+    rng = np.random.default_rng(0)
+    K = 64
+    B = oracle.fill((48, K), 9, po.NORMAL, 0.0, 1.0)
+    # permutation A: C row i = B row-sums picked by one-hot positions
+    perm = rng.permutation(K)[:32]
+    A = np.zeros((32, K), np.uint8)
+    A[np.arange(32), perm] = 0x38  # 1.0
+    bf = oracle.e4m3_to_f32(B)
+    want = oracle.f32_to_bf16(bf[:, perm].T.copy())
+    assert np.array_equal(oracle.gemm(A, B), want)
+    # all-ones A: every row equals the row sums of B (exact: small integers*2^-9)
+    Bu = oracle.fill((48, K), 10, po.UNIFORM, -1.0, 1.0)
+    ones = np.full((5, K), 0x38, np.uint8)
+    sums = oracle.e4m3_to_f32(Bu).astype(np.float64).sum(axis=1)
+    want = np.tile(oracle.f32_to_bf16(sums.astype(np.float32)), (5, 1))
+    assert np.array_equal(oracle.gemm(ones, Bu), want)
+    # zero A
+    assert np.all(oracle.gemm(np.zeros((3, K), np.uint8), B) == 0)
+
+
+def test_gemm_scale_extension(oracle):
+    """C = bf16(acc * (sa*sb)) with the fp32 accumulator of the same order."""
+    M, N, K = 24, 40, 320
+    A, B = _inputs(oracle, M, N, K, 7)
+    sa, sb = np.float32(1.7), np.float32(0.6)
+    rows = np.arange(M)
+    acc = oracle.gemm_rows_acc(A, B, rows)
+    want = oracle.f32_to_bf16((acc * np.float32(sa * sb)).astype(np.float32))
+    assert np.array_equal(oracle.gemm(A, B, float(sa), float(sb)), want)
+    assert np.array_equal(oracle.gemm(A, B, float(sa), float(sb), faithful=True),
+                          want)
+    assert np.array_equal(oracle.gemm(A, B, 1.0, 1.0), oracle.f32_to_bf16(acc))
+
+
+def test_gemm_rows_subset(oracle):
+    M, N, K = 50, 70, 192
+    A, B = _inputs(oracle, M, N, K, 8)
+    full = oracle.gemm(A, B, 1.3, 0.9)
+    rows = [0, 7, 49, 7, 13]
+    assert np.array_equal(oracle.gemm_rows(A, B, rows, 1.3, 0.9), full[rows])
+    ex = oracle.gemm_rows_f64(A, B, rows)
+    acc = oracle.gemm_rows_acc(A, B, rows)
+    assert np.allclose(ex, acc, rtol=1e-5, atol=1e-4)
+
+
+def test_gemm_nan_and_saturation(oracle):
+    K = 64
+    A = np.full((4, K), 0x7E, np.uint8)   # 448
+    B = np.full((3, K), 0x7E, np.uint8)
+    want = oracle.lib.hg_f32_to_bf16(448.0 * 448.0 * K)
+    assert np.all(oracle.gemm(A, B) == want)
+    A[2, 5] = 0x7F  # NaN
+    C = oracle.gemm(A, B)
+    assert np.all(np.isnan(oracle.bf16_to_f32(C[2])))
+    assert not np.any(np.isnan(oracle.bf16_to_f32(C[[0, 1, 3]])))
+
+
+def test_golden_vectors(oracle):
+    """Committed vectors made by tests/golden/make_golden.py (oracle output,
+    cross-checked at generation time against the reference's gemm_cpu)."""
+    path = os.path.join(GOLDEN, "gemm_small.npz")
+    z = np.load(path)
+    names = sorted({k.rsplit("_", 1)[0] for k in z.files})
+    assert names
+    for nm in names:
+        A, B, C = z[nm + "_A"], z[nm + "_B"], z[nm + "_C"]
+        sa, sb = (float(x) for x in z[nm + "_S"])
+        assert np.array_equal(oracle.gemm(A, B, sa, sb), C), nm
+        assert np.array_equal(oracle.gemm(A, B, sa, sb, faithful=True), C), nm
