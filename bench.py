@@ -55,6 +55,11 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="before the GEMMs, run one elementwise copy kernel "
+                         "over this many MiB (reads N, writes N bytes) as the "
+                         "known-size reference for rocprof FETCH_SIZE / "
+                         "WRITE_SIZE")
     return ap.parse_args()
 
 
@@ -160,6 +165,15 @@ def main():
     def launch(i):
         hg.fp8_gemm_bf16(As[i % nsets], Bs[i % nsets], sa, sb, out,
                          variant=variant, stream=stream)
+
+    if args.calibrate_copy_mib > 0:
+        n = (args.calibrate_copy_mib << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.neg(src, out=dst)  # one kernel: n*4 bytes in, n*4 bytes out
+        torch.cuda.synchronize()
+        del src, dst
 
     for i in range(args.warmup):
         launch(i)

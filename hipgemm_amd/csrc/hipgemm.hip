@@ -109,7 +109,7 @@ const char* hipgemm_variant_name(int variant) {
     case HIPGEMM_VARIANT_AUTO:
       return "auto";
     case HIPGEMM_VARIANT_4WAVE:
-      return "4wave_256x256x64_s4";
+      return "4wave_256x256x128_q4";
     default:
       return nullptr;
   }
@@ -137,7 +137,7 @@ int hipgemm_tile_order(int grid, int tiles_m, int tiles_n, int group_m,
 }
 
 int hipgemm_lds_slot(int row, int chunk) {
-  if (row < 0 || chunk < 0 || chunk > 3) return -1;
+  if (row < 0 || chunk < 0 || chunk > 7) return -1;
   return chunk ^ slot_xor(row);
 }
 

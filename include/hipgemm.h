@@ -98,8 +98,8 @@ int hipgemm_tile_order(int grid, int tiles_m, int tiles_n, int group_m,
                        int *tile_m, int *tile_n, int cap);
 
 /*
- * Host-side view of the LDS tile layout: the 16-byte slot (0..3) at which
- * K-chunk `chunk` (0..3) of tile row `row` sits inside its 64-byte LDS row.
+ * Host-side view of the LDS tile layout: the 16-byte slot (0..7) at which
+ * K-chunk `chunk` (0..7) of tile row `row` sits inside its 128-byte LDS row.
  * For tests of the bank-conflict-freedom of the layout; no GPU needed.
  * Returns -1 for out-of-range arguments.  Replaces the swizzle helpers at
  * fp8_4wave.hpp:136-177 (not callable there).

@@ -99,25 +99,46 @@ __device__ __forceinline__ int wave_id() {
 __device__ __forceinline__ int lane_id() { return threadIdx.x % kWave; }
 
 // Explicit counters.  The compiler does not order LDS reads after LDS-DMA
-// writes, so every stage hand-off below is an explicit vmcnt wait + barrier.
-// The "memory" clobbers keep the compiler from moving loads or stores across.
+// writes, so every stage hand-off is an explicit vmcnt wait + barrier.  The
+// waits go through __builtin_amdgcn_s_waitcnt (not inline asm) so the
+// compiler's own waitcnt insertion sees them and adds no redundant waits;
+// sched_barrier(0) keeps the scheduler from moving any instruction (MFMA
+// included) across a wait or barrier, and the empty asm with a "memory"
+// clobber keeps IR passes from moving loads and stores across.
+// gfx9 s_waitcnt immediate: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] |
+// vmcnt[5:4] at [15:14]; a field at its maximum means "do not wait".
+constexpr int waitcnt_imm(int vmcnt, int lgkmcnt) {
+  return (vmcnt & 15) | ((vmcnt >> 4) << 14) | (7 << 4) | (lgkmcnt << 8);
+}
+__device__ __forceinline__ void sched_fence() {
+  __builtin_amdgcn_sched_barrier(0);
+}
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+  compiler_fence();
+  sched_fence();
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(N, 15));
+  sched_fence();
+  compiler_fence();
 }
 template <int N>
 __device__ __forceinline__ void wait_lgkmcnt() {
   static_assert(N >= 0 && N < 16, "lgkmcnt range");
-  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+  compiler_fence();
+  sched_fence();
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, N));
+  sched_fence();
+  compiler_fence();
 }
 __device__ __forceinline__ void barrier() {
-  asm volatile("" ::: "memory");
+  compiler_fence();
+  sched_fence();
   __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-__device__ __forceinline__ void sched_fence() {
-  __builtin_amdgcn_sched_barrier(0);
+  sched_fence();
+  compiler_fence();
 }
 
 }  // namespace detail

@@ -10,23 +10,35 @@
 //     tiles, so any grid size >= 1 is correct.
 //   * Wave w owns the contiguous 128 x 128 quadrant (w / 2, w % 2) of the tile
 //     as 4 x 4 blocks of 32 x 32 fp32 accumulators (256 AGPRs per lane).
-//   * K advances 64 bytes per step: one v_mfma_f32_32x32x64_f8f6f4 per block,
-//     16 per wave per step.
+//   * K advances 128 bytes per step (one LDS stage); each of the 16 blocks
+//     takes two v_mfma_f32_32x32x64_f8f6f4 per step (K-halves).
 //
-// Pipeline (STAGES = 4 LDS buffers of 256 x 64 B for A and for B, 128 KiB)
-//   step kt, LDS stage s = kt % 4, register set p = kt % 2:
-//     wait own DMA of step kt+1 (vmcnt), wait own LDS reads of step kt
-//     (lgkmcnt), s_barrier                      -- the only barrier per step
-//     DMA step kt+4 into stage s                -- 3 steps of latency slack
-//     16 MFMA on register set p, interleaved with the 16 ds_read_b128 that
-//     fill set p^1 with step kt+1 from stage (kt+1) % 4.
-//   Steps past the end of K read zeros (every lane out of range), so the K
-//   loop runs a multiple of 4 steps with no branches inside the unrolled body.
+// Operand registers: four tiles of 64 rows x 128 K-bytes (32 VGPRs each):
+// a_lo / a_hi = the wave's A rows 0-63 / 64-127, b_lo / b_hi likewise for B.
+// A step runs four quarter-steps Q00, Q01, Q10, Q11; quarter Qij takes the
+// 2 x 2 blocks (a_i, b_j), 8 MFMA.  A tile is reloaded for the next step as
+// soon as its second use is over:
+//   Q00(k): MFMA a_lo x b_lo | read b_hi(k)   | DMA B_lo group, step k+2
+//   Q01(k): MFMA a_lo x b_hi | read a_hi(k)   | DMA B_hi group, step k+2
+//   Q10(k): MFMA a_hi x b_lo | read a_lo(k+1) | DMA A_hi group, step k+2
+//   Q11(k): MFMA a_hi x b_hi | read b_lo(k+1) | DMA A_lo group, step k+3
+// LDS holds 2 stages (A 256 x 128 B + B 256 x 128 B each, 128 KiB).  Each
+// 64-row sub-buffer group (e.g. "A_lo" = A rows 0-63 and 128-191, the a_lo
+// rows of both wave rows) is read in one quarter-step and refilled in the
+// next; the refill is read seven quarter-steps later (~1.75 steps, ~3.5K
+// cycles of DMA latency slack).  Every quarter-step starts with: wait own
+// LDS reads (the group read last quarter is free), wait own DMA up to the
+// group read this quarter (vmcnt 24), s_barrier.  Inside a quarter the 8 LDS
+// reads go two per MFMA in the first half and the 4 DMA one per MFMA in the
+// second half, so the per-CU address unit is never offered more than about
+// one 1 KiB DMA per 16 cycles.  DMA issued for steps past the end of K reads
+// zeros (every lane out of range); the step count is padded to even.
 //
-// Global -> LDS: buffer_load_dwordx4 ... lds, 16 rows x 64 B per instruction,
-// 8 instructions per wave per step.  The buffer resource of a tile covers only
-// its valid rows, so rows past M (or N) read zero; K-chunks past K are given
-// an out-of-range offset.  Nothing outside A or B is ever addressed.
+// Global -> LDS: buffer_load_dwordx4 ... lds, 8 rows x 128 B per instruction
+// (whole 128-byte lines), 16 instructions per wave per step.  The buffer
+// resource of a tile covers only its valid rows, so rows past M (or N) read
+// zero; K-chunks past K get an out-of-range offset.  Nothing outside A or B is
+// ever addressed.
 //
 // Epilogue: acc * (scale_a * scale_b) -> bf16 (RNE), one 8-byte store of 4
 // consecutive columns per lane per (block, 8-row group); per-lane masks keep
@@ -60,20 +72,34 @@ __host__ __device__ constexpr int default_group_m(int tiles_m, int tiles_n) {
 
 struct Cfg4w {
   static constexpr int kThreads = 256;
-  static constexpr int kBM = 256, kBN = 256, kBK = 64, kStages = 4;
-  static constexpr int kAStage = kBM * kBK;  // 16 KiB
-  static constexpr int kBStage = kBN * kBK;  // 16 KiB
+  static constexpr int kBM = 256, kBN = 256, kBK = 128, kStages = 2;
+  static constexpr int kAStage = kBM * kBK;  // 32 KiB
+  static constexpr int kBStage = kBN * kBK;  // 32 KiB
   static constexpr int kABase = 0;
   static constexpr int kBBase = kStages * kAStage;
   static constexpr int kLdsBytes = kStages * (kAStage + kBStage);  // 128 KiB
-  static constexpr int kDmaPerStep = 8;  // per wave: 4 for A, 4 for B
+  static constexpr int kDmaPerStep = 16;  // per wave: 8 for A, 8 for B
 };
+
+// sched_group_barrier pattern of one quarter-step: 8 MFMA (0x008); two LDS
+// reads (0x100) after each of the first 4, one DMA (0x020) after each of the
+// last 4.
+__device__ __forceinline__ void quarter_schedule() {
+  for (int x = 0; x < 4; ++x) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+  }
+  for (int x = 0; x < 4; ++x) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+  }
+}
 
 template <bool kVecStore>
 __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                                                 lds_u8* lds) {
   using Cfg = Cfg4w;
-  constexpr int S = Cfg::kStages;
+  constexpr int kDmaPerGroup = 4;  // per wave
   const int lane = lane_id();
   const int wave = wave_id();
   const int wm = wave >> 1, wn = wave & 1;
@@ -83,32 +109,37 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   const int tiles_n = (N + Cfg::kBN - 1) / Cfg::kBN;
   const int tiles = tiles_m * tiles_n;
   const int kt_real = (K + Cfg::kBK - 1) / Cfg::kBK;
-  const int kt_pad = (kt_real + S - 1) / S * S;
+  const int kt_pad = (kt_real + 1) & ~1;
 
   const float sa = g.scale_a ? *g.scale_a : 1.0f;
   const float sb = g.scale_b ? *g.scale_b : 1.0f;
   const float scale = sa * sb;
 
-  // ---- DMA lane geometry: 16 rows x 4 slots per instruction -------------
-  const int drow = lane >> 2;
-  const int dchunk = (lane & 3) ^ slot_xor(drow);
-  uint32_t voff_a[4], voff_b[4];
+  // ---- DMA lane geometry: instruction q of wave w covers rows
+  // (4q + w) * 8 .. +8; lane l takes row +l/8, slot l%8.  q in {0,1,4,5}
+  // lands in rows 0-63 and 128-191 ("lo" group), q in {2,3,6,7} in rows
+  // 64-127 and 192-255 ("hi" group). ------------------------------------------
+  const int drow = lane >> 3;
+  const int dchunk = (lane & 7) ^ slot_xor(8 * (wave & 1) + drow);
+  uint32_t voff_a[8], voff_b[8];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int row = (4 * q + wave) * 16 + drow;
+  for (int q = 0; q < 8; ++q) {
+    const int row = (4 * q + wave) * 8 + drow;
     voff_a[q] = (uint32_t)row * (uint32_t)g.lda + dchunk * 16;
     voff_b[q] = (uint32_t)row * (uint32_t)g.ldb + dchunk * 16;
   }
 
-  // ---- ds_read lane geometry: fragment row lane%32, K-half lane/32 -------
+  // ---- ds_read lane geometry: fragment row lane%32; K-half kh, lane group
+  // g = lane/32 and sub-chunk t read K-chunk 4kh + 2g + t. -------------------
   const int rrow = lane & 31;
   const int rslot = (2 * (lane >> 5)) ^ slot_xor(rrow & 15);
   const uint32_t off_a = Cfg::kABase + (wm * 128 + rrow) * Cfg::kBK + rslot * 16;
   const uint32_t off_b = Cfg::kBBase + (wn * 128 + rrow) * Cfg::kBK + rslot * 16;
-  const lds_u8* pa0 = lds + off_a;
-  const lds_u8* pa1 = lds + (off_a ^ 16u);
-  const lds_u8* pb0 = lds + off_b;
-  const lds_u8* pb1 = lds + (off_b ^ 16u);
+  // chunk bits (kh, g, t) sit at address bits (6, 5, 4): flip them with XOR.
+  const lds_u8* pa[2][2] = {{lds + off_a, lds + (off_a ^ 16u)},
+                            {lds + (off_a ^ 64u), lds + (off_a ^ 80u)}};
+  const lds_u8* pb[2][2] = {{lds + off_b, lds + (off_b ^ 16u)},
+                            {lds + (off_b ^ 64u), lds + (off_b ^ 80u)}};
 
   const int grid = gridDim.x;
   for (int t = xcd_contiguous(blockIdx.x, grid); t < tiles; t += grid) {
@@ -122,36 +153,43 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
         make_rsrc(g.B + (size_t)tc.n * Cfg::kBN * g.ldb,
                   (uint32_t)rows_b * (uint32_t)g.ldb);
 
-    auto issue_dma = [&](int kb, int stage) {
+    // DMA of one sub-buffer group of step kb into `stage`: operand op (0 = A,
+    // 1 = B), half hi (0 = lo group, 1 = hi group).  4 instructions per wave.
+    auto dma_group = [&](int kb, int stage, int op, int hi) {
       uint32_t k0 = (uint32_t)kb * Cfg::kBK;
       // Opaque to the optimiser: keeps the per-step lane masks from being
-      // hoisted out of the tile loop (they would pin 32 VGPRs and spill).
+      // hoisted out of the tile loop (they would pin VGPRs and spill).
       asm volatile("" : "+s"(k0));
       const bool ok = (int)(k0 + dchunk * 16) < K;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        dma16(rsrc_a,
-              lds + Cfg::kABase + stage * Cfg::kAStage + (4 * q + wave) * 1024,
-              ok ? voff_a[q] : kOobOffset, k0);
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        dma16(rsrc_b,
-              lds + Cfg::kBBase + stage * Cfg::kBStage + (4 * q + wave) * 1024,
-              ok ? voff_b[q] : kOobOffset, k0);
+      for (int qq = 0; qq < kDmaPerGroup; ++qq) {
+        const int q = (qq & 1) + 4 * (qq >> 1) + 2 * hi;
+        if (op == 0)
+          dma16(rsrc_a,
+                lds + Cfg::kABase + stage * Cfg::kAStage + (4 * q + wave) * 1024,
+                ok ? voff_a[q] : kOobOffset, k0);
+        else
+          dma16(rsrc_b,
+                lds + Cfg::kBBase + stage * Cfg::kBStage + (4 * q + wave) * 1024,
+                ok ? voff_b[q] : kOobOffset, k0);
+      }
     };
 
-    i32x8 fa[2][4], fb[2][4];
-    auto read_operands = [&](int set, int stage) {
+    i32x8 fa[4][2], fb[4][2];  // [32-row fragment][K-half]
+    // Register tile (op, hi) of `stage`: fragments 2hi, 2hi+1, both K-halves.
+    auto read_tile = [&](int op, int hi, int stage) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int o = stage * Cfg::kAStage + i * 32 * Cfg::kBK;
-        fa[set][i] = join(lds_read16(pa0 + o), lds_read16(pa1 + o));
-      }
+      for (int f = 2 * hi; f < 2 * hi + 2; ++f)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int o = stage * Cfg::kBStage + j * 32 * Cfg::kBK;
-        fb[set][j] = join(lds_read16(pb0 + o), lds_read16(pb1 + o));
-      }
+        for (int kh = 0; kh < 2; ++kh) {
+          if (op == 0) {
+            const int o = stage * Cfg::kAStage + f * 32 * Cfg::kBK;
+            fa[f][kh] = join(lds_read16(pa[kh][0] + o), lds_read16(pa[kh][1] + o));
+          } else {
+            const int o = stage * Cfg::kBStage + f * 32 * Cfg::kBK;
+            fb[f][kh] = join(lds_read16(pb[kh][0] + o), lds_read16(pb[kh][1] + o));
+          }
+        }
     };
 
     f32x16 acc[4][4];
@@ -160,40 +198,70 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
+    // Quarter (qi, qj): blocks i in {2qi, 2qi+1} x j in {2qj, 2qj+1}, K-half
+    // major so the two MFMA of one accumulator are 4 apart.
+    auto quarter_mfma = [&](int qi, int qj) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int i = 2 * qi; i < 2 * qi + 2; ++i)
+#pragma unroll
+          for (int j = 2 * qj; j < 2 * qj + 2; ++j)
+            acc[i][j] = mfma_32x32x64(fb[j][kh], fa[i][kh], acc[i][j]);
+    };
+
+    auto quarter_sync = [&]() {
+      wait_lgkmcnt<0>();
+      wait_vmcnt<6 * kDmaPerGroup>();
+      barrier();
+    };
+
     // Previous tile: all LDS reads done and all stores retired before the
     // stages are overwritten.
     wait_vmcnt<0>();
     barrier();
 
-    // Prologue: steps 0..S-1 in flight, step 0 in registers.
+    // Prologue: steps 0 and 1 in group order A_lo, B_lo, B_hi, A_hi; then
+    // a_lo(0), b_lo(0) into registers and the A_lo group of step 2.
 #pragma unroll
-    for (int p = 0; p < S; ++p) issue_dma(p, p);
-    wait_vmcnt<(S - 1) * Cfg::kDmaPerStep>();
+    for (int st = 0; st < 2; ++st) {
+      dma_group(st, st, 0, 0);
+      dma_group(st, st, 1, 0);
+      dma_group(st, st, 1, 1);
+      dma_group(st, st, 0, 1);
+    }
+    wait_vmcnt<6 * kDmaPerGroup>();
     barrier();
-    read_operands(0, 0);
+    read_tile(0, 0, 0);
+    read_tile(1, 0, 0);
+    wait_lgkmcnt<0>();
+    barrier();
+    dma_group(2, 0, 0, 0);
 
-    for (int kt0 = 0; kt0 < kt_pad; kt0 += S) {
+    for (int kt0 = 0; kt0 < kt_pad; kt0 += 2) {
 #pragma unroll
-      for (int s = 0; s < S; ++s) {
-        const int p = s & 1;
-        wait_vmcnt<(S - 2) * Cfg::kDmaPerStep>();
-        wait_lgkmcnt<0>();
-        barrier();
-        issue_dma(kt0 + s + S, s);
-        read_operands(p ^ 1, (s + 1) % S);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[i][j] = mfma_32x32x64(fb[p][j], fa[p][i], acc[i][j]);
-        // Issue order: DMA first, then one LDS read per MFMA.
-#pragma unroll
-        for (int x = 0; x < 8; ++x) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-#pragma unroll
-        for (int x = 0; x < 16; ++x) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        }
+      for (int s = 0; s < 2; ++s) {
+        const int kt = kt0 + s;
+        quarter_sync();  // Q00
+        quarter_mfma(0, 0);
+        read_tile(1, 1, s);
+        dma_group(kt + 2, s, 1, 0);
+        quarter_schedule();
+        quarter_sync();  // Q01
+        quarter_mfma(0, 1);
+        read_tile(0, 1, s);
+        dma_group(kt + 2, s, 1, 1);
+        quarter_schedule();
+        quarter_sync();  // Q10
+        quarter_mfma(1, 0);
+        read_tile(0, 0, s ^ 1);
+        dma_group(kt + 2, s, 0, 1);
+        quarter_schedule();
+        quarter_sync();  // Q11
+        quarter_mfma(1, 1);
+        read_tile(1, 0, s ^ 1);
+        dma_group(kt + 3, s ^ 1, 0, 0);
+        quarter_schedule();
       }
     }
     wait_vmcnt<0>();

@@ -1,23 +1,23 @@
 // hipgemm -- data layout rules shared by host and device code.
 //
-// 1. LDS tile layout ("64-byte rows, XOR-swizzled 16-byte slots").
-//    A K-stage of an operand tile holds R rows x 64 K-bytes.  Row r occupies
-//    LDS bytes [64 r, 64 r + 64) as four 16-byte slots; slot s of row r holds
+// 1. LDS tile layout ("128-byte rows, XOR-swizzled 16-byte slots").
+//    A K-stage of an operand tile holds R rows x 128 K-bytes, row r at LDS
+//    bytes [128 r, 128 r + 128) as eight 16-byte slots; slot s of row r holds
 //    global K-chunk (s ^ slot_xor(r)) of that row.  The DMA writes each
-//    instruction's 64 lanes x 16 B linearly, so the permutation is applied on
-//    the global side: DMA lane l fetches chunk (l%4) ^ slot_xor(row).
+//    instruction's 64 lanes x 16 B linearly (8 rows x 128 B, every global
+//    request a whole 128-byte line), so the permutation is applied on the
+//    global side: DMA lane l fetches chunk (l%8) ^ slot_xor(row).
 //
-//    slot_xor depends on r mod 16 only and is chosen so that ds_read_b128 by
-//    an MFMA operand fetch (16 consecutive rows at one K-chunk per 16-lane
-//    group) touches 16 distinct 16-byte bank groups out of 256 bytes, and
-//    every 8-lane half of it 8 distinct groups out of 128 bytes: bank-conflict
-//    free whether the LDS serves 256 or 128 bytes per cycle.  Proof sketch for
-//    r = (r3 r2 r1 r0): slot_xor = ((r3 ^ r1) << 1) | r2.
-//      - 16 rows, one residue r mod 4 = (r1 r0): (r3, r2) -> slot_xor is a
-//        bijection, and the row's bank offset is 64 * (r mod 4).
-//      - 8 rows (r3 fixed), one parity r0: (r2, r1) -> slot_xor is a
-//        bijection, and the row's offset mod 128 is 64 * r0.
-//    tests/test_layout.py checks both properties exhaustively.
+//    slot_xor(r) = (r & 7) ^ ((r >> 3) & 1) depends on r mod 16 only and makes
+//    an MFMA operand fetch -- ds_read_b128 of 16 consecutive rows at one
+//    K-chunk per 16-lane group -- conflict-free whether the LDS serves 256 or
+//    128 bytes per cycle:
+//      - 256 B (16 lanes): a row's bank offset is 128 * (r & 1); for each
+//        parity the 8 rows of a 16-row block get 8 distinct slots;
+//      - 128 B (8 lanes): the 8 rows of an aligned 8-row block get 8
+//        distinct slots.
+//    tests/test_layout.py checks both properties exhaustively through the
+//    built library.
 //
 // 2. Output tile order ("XCD-contiguous, grouped columns").
 //    The dispatcher hands workgroup b to XCD b % 8.  tile_of_block() first
@@ -27,8 +27,8 @@
 //    the workgroups resident on one XCD share A rows and B columns in its L2.
 //    Bijective on [0, tiles) for every grid, tiles_m, tiles_n, group_m >= 1.
 //
-// Reference counterparts: fp8_4wave.hpp:136-177 (a different swizzle over
-// 128-byte rows) and :357-377 (a remap that is a bijection only when the
+// Reference counterparts: fp8_4wave.hpp:136-177 (a different swizzle, row
+// pairs XORed with (r >> 1) & 7) and :357-377 (a remap that is a bijection only when the
 // grid is a multiple of 8).
 #pragma once
 
@@ -39,9 +39,7 @@ namespace detail {
 
 constexpr int kNumXcds = 8;
 
-__host__ __device__ constexpr int slot_xor(int r) {
-  return ((((r >> 3) ^ (r >> 1)) & 1) << 1) | ((r >> 2) & 1);
-}
+__host__ __device__ constexpr int slot_xor(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 struct TileCoord {
   int m, n;

@@ -1,6 +1,6 @@
 """LDS layout and workgroup->tile order, through the built library (no GPU).
 
-The kernel's LDS tile rows are 64 bytes (four 16-byte slots).  hipgemm_lds_slot
+The kernel's LDS tile rows are 128 bytes (eight 16-byte slots).  hipgemm_lds_slot
 exposes the slot of (row, K-chunk); these tests check the properties the
 kernel relies on rather than restating the formula:
   * each row's chunk->slot map is a permutation (DMA lands every chunk once);
@@ -18,48 +18,54 @@ import pytest
 import hipgemm_amd as hg
 
 
+ROW = 128  # bytes per LDS tile row
+SLOTS = 8
+
+
 def slot(r, c):
     s = hg.lds_slot(r, c)
-    assert 0 <= s < 4
+    assert 0 <= s < SLOTS
     return s
 
 
 def test_slot_is_permutation_per_row():
     for r in range(512):
-        assert sorted(slot(r, c) for c in range(4)) == [0, 1, 2, 3], r
-    assert hg.lds_slot(-1, 0) == -1 and hg.lds_slot(0, 4) == -1
+        assert sorted(slot(r, c) for c in range(SLOTS)) == list(range(SLOTS)), r
+    assert hg.lds_slot(-1, 0) == -1 and hg.lds_slot(0, SLOTS) == -1
 
 
 def test_slot_depends_on_row_mod_16_only():
     for r in range(256):
-        for c in range(4):
+        for c in range(SLOTS):
             assert slot(r, c) == slot(r % 16, c)
 
 
 @pytest.mark.parametrize("base", [0, 32, 64, 96, 128, 160, 192, 224])
 def test_operand_fetch_bank_conflict_free(base):
     # lane l of an MFMA fragment fetch reads row base + l%32 at chunk
-    # 2*(l//32) + t, t in {0, 1}; hardware serves 16 (or 8) lanes at a time.
-    for t in (0, 1):
-        addrs = [(base + l % 32) * 64 + slot(base + l % 32, 2 * (l // 32) + t) * 16
+    # 4*kh + 2*(l//32) + t (K-half kh, sub-chunk t); hardware serves 16 (or 8)
+    # lanes at a time.
+    for kh, t in ((0, 0), (0, 1), (1, 0), (1, 1)):
+        addrs = [(base + l % 32) * ROW +
+                 slot(base + l % 32, 4 * kh + 2 * (l // 32) + t) * 16
                  for l in range(64)]
         for g0 in range(0, 64, 16):
             grp = addrs[g0:g0 + 16]
-            assert len({(a % 256) // 16 for a in grp}) == 16, (base, t, g0)
+            assert len({(a % 256) // 16 for a in grp}) == 16, (base, kh, t, g0)
         for g0 in range(0, 64, 8):
             grp = addrs[g0:g0 + 8]
-            assert len({(a % 128) // 16 for a in grp}) == 8, (base, t, g0)
+            assert len({(a % 128) // 16 for a in grp}) == 8, (base, kh, t, g0)
 
 
 def test_dma_fill_covers_every_chunk_once():
-    # DMA lane l of the instruction for rows [R0, R0+16) fetches chunk
-    # (l%4) ^ xor(row) into slot l%4 of row R0 + l//4; i.e. slot s of row r
+    # DMA lane l of the instruction for rows [R0, R0+8) fetches chunk
+    # (l%8) ^ xor(row) into slot l%8 of row R0 + l//8; i.e. slot s of row r
     # holds chunk c with lds_slot(r, c) == s.  Every (row, chunk) lands once.
-    for R0 in (0, 16, 240):
+    for R0 in (0, 8, 16, 248):
         seen = set()
         for l in range(64):
-            r, s = R0 + l // 4, l % 4
-            c = [c for c in range(4) if slot(r, c) == s]
+            r, s = R0 + l // 8, l % 8
+            c = [c for c in range(SLOTS) if slot(r, c) == s]
             assert len(c) == 1
             seen.add((r, c[0]))
         assert len(seen) == 64

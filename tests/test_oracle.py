@@ -184,7 +184,7 @@ def test_gemm_closed_forms(oracle):
     A = np.zeros((32, K), np.uint8)
     A[np.arange(32), perm] = 0x38  # 1.0
     bf = oracle.e4m3_to_f32(B)
-    want = oracle.f32_to_bf16(bf[:, perm].T.copy())
+    want = oracle.f32_to_bf16(bf[:, perm].T + np.float32(0))  # -0 sums to +0
     assert np.array_equal(oracle.gemm(A, B), want)
     # all-ones A: every row equals the row sums of B (exact: small integers*2^-9)
     Bu = oracle.fill((48, K), 10, po.UNIFORM, -1.0, 1.0)
