@@ -19,7 +19,7 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm_4wave(GemmArgs g) {
   gemm_4wave_body<kVecStore>(g, (lds_u8*)lds);
 }
 
-constexpr int kMaxLd = 1 << 23;  // 256 rows * ld must stay below 2^31
+constexpr int kMaxLd = 1 << 23;  // 256 rows * ld (bytes) must stay below 2^31
 
 bool aligned(const void* p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
@@ -31,7 +31,8 @@ hipError_t validate(const void* A, const void* B_T, void* C, int M, int N,
   if (variant < 0 || variant >= HIPGEMM_VARIANT_COUNT)
     return hipErrorInvalidValue;
   if (M == 0 || N == 0) return hipSuccess;
-  if (!C || !aligned(C, 2) || ldc < N) return hipErrorInvalidValue;
+  if (!C || !aligned(C, 2) || ldc < N || ldc > kMaxLd)
+    return hipErrorInvalidValue;
   if (K == 0) return hipSuccess;  // A and B_T are not read
   if (!A || !B_T) return hipErrorInvalidValue;
   if (K % 16 != 0) return hipErrorInvalidValue;
@@ -48,7 +49,9 @@ int tiles_of(int M, int N) {
 
 hipError_t launch_4wave(const GemmArgs& g, hipStream_t stream) {
   const int grid = tiles_of(g.M, g.N);
-  const bool vec = (g.ldc % 4 == 0) && aligned(g.C, 8);
+  // 16-byte epilogue stores need 8-column groups that never straddle N and
+  // 16-byte aligned rows.
+  const bool vec = (g.N % 8 == 0) && (g.ldc % 8 == 0) && aligned(g.C, 16);
   void* args[] = {const_cast<GemmArgs*>(&g)};
   const void* fn = vec ? reinterpret_cast<const void*>(&k_fp8_gemm_4wave<true>)
                        : reinterpret_cast<const void*>(&k_fp8_gemm_4wave<false>);

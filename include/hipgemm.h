@@ -20,7 +20,7 @@
  * Errors: every entry point returns a hipError_t and never exits the
  * process.  Argument errors return hipErrorInvalidValue before any HIP call,
  * so they can be checked on a machine without a GPU.  Requirements:
- *   M, N, K >= 0;  C non-NULL, 2-byte aligned, ldc >= N;
+ *   M, N, K >= 0;  C non-NULL, 2-byte aligned, N <= ldc <= 2^23;
  *   A, B_T non-NULL and 16-byte aligned;  K % 16 == 0;
  *   lda >= K, ldb >= K, lda % 16 == 0, ldb % 16 == 0, lda, ldb <= 2^23.
  * M == 0 or N == 0 is a no-op (nothing is checked or written).  K == 0

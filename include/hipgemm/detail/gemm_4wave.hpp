@@ -40,9 +40,11 @@
 // zero; K-chunks past K get an out-of-range offset.  Nothing outside A or B is
 // ever addressed.
 //
-// Epilogue: acc * (scale_a * scale_b) -> bf16 (RNE), one 8-byte store of 4
-// consecutive columns per lane per (block, 8-row group); per-lane masks keep
-// every write inside M x N.
+// Epilogue: acc * (scale_a * scale_b) -> bf16 (RNE), staged through LDS so
+// that every store instruction writes whole 128-byte lines of C (16 bytes per
+// lane, 4 rows x 256 B); 2-byte stores straight from the accumulators when N,
+// ldc or C's alignment do not allow 16.  No branches: lanes outside M x N are
+// dropped by the buffer range check.
 #pragma once
 
 #include "arch.hpp"
@@ -269,33 +271,111 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
 
     // ---- epilogue --------------------------------------------------------
     // acc[i][j] holds D = B_blk . A_blk^T, i.e. C^T for the 32x32 block:
-    // lane l, register r -> C row (l % 32), C column 8*(r/4) + 4*(l/32) + r%4.
-    const int m_lane = tc.m * Cfg::kBM + wm * 128 + (lane & 31);
-    const int n_lane = tc.n * Cfg::kBN + wn * 128 + 4 * (lane >> 5);
+    // lane l, register r -> C row (l % 32), C column 8*(r/4) + 4*(l/32) + r%4,
+    // so each lane holds 4 consecutive bf16 (8 bytes) per (i, j, r/4).
+    // Multiplying by a scale of 1.0 is exact (NaN and -0 included), so every
+    // call takes the same path.
+    auto cvt4 = [&](const f32x16& v, int q) {
+      return u32x2{pack_bf16x2(v[4 * q + 0] * scale, v[4 * q + 1] * scale),
+                   pack_bf16x2(v[4 * q + 2] * scale, v[4 * q + 3] * scale)};
+    };
+    // Out-of-range bit for "x < limit" as plain arithmetic (no lane masks,
+    // which would pin scalar register pairs): kOobOffset when x >= limit.
+    auto oob_unless = [](int x, int limit) -> uint32_t {
+      return (uint32_t)((limit - 1 - x) >> 31) & kOobOffset;
+    };
+    // Every store is a buffer store over this tile's window of C; a lane
+    // whose row or columns fall outside M x N gets an out-of-range offset and
+    // its write is dropped by the hardware range check -- no branches.
+    // Lane-derived epilogue values hang off an opaque copy of the lane id so
+    // the optimiser cannot hoist them out of the tile loop, where they would
+    // stay live through the K loop and spill.
+    int elane = lane;
+    asm volatile("" : "+v"(elane));
+    const int rows_c = min(Cfg::kBM, M - tc.m * Cfg::kBM);
+    const __amdgpu_buffer_rsrc_t rsrc_c = make_rsrc(
+        g.C + (size_t)tc.m * Cfg::kBM * g.ldc + (size_t)tc.n * Cfg::kBN,
+        (uint32_t)(((rows_c - 1) * g.ldc + Cfg::kBN) * 2));
+    const int rows_left = M - tc.m * Cfg::kBM - wm * 128;  // from wave row 0
+    const int cols_left = N - tc.n * Cfg::kBN - wn * 128;  // from wave col 0
+
+    if constexpr (kVecStore) {
+      // Through LDS: each wave stages its 128 x 128 bf16 quadrant (32 KiB) in
+      // its own quarter of the now idle stage buffers, then stores 16 bytes
+      // per lane row-major -- 4 rows x 256 B per instruction, whole 128-byte
+      // lines.  Staging layout: row r at 256 r, 16-byte chunk k of the row
+      // at slot k ^ (r % 16): conflict-free for the 8-byte writes (16 rows,
+      // one chunk) and for the 16-byte reads (one row, 16 chunks).
+      wait_vmcnt<0>();   // no DMA (real or padding) still landing in LDS
+      barrier();         // every wave is done reading the stages
+      lds_u8* stage_c = lds + wave * (128 * 256);
+      const uint32_t wlane = (elane & 31) * 256 + 8 * (elane >> 5);
+      const uint32_t xr16 = (elane & 15) * 16;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = m_lane + 32 * i;
-      if (m < M) {
-        uint16_t* crow = g.C + (size_t)m * g.ldc;
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            lds_write8(stage_c + wlane + 32 * i * 256 + (((4 * j + q) * 16) ^ xr16),
+                       cvt4(acc[i][j], q));
+          sched_fence();  // bound the live range: one block at a time
+        }
+      wait_lgkmcnt<0>();  // own quadrant only: no cross-wave hand-off
+      // read: lane l takes row 4p + l/16, chunk l % 16
+      const int rsub = elane >> 4, chunk = elane & 15;
+      const uint32_t rlane_base = rsub * 256;
+      uint32_t rx[4];
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+        rx[x] = rlane_base + ((chunk ^ ((4 * x + rsub) & 15)) * 16);
+      const uint32_t vcol = (uint32_t)((rsub * g.ldc + wn * 128 + 8 * chunk) * 2);
+      const uint32_t col_oob = oob_unless(8 * chunk, cols_left);
+#pragma unroll
+      for (int p0 = 0; p0 < 32; p0 += 8) {
+        i32x4 v[8];
+#pragma unroll
+        for (int p = p0; p < p0 + 8; ++p)
+          v[p - p0] = lds_read16(stage_c + rx[p & 3] + 1024 * p);
+#pragma unroll
+        for (int p = p0; p < p0 + 8; ++p) {
+          int row4 = 4 * p;
+          asm volatile("" : "+s"(row4));  // recompute per store, never hoist
+          const int srow =
+              __builtin_amdgcn_readfirstlane((wm * 128 + row4) * g.ldc * 2);
+          __builtin_amdgcn_raw_buffer_store_b128(
+              v[p - p0], rsrc_c,
+              vcol | col_oob | oob_unless(row4 + rsub, rows_left), srow, 0);
+        }
+        sched_fence();  // at most 8 rows (32 VGPRs) in flight
+      }
+    } else {
+      // N, ldc or C's alignment rule out 16-byte stores: 2-byte stores
+      // straight from the accumulators, lane masks as out-of-range offsets.
+      const uint32_t vlane =
+          (uint32_t)(((elane & 31) * g.ldc + wn * 128 + 4 * (elane >> 5)) * 2);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int srow =
+            __builtin_amdgcn_readfirstlane((wm * 128 + 32 * i) * g.ldc * 2);
+        const uint32_t vrow = vlane | oob_unless(32 * i + (elane & 31), rows_left);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int n0 = n_lane + 32 * j + 8 * q;
-            const float v0 = acc[i][j][4 * q + 0] * scale;
-            const float v1 = acc[i][j][4 * q + 1] * scale;
-            const float v2 = acc[i][j][4 * q + 2] * scale;
-            const float v3 = acc[i][j][4 * q + 3] * scale;
-            const uint32_t lo = pack_bf16x2(v0, v1), hi = pack_bf16x2(v2, v3);
-            if (kVecStore && n0 + 3 < N) {
-              *reinterpret_cast<u32x2*>(crow + n0) = u32x2{lo, hi};
-            } else {
-              if (n0 + 0 < N) crow[n0 + 0] = (uint16_t)lo;
-              if (n0 + 1 < N) crow[n0 + 1] = (uint16_t)(lo >> 16);
-              if (n0 + 2 < N) crow[n0 + 2] = (uint16_t)hi;
-              if (n0 + 3 < N) crow[n0 + 3] = (uint16_t)(hi >> 16);
+            const int c = 32 * j + 8 * q + 4 * (elane >> 5);
+            const u32x2 v = cvt4(acc[i][j], q);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const uint32_t w = (r < 2 ? v.x : v.y) >> (16 * (r & 1));
+              __builtin_amdgcn_raw_buffer_store_b16(
+                  (unsigned short)w, rsrc_c,
+                  (vrow | oob_unless(c + r, cols_left)) +
+                      (32 * j + 8 * q + r) * 2,
+                  srow, 0);
             }
           }
+          sched_fence();  // bound the live range: one block at a time
         }
       }
     }

@@ -49,6 +49,7 @@ def test_version_and_variants():
     dict(B=FAKE + 4),                  # B_T not 16-byte aligned
     dict(C=FAKE + 1),                  # C not 2-byte aligned
     dict(lda=(1 << 23) + 16),          # lda too large for 32-bit offsets
+    dict(ldc=(1 << 23) + 4),           # ldc too large for 32-bit offsets
     dict(variant=7), dict(variant=-1),
 ])
 def test_argument_validation(args):
