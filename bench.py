@@ -200,6 +200,10 @@ def main():
         f"best={kern_ms.min():.4f} -> {achieved:.1f} TFLOP/s avg, "
         f"{flop / (kern_ms.min() * 1e-3) / 1e12:.1f} best; wall/step "
         f"{ms_per_step:.4f} ms")
+    # Sustained launches settle to a power-limited clock: show the drift.
+    parts = np.array_split(kern_ms, min(10, len(kern_ms)))
+    log("bench: kernel ms by tenth of the timed loop: "
+        + " ".join(f"{p.mean():.4f}" for p in parts))
 
     workload = f"fp8_gemm_{M}x{N}x{K}"
     result = {

@@ -85,6 +85,22 @@ __device__ __forceinline__ f32x4 mfma_16x16x128(i32x8 x, i32x8 y, f32x4 acc) {
                                                           0, 0);
 }
 
+// One accumulator element (AGPR) -> VGPR at this point of the program.  The
+// compiler otherwise copies every live accumulator to VGPRs at the end of the
+// K loop in one burst, which needs 256 VGPRs on top of the live ones.
+__device__ __forceinline__ float acc_read(float a) {
+  float v;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+  return v;
+}
+// 32 wait states, issued in place: covers the MFMA-result-to-VALU-read
+// latency ahead of the first acc_read after an MFMA.
+__device__ __forceinline__ void mfma_drain() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 15\n\ts_nop 15" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // Two fp32 -> packed bf16x2, round-to-nearest-even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   bf16x2_t v = __builtin_convertvector(f32x2{lo, hi}, bf16x2_t);

@@ -268,6 +268,11 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     }
     wait_vmcnt<0>();
     wait_lgkmcnt<0>();
+    // The accumulators are read below by explicit v_accvgpr_read (acc_read),
+    // which the compiler's hazard tracking does not see: give the last MFMA
+    // its result latency here (a 16-pass XDL write needs 19 wait states
+    // before a VALU read; 32 are inserted).
+    mfma_drain();
 
     // ---- epilogue --------------------------------------------------------
     // acc[i][j] holds D = B_blk . A_blk^T, i.e. C^T for the 32x32 block:
@@ -276,8 +281,10 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     // Multiplying by a scale of 1.0 is exact (NaN and -0 included), so every
     // call takes the same path.
     auto cvt4 = [&](const f32x16& v, int q) {
-      return u32x2{pack_bf16x2(v[4 * q + 0] * scale, v[4 * q + 1] * scale),
-                   pack_bf16x2(v[4 * q + 2] * scale, v[4 * q + 3] * scale)};
+      return u32x2{pack_bf16x2(acc_read(v[4 * q + 0]) * scale,
+                               acc_read(v[4 * q + 1]) * scale),
+                   pack_bf16x2(acc_read(v[4 * q + 2]) * scale,
+                               acc_read(v[4 * q + 3]) * scale)};
     };
     // Out-of-range bit for "x < limit" as plain arithmetic (no lane masks,
     // which would pin scalar register pairs): kOobOffset when x >= limit.
