@@ -46,7 +46,7 @@ extern "C" {
 /* Schedules.  AUTO picks by shape (hipgemm_select_variant). */
 enum {
   HIPGEMM_VARIANT_AUTO = 0,
-  /* 256 threads (4 waves, one per SIMD), 256 x 256 tile, 4-stage LDS ring,
+  /* 256 threads (4 waves, one per SIMD), 256 x 256 tile, 2 LDS stages,
    * v_mfma_f32_32x32x64_f8f6f4.  The schedule behind the drop-in template. */
   HIPGEMM_VARIANT_4WAVE = 1,
   HIPGEMM_VARIANT_COUNT = 2

@@ -251,6 +251,32 @@ class RefLib:
         return out
 
 
+class RefGpu:
+    """The reference's GPU kernel (fp8_4wave.hpp:334-567) behind the launcher
+    of ref_kernel_launch.hip, built into oracle/_ref/libref_gpu.so by ``make
+    -C oracle ref``.  Measurement only: bench.py times it beside the product
+    kernel.  It has no scales and truncates to bf16."""
+
+    SHAPES = {(4096, 4096, 4096), (8192, 8192, 8192), (8192, 28672, 8192),
+              (8192, 8192, 28672)}
+
+    def __init__(self, path: Optional[str] = None):
+        path = path or os.path.join(HERE, "_ref", "libref_gpu.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        self.lib = ctypes.CDLL(path)
+        self.fn = self.lib.hipgemm_reference_4wave
+        self.fn.argtypes = [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int,
+                            ctypes.c_int, _vp]
+        self.fn.restype = ctypes.c_int
+
+    def launch(self, A_ptr: int, B_ptr: int, C_ptr: int, M: int, N: int,
+               K: int, stream_ptr: int) -> None:
+        err = self.fn(A_ptr, B_ptr, C_ptr, M, N, K, stream_ptr)
+        if err != 0:
+            raise RuntimeError(f"reference kernel launch failed: {err}")
+
+
 _oracle: Optional[Oracle] = None
 
 

@@ -1,0 +1,70 @@
+"""Same-harness speed check against the reference's own kernel.
+
+The reference's fp8_gemm_4wave_256x256x128<M,N,K> (fp8_4wave.hpp:334-567),
+compiled from its sources into oracle/_ref/libref_gpu.so, and this library's
+kernel are timed by bench.time_kernel -- the bench's own protocol: warm-up,
+then back-to-back launches over rotating A/B sets of at least 512 MiB -- on
+the same inputs, stream and output buffer, in the same process.  The test
+prints both rates and fails if this library falls below 90% of the
+reference (a regression gate, not the target).  Skipped where the reference
+build is absent.
+"""
+from __future__ import annotations
+
+import math
+import os
+
+import pytest
+
+from util import say
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(8192, 8192, 8192), (4096, 4096, 4096)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_speed_vs_reference_kernel(gpu, M, N, K):
+    torch = gpu
+    from oracle import pyoracle as po
+    try:
+        ref = po.RefGpu()
+    except (FileNotFoundError, OSError):
+        pytest.skip("oracle/_ref/libref_gpu.so not built")
+    import bench
+    import hipgemm_amd as hg
+
+    dev = torch.device("cuda:0")
+    nsets = max(1, math.ceil((512 << 20) / (M * K + N * K)))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    As = [torch.randn((M, K), generator=gen, device=dev).clamp_(-448, 448)
+          .to(torch.float8_e4m3fn) for _ in range(nsets)]
+    Bs = [torch.randn((N, K), generator=gen, device=dev).clamp_(-448, 448)
+          .to(torch.float8_e4m3fn) for _ in range(nsets)]
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    ptrs = [(a.data_ptr(), b.data_ptr()) for a, b in zip(As, Bs)]
+    cptr, sptr = out.data_ptr(), stream.cuda_stream
+
+    def mine(i):
+        a, b = ptrs[i % nsets]
+        code = hg.gemm_raw(a, b, cptr, M, N, K, K, K, N, 0, 0, 0, sptr)
+        assert code == 0, code
+
+    def theirs(i):
+        a, b = ptrs[i % nsets]
+        ref.launch(a, b, cptr, M, N, K, sptr)
+
+    steps = int(os.environ.get("HIPGEMM_PERF_STEPS", "200"))
+    flop = 2.0 * M * N * K
+    say(f"speed {M}x{N}x{K}: timing reference then hipgemm, {steps} steps")
+    r = bench.time_kernel(theirs, steps, steps, stream)
+    m = bench.time_kernel(mine, steps, steps, stream)
+    tr = flop / (r["wall_ms"] * 1e-3) / 1e12
+    tm = flop / (m["wall_ms"] * 1e-3) / 1e12
+    say(f"speed {M}x{N}x{K}: reference {tr:.1f} TFLOP/s "
+        f"({r['wall_ms']:.4f} ms/step, best {r['best_ms']:.4f}); "
+        f"hipgemm {tm:.1f} TFLOP/s ({m['wall_ms']:.4f} ms/step, best "
+        f"{m['best_ms']:.4f}); ratio {tm / tr:.3f}")
+    assert tm >= 0.9 * tr
