@@ -5,6 +5,7 @@
 // include/hipgemm/detail/, instantiated here with runtime shapes.
 #include "hipgemm.h"
 
+#include <atomic>
 #include <cstdint>
 
 #include "hipgemm/fp8_gemm.hpp"
@@ -13,10 +14,10 @@ namespace {
 
 using namespace hipgemm::detail;
 
-template <bool kVecStore>
+template <bool kVecStore, int kMf>
 __global__ __launch_bounds__(256, 1) void k_fp8_gemm_4wave(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg4w::kLdsBytes];
-  gemm_4wave_body<kVecStore>(g, (lds_u8*)lds);
+  gemm_4wave_body<kVecStore, kMf>(g, (lds_u8*)lds);
 }
 
 constexpr int kMaxLd = 1 << 23;  // 256 rows * ld (bytes) must stay below 2^31
@@ -47,14 +48,38 @@ int tiles_of(int M, int N) {
   return ((M + Cfg4w::kBM - 1) / Cfg4w::kBM) * ((N + Cfg4w::kBN - 1) / Cfg4w::kBN);
 }
 
-hipError_t launch_4wave(const GemmArgs& g, hipStream_t stream) {
-  const int grid = tiles_of(g.M, g.N);
+// Compute units of the current device, queried once per device (a lazily
+// filled, thread-safe cache; concurrent first calls store the same value).
+int cu_count() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+            hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+template <int kMf>
+hipError_t launch_4wave(GemmArgs g, hipStream_t stream) {
+  // Persistent grid: one workgroup per CU at most (the kernel's 160 KiB of
+  // LDS allows no more), each walking tiles w, w + grid, ...
+  const int tiles = tiles_of(g.M, g.N);
+  const int cus = cu_count();
+  const int grid = tiles < cus ? tiles : cus;
+  g.workers = grid;
   // 16-byte epilogue stores need 8-column groups that never straddle N and
   // 16-byte aligned rows.
   const bool vec = (g.N % 8 == 0) && (g.ldc % 8 == 0) && aligned(g.C, 16);
-  void* args[] = {const_cast<GemmArgs*>(&g)};
-  const void* fn = vec ? reinterpret_cast<const void*>(&k_fp8_gemm_4wave<true>)
-                       : reinterpret_cast<const void*>(&k_fp8_gemm_4wave<false>);
+  void* args[] = {&g};
+  const void* fn =
+      vec ? reinterpret_cast<const void*>(&k_fp8_gemm_4wave<true, kMf>)
+          : reinterpret_cast<const void*>(&k_fp8_gemm_4wave<false, kMf>);
   return hipLaunchKernel(fn, dim3(grid), dim3(Cfg4w::kThreads), args, 0,
                          stream);
 }
@@ -67,7 +92,9 @@ int hipgemm_select_variant(int M, int N, int K) {
   (void)M;
   (void)N;
   (void)K;
-  return HIPGEMM_VARIANT_4WAVE;
+  // 16x16x128 sustains a higher clock than 32x32x64 under the power limit
+  // that caps long GEMMs on MI355X (same work per step).
+  return HIPGEMM_VARIANT_4WAVE_MFMA16;
 }
 
 hipError_t hipgemm_fp8_gemm_bf16(const void* A, const void* B_T, void* C,
@@ -92,11 +119,14 @@ hipError_t hipgemm_fp8_gemm_bf16(const void* A, const void* B_T, void* C,
              lda,
              ldb,
              ldc,
-             default_group_m(tiles_m, tiles_n)};
+             default_group_m(tiles_m, tiles_n),
+             0};
   switch (variant) {
+    case HIPGEMM_VARIANT_4WAVE_MFMA16:
+      return launch_4wave<16>(g, stream);
     case HIPGEMM_VARIANT_4WAVE:
     default:
-      return launch_4wave(g, stream);
+      return launch_4wave<32>(g, stream);
   }
 }
 
@@ -104,7 +134,7 @@ hipError_t hipgemm_fp8_gemm_4wave_256x256x128(const void* A, const void* B_T,
                                               void* C, int M, int N, int K,
                                               hipStream_t stream) {
   return hipgemm_fp8_gemm_bf16(A, B_T, C, M, N, K, K, K, N, nullptr, nullptr,
-                               HIPGEMM_VARIANT_4WAVE, stream);
+                               HIPGEMM_VARIANT_4WAVE_MFMA16, stream);
 }
 
 const char* hipgemm_variant_name(int variant) {
@@ -112,7 +142,9 @@ const char* hipgemm_variant_name(int variant) {
     case HIPGEMM_VARIANT_AUTO:
       return "auto";
     case HIPGEMM_VARIANT_4WAVE:
-      return "4wave_256x256x128_q4";
+      return "4wave_256x256x128_mfma32";
+    case HIPGEMM_VARIANT_4WAVE_MFMA16:
+      return "4wave_256x256x128_mfma16";
     default:
       return nullptr;
   }

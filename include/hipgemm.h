@@ -47,9 +47,12 @@ extern "C" {
 enum {
   HIPGEMM_VARIANT_AUTO = 0,
   /* 256 threads (4 waves, one per SIMD), 256 x 256 tile, 2 LDS stages,
-   * v_mfma_f32_32x32x64_f8f6f4.  The schedule behind the drop-in template. */
+   * persistent grid, v_mfma_f32_32x32x64_f8f6f4. */
   HIPGEMM_VARIANT_4WAVE = 1,
-  HIPGEMM_VARIANT_COUNT = 2
+  /* The same schedule on v_mfma_f32_16x16x128_f8f6f4.  AUTO's choice, and
+   * the schedule behind the drop-in template. */
+  HIPGEMM_VARIANT_4WAVE_MFMA16 = 2,
+  HIPGEMM_VARIANT_COUNT = 3
 };
 
 /*
@@ -67,7 +70,7 @@ hipError_t hipgemm_fp8_gemm_bf16(const void *A, const void *B_T, void *C,
 
 /*
  * The reference launch with runtime shapes: packed strides (lda = ldb = K,
- * ldc = N), no scales, the 4-wave schedule.
+ * ldc = N), no scales, the 4-wave schedule (16x16x128 MFMA).
  * Replaces: fp8_gemm_4wave_256x256x128<M, N, K><<<(M*N)/65536, 256>>>(A, B_T,
  * C) at test.cpp:79 and bench.cpp:55/78.
  */

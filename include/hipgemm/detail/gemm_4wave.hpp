@@ -5,13 +5,17 @@
 // fp8_4wave.hpp:334-567 (same interface and block shape, different design).
 //
 // Work decomposition
-//   * One workgroup = 256 threads = 4 waves (one per SIMD) = one 256 x 256
-//     output tile at a time; a grid smaller than the tile count loops over
-//     tiles, so any grid size >= 1 is correct.
-//   * Wave w owns the contiguous 128 x 128 quadrant (w / 2, w % 2) of the tile
+//   * One workgroup = 256 threads = 4 waves (one per SIMD).  The grid is
+//     persistent: `workers` workgroups (at most one per CU) walk the 256 x 256
+//     output tiles t = w, w + workers, w + 2 * workers, ...  Workgroups with
+//     blockIdx.x >= workers return at once, so any launch grid >= 1 is
+//     correct.
+//   * Wave w owns the contiguous 128 x 128 quadrant (w / 2, w % 2) of a tile
 //     as 4 x 4 blocks of 32 x 32 fp32 accumulators (256 AGPRs per lane).
 //   * K advances 128 bytes per step (one LDS stage); each of the 16 blocks
-//     takes two v_mfma_f32_32x32x64_f8f6f4 per step (K-halves).
+//     takes two v_mfma_f32_32x32x64_f8f6f4 per step (K-halves).  The step
+//     count per tile is padded to an even number >= 4 (padding steps read
+//     zeros).
 //
 // Operand registers: four tiles of 64 rows x 128 K-bytes (32 VGPRs each):
 // a_lo / a_hi = the wave's A rows 0-63 / 64-127, b_lo / b_hi likewise for B.
@@ -25,14 +29,23 @@
 // LDS holds 2 stages (A 256 x 128 B + B 256 x 128 B each, 128 KiB).  Each
 // 64-row sub-buffer group (e.g. "A_lo" = A rows 0-63 and 128-191, the a_lo
 // rows of both wave rows) is read in one quarter-step and refilled in the
-// next; the refill is read seven quarter-steps later (~1.75 steps, ~3.5K
-// cycles of DMA latency slack).  Every quarter-step starts with: wait own
-// LDS reads (the group read last quarter is free), wait own DMA up to the
-// group read this quarter (vmcnt 24), s_barrier.  Inside a quarter the 8 LDS
-// reads go two per MFMA in the first half and the 4 DMA one per MFMA in the
-// second half, so the per-CU address unit is never offered more than about
-// one 1 KiB DMA per 16 cycles.  DMA issued for steps past the end of K reads
-// zeros (every lane out of range); the step count is padded to even.
+// next; the refill is read seven quarter-steps later (~1.75 steps of DMA
+// latency slack).  Every quarter-step starts with: wait own LDS reads (the
+// group read last quarter is free), wait own DMA up to the group read this
+// quarter, s_barrier.  Inside a quarter the 8 LDS reads go two per MFMA in
+// the first half and the 4 DMA one per MFMA in the second half.
+//
+// Across tiles the pipeline does not drain: "step k+2" and "step k+3" of the
+// last steps of a tile are steps 0, 1 and 2 of the workgroup's next tile
+// (all-zero reads when there is none), so the next tile's operands are in
+// LDS, and its a_lo / b_lo in registers, when the epilogue runs.  The
+// epilogue stages through a separate 32 KiB LDS region and issues its 32
+// stores per wave without waiting for them; the next tile's first seven
+// quarter-steps wait with vmcnt 24 + 32 (the stores sit between the DMA
+// group each of them needs and the newer DMAs), the eighth and later with
+// vmcnt 24, by when the stores have long completed.  vmcnt retires memory
+// operations in issue order, loads and stores alike.  The first tile of a
+// workgroup waits for all of its prologue DMA instead.
 //
 // Global -> LDS: buffer_load_dwordx4 ... lds, 8 rows x 128 B per instruction
 // (whole 128-byte lines), 16 instructions per wave per step.  The buffer
@@ -40,12 +53,14 @@
 // zero; K-chunks past K get an out-of-range offset.  Nothing outside A or B is
 // ever addressed.
 //
-// Epilogue: acc * (scale_a * scale_b) -> bf16 (RNE), staged through LDS so
-// that every store instruction writes whole 128-byte lines of C (16 bytes per
-// lane, 4 rows x 256 B); 2-byte stores straight from the accumulators when N,
-// ldc or C's alignment do not allow 16.  No branches: lanes outside M x N are
-// dropped by the buffer range check.
+// Epilogue: acc * (scale_a * scale_b) -> bf16 (RNE), staged 32 rows at a time
+// through the wave's own 8 KiB of LDS so that every store instruction writes
+// whole 128-byte lines of C (16 bytes per lane, 4 rows x 256 B); 2-byte stores
+// straight from the accumulators when N, ldc or C's alignment do not allow
+// 16.  No branches: lanes outside M x N are dropped by the buffer range check.
 #pragma once
+
+#include <type_traits>
 
 #include "arch.hpp"
 #include "layout.hpp"
@@ -62,6 +77,7 @@ struct GemmArgs {
   int M, N, K;
   int lda, ldb, ldc;
   int group_m;
+  int workers;  // persistent workgroups (<= grid); 0 = the whole grid
 };
 
 __host__ __device__ constexpr int default_group_m(int tiles_m, int tiles_n) {
@@ -79,29 +95,96 @@ struct Cfg4w {
   static constexpr int kBStage = kBN * kBK;  // 32 KiB
   static constexpr int kABase = 0;
   static constexpr int kBBase = kStages * kAStage;
-  static constexpr int kLdsBytes = kStages * (kAStage + kBStage);  // 128 KiB
+  static constexpr int kStageEnd = kStages * (kAStage + kBStage);  // 128 KiB
+  static constexpr int kStoreRows = 32;                 // epilogue chunk
+  static constexpr int kStoreStage = kStoreRows * 256;  // 8 KiB per wave
+  static constexpr int kStoreBase = kStageEnd;
+  static constexpr int kLdsBytes = kStageEnd + 4 * kStoreStage;  // 160 KiB
   static constexpr int kDmaPerStep = 16;  // per wave: 8 for A, 8 for B
+  static constexpr int kStoresPerTile = 32;  // per wave, 16-byte path
+  // Workers of the C++ drop-in template, whose grid the caller sizes to the
+  // tile count: one per CU of an MI355X.
+  static constexpr int kDropinWorkers = 256;
 };
 
-// sched_group_barrier pattern of one quarter-step: 8 MFMA (0x008); two LDS
-// reads (0x100) after each of the first 4, one DMA (0x020) after each of the
-// last 4.
-__device__ __forceinline__ void quarter_schedule() {
-  for (int x = 0; x < 4; ++x) {
+// MFMA per quarter-step, and how many of them (the "tail") are issued after
+// the next quarter-step's wait + barrier instead of before it.  MFMA read
+// only registers, so they may straddle the barrier; the tail keeps the
+// matrix unit busy while the waves meet, which hides the skew between them
+// (one 64-cycle MFMA for 32x32x64, two 32-cycle ones for 16x16x128).
+template <int kMf>
+struct QuarterShape {
+  static constexpr int kMfma = kMf == 16 ? 16 : 8;
+  static constexpr int kTail = kMf == 16 ? 2 : 1;
+  static constexpr int kHead = kMfma - kTail;
+};
+
+// sched_group_barrier pattern of one quarter-step region: the previous
+// quarter's tail MFMA (0x008) first, then this quarter's head MFMA with its
+// 8 LDS reads (0x100) in the first half and its 4 DMA (0x020) after.
+// 32x32x64: [M R R] x 4, [M D] x 2, [M D D].  16x16x128: [M R] x 8,
+// [M D] x 4, [M] x 2.
+template <int kMf>
+__device__ __forceinline__ void quarter_schedule(bool tail) {
+  if (tail)
+    __builtin_amdgcn_sched_group_barrier(0x008, QuarterShape<kMf>::kTail, 0);
+  if constexpr (kMf == 16) {
+    for (int x = 0; x < 8; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    for (int x = 0; x < 4; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  } else {
+    for (int x = 0; x < 4; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    for (int x = 0; x < 2; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-  }
-  for (int x = 0; x < 4; ++x) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
   }
 }
 
-template <bool kVecStore>
+// Operand windows of one output tile: buffer resources over the tile's valid
+// rows of A and B_T (none at all past the last tile, so every read is zero).
+struct TileSrc {
+  __amdgpu_buffer_rsrc_t a, b;
+};
+
+__device__ __forceinline__ TileSrc tile_src(const GemmArgs& g, int t,
+                                            int tiles, int tiles_m,
+                                            int tiles_n) {
+  if (t >= tiles) return TileSrc{make_rsrc(g.A, 0), make_rsrc(g.B, 0)};
+  const TileCoord tc = grouped_tile(t, tiles_m, tiles_n, g.group_m);
+  const int rows_a = min(Cfg4w::kBM, g.M - tc.m * Cfg4w::kBM);
+  const int rows_b = min(Cfg4w::kBN, g.N - tc.n * Cfg4w::kBN);
+  return TileSrc{make_rsrc(g.A + (size_t)tc.m * Cfg4w::kBM * g.lda,
+                           (uint32_t)rows_a * (uint32_t)g.lda),
+                 make_rsrc(g.B + (size_t)tc.n * Cfg4w::kBN * g.ldb,
+                           (uint32_t)rows_b * (uint32_t)g.ldb)};
+}
+
+// kMf selects the MFMA: 32 = v_mfma_f32_32x32x64_f8f6f4 (4 x 4 blocks of
+// 32 x 32 per wave, two MFMA per block per step), 16 =
+// v_mfma_f32_16x16x128_f8f6f4 (8 x 8 blocks of 16 x 16, one per block per
+// step).  Same data flow and the same 2048 MFMA cycles per step either way.
+template <bool kVecStore, int kMf = 32>
 __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                                                 lds_u8* lds) {
   using Cfg = Cfg4w;
+  static_assert(kMf == 32 || kMf == 16, "MFMA shape");
+  constexpr bool k16 = kMf == 16;
   constexpr int kDmaPerGroup = 4;  // per wave
+  constexpr int kWaitSteady = 6 * kDmaPerGroup;
+  constexpr int kWaitAfterStores = kWaitSteady + Cfg::kStoresPerTile;
+  static_assert(kWaitAfterStores < 64, "vmcnt range");
   const int lane = lane_id();
   const int wave = wave_id();
   const int wm = wave >> 1, wn = wave & 1;
@@ -111,7 +194,12 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   const int tiles_n = (N + Cfg::kBN - 1) / Cfg::kBN;
   const int tiles = tiles_m * tiles_n;
   const int kt_real = (K + Cfg::kBK - 1) / Cfg::kBK;
-  const int kt_pad = (kt_real + 1) & ~1;
+  const int kt_pad = max(4, (kt_real + 1) & ~1);
+  const int workers = g.workers > 0 ? min((int)gridDim.x, g.workers)
+                                    : (int)gridDim.x;
+  if ((int)blockIdx.x >= workers) return;
+  int t = xcd_contiguous(blockIdx.x, workers);
+  if (t >= tiles) return;
 
   const float sa = g.scale_a ? *g.scale_a : 1.0f;
   const float sb = g.scale_b ? *g.scale_b : 1.0f;
@@ -142,139 +230,199 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                             {lds + (off_a ^ 64u), lds + (off_a ^ 80u)}};
   const lds_u8* pb[2][2] = {{lds + off_b, lds + (off_b ^ 16u)},
                             {lds + (off_b ^ 64u), lds + (off_b ^ 80u)}};
+  // 16x16x128: fragment row lane%16; lane group g = lane/16 reads K-chunks
+  // 2g and 2g + 1 (32 bytes).
+  const int rrow16 = lane & 15;
+  const int rslot16 = (2 * (lane >> 4)) ^ slot_xor(rrow16);
+  const uint32_t off16_a =
+      Cfg::kABase + (wm * 128 + rrow16) * Cfg::kBK + rslot16 * 16;
+  const uint32_t off16_b =
+      Cfg::kBBase + (wn * 128 + rrow16) * Cfg::kBK + rslot16 * 16;
+  const lds_u8* pa16[2] = {lds + off16_a, lds + (off16_a ^ 16u)};
+  const lds_u8* pb16[2] = {lds + off16_b, lds + (off16_b ^ 16u)};
 
-  const int grid = gridDim.x;
-  for (int t = xcd_contiguous(blockIdx.x, grid); t < tiles; t += grid) {
-    const TileCoord tc = grouped_tile(t, tiles_m, tiles_n, g.group_m);
-    const int rows_a = min(Cfg::kBM, M - tc.m * Cfg::kBM);
-    const int rows_b = min(Cfg::kBN, N - tc.n * Cfg::kBN);
-    const __amdgpu_buffer_rsrc_t rsrc_a =
-        make_rsrc(g.A + (size_t)tc.m * Cfg::kBM * g.lda,
-                  (uint32_t)rows_a * (uint32_t)g.lda);
-    const __amdgpu_buffer_rsrc_t rsrc_b =
-        make_rsrc(g.B + (size_t)tc.n * Cfg::kBN * g.ldb,
-                  (uint32_t)rows_b * (uint32_t)g.ldb);
+  TileSrc cur = tile_src(g, t, tiles, tiles_m, tiles_n);
+  TileSrc nxt = tile_src(g, t + workers, tiles, tiles_m, tiles_n);
 
-    // DMA of one sub-buffer group of step kb into `stage`: operand op (0 = A,
-    // 1 = B), half hi (0 = lo group, 1 = hi group).  4 instructions per wave.
-    auto dma_group = [&](int kb, int stage, int op, int hi) {
-      uint32_t k0 = (uint32_t)kb * Cfg::kBK;
-      // Opaque to the optimiser: keeps the per-step lane masks from being
-      // hoisted out of the tile loop (they would pin VGPRs and spill).
-      asm volatile("" : "+s"(k0));
-      const bool ok = (int)(k0 + dchunk * 16) < K;
+  // DMA of one sub-buffer group of pipeline step kb into `stage`: operand op
+  // (0 = A, 1 = B), half hi (0 = lo group, 1 = hi group).  Steps kb >= kt_pad
+  // are steps kb - kt_pad of the next tile.  4 instructions per wave.
+  auto dma_group = [&](int kb, int stage, int op, int hi) {
+    const bool next = kb >= kt_pad;  // wave-uniform
+    uint32_t k0 = (uint32_t)(next ? kb - kt_pad : kb) * Cfg::kBK;
+    // Opaque to the optimiser: keeps the per-step lane masks from being
+    // hoisted out of the tile loop (they would pin VGPRs and spill).
+    asm volatile("" : "+s"(k0));
+    const bool ok = (int)(k0 + dchunk * 16) < K;
+    const __amdgpu_buffer_rsrc_t src =
+        op == 0 ? (next ? nxt.a : cur.a) : (next ? nxt.b : cur.b);
 #pragma unroll
-      for (int qq = 0; qq < kDmaPerGroup; ++qq) {
-        const int q = (qq & 1) + 4 * (qq >> 1) + 2 * hi;
-        if (op == 0)
-          dma16(rsrc_a,
-                lds + Cfg::kABase + stage * Cfg::kAStage + (4 * q + wave) * 1024,
-                ok ? voff_a[q] : kOobOffset, k0);
-        else
-          dma16(rsrc_b,
-                lds + Cfg::kBBase + stage * Cfg::kBStage + (4 * q + wave) * 1024,
-                ok ? voff_b[q] : kOobOffset, k0);
-      }
-    };
+    for (int qq = 0; qq < kDmaPerGroup; ++qq) {
+      const int q = (qq & 1) + 4 * (qq >> 1) + 2 * hi;
+      if (op == 0)
+        dma16(src, lds + Cfg::kABase + stage * Cfg::kAStage + (4 * q + wave) * 1024,
+              ok ? voff_a[q] : kOobOffset, k0);
+      else
+        dma16(src, lds + Cfg::kBBase + stage * Cfg::kBStage + (4 * q + wave) * 1024,
+              ok ? voff_b[q] : kOobOffset, k0);
+    }
+  };
 
-    i32x8 fa[4][2], fb[4][2];  // [32-row fragment][K-half]
-    // Register tile (op, hi) of `stage`: fragments 2hi, 2hi+1, both K-halves.
-    auto read_tile = [&](int op, int hi, int stage) {
+  i32x8 fa[4][2], fb[4][2];  // 32x32x64: [32-row fragment][K-half]
+  i32x8 fa16[8], fb16[8];    // 16x16x128: [16-row fragment]
+  // Register tile (op, hi) of `stage`: rows 64hi .. 64hi + 63 of the wave's
+  // 128 A (op 0) or B (op 1) rows, all 128 K-bytes.
+  auto read_tile = [&](int op, int hi, int stage) {
+    if constexpr (k16) {
 #pragma unroll
-      for (int f = 2 * hi; f < 2 * hi + 2; ++f)
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-          if (op == 0) {
-            const int o = stage * Cfg::kAStage + f * 32 * Cfg::kBK;
-            fa[f][kh] = join(lds_read16(pa[kh][0] + o), lds_read16(pa[kh][1] + o));
-          } else {
-            const int o = stage * Cfg::kBStage + f * 32 * Cfg::kBK;
-            fb[f][kh] = join(lds_read16(pb[kh][0] + o), lds_read16(pb[kh][1] + o));
-          }
+      for (int f = 4 * hi; f < 4 * hi + 4; ++f) {
+        if (op == 0) {
+          const int o = stage * Cfg::kAStage + f * 16 * Cfg::kBK;
+          fa16[f] = join(lds_read16(pa16[0] + o), lds_read16(pa16[1] + o));
+        } else {
+          const int o = stage * Cfg::kBStage + f * 16 * Cfg::kBK;
+          fb16[f] = join(lds_read16(pb16[0] + o), lds_read16(pb16[1] + o));
         }
-    };
-
-    f32x16 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-
-    // Quarter (qi, qj): blocks i in {2qi, 2qi+1} x j in {2qj, 2qj+1}, K-half
-    // major so the two MFMA of one accumulator are 4 apart.
-    auto quarter_mfma = [&](int qi, int qj) {
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int i = 2 * qi; i < 2 * qi + 2; ++i)
-#pragma unroll
-          for (int j = 2 * qj; j < 2 * qj + 2; ++j)
-            acc[i][j] = mfma_32x32x64(fb[j][kh], fa[i][kh], acc[i][j]);
-    };
-
-    auto quarter_sync = [&]() {
-      wait_lgkmcnt<0>();
-      wait_vmcnt<6 * kDmaPerGroup>();
-      barrier();
-    };
-
-    // Previous tile: all LDS reads done and all stores retired before the
-    // stages are overwritten.
-    wait_vmcnt<0>();
-    barrier();
-
-    // Prologue: steps 0 and 1 in group order A_lo, B_lo, B_hi, A_hi; then
-    // a_lo(0), b_lo(0) into registers and the A_lo group of step 2.
-#pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      dma_group(st, st, 0, 0);
-      dma_group(st, st, 1, 0);
-      dma_group(st, st, 1, 1);
-      dma_group(st, st, 0, 1);
-    }
-    wait_vmcnt<6 * kDmaPerGroup>();
-    barrier();
-    read_tile(0, 0, 0);
-    read_tile(1, 0, 0);
-    wait_lgkmcnt<0>();
-    barrier();
-    dma_group(2, 0, 0, 0);
-
-    for (int kt0 = 0; kt0 < kt_pad; kt0 += 2) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int kt = kt0 + s;
-        quarter_sync();  // Q00
-        quarter_mfma(0, 0);
-        read_tile(1, 1, s);
-        dma_group(kt + 2, s, 1, 0);
-        quarter_schedule();
-        quarter_sync();  // Q01
-        quarter_mfma(0, 1);
-        read_tile(0, 1, s);
-        dma_group(kt + 2, s, 1, 1);
-        quarter_schedule();
-        quarter_sync();  // Q10
-        quarter_mfma(1, 0);
-        read_tile(0, 0, s ^ 1);
-        dma_group(kt + 2, s, 0, 1);
-        quarter_schedule();
-        quarter_sync();  // Q11
-        quarter_mfma(1, 1);
-        read_tile(1, 0, s ^ 1);
-        dma_group(kt + 3, s ^ 1, 0, 0);
-        quarter_schedule();
       }
+      return;
     }
-    wait_vmcnt<0>();
-    wait_lgkmcnt<0>();
-    // The accumulators are read below by explicit v_accvgpr_read (acc_read),
-    // which the compiler's hazard tracking does not see: give the last MFMA
-    // its result latency here (a 16-pass XDL write needs 19 wait states
-    // before a VALU read; 32 are inserted).
-    mfma_drain();
+#pragma unroll
+    for (int f = 2 * hi; f < 2 * hi + 2; ++f)
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        if (op == 0) {
+          const int o = stage * Cfg::kAStage + f * 32 * Cfg::kBK;
+          fa[f][kh] = join(lds_read16(pa[kh][0] + o), lds_read16(pa[kh][1] + o));
+        } else {
+          const int o = stage * Cfg::kBStage + f * 32 * Cfg::kBK;
+          fb[f][kh] = join(lds_read16(pb[kh][0] + o), lds_read16(pb[kh][1] + o));
+        }
+      }
+  };
+
+  f32x16 acc[4][4];   // 32x32x64 accumulators
+  f32x4 acc16[8][8];  // 16x16x128 accumulators
+
+  // Quarter (qi, qj): the wave's rows 64qi.. x columns 64qj.. (32x32x64:
+  // blocks i in {2qi, 2qi+1} x j in {2qj, 2qj+1}, K-half major so the two
+  // MFMA of one accumulator are 4 apart; 16x16x128: 4 x 4 blocks).
+  auto quarter_mfma = [&](int qi, int qj, int from, int to) {
+    if constexpr (k16) {
+#pragma unroll
+      for (int n = from; n < to; ++n) {
+        const int i = 4 * qi + n / 4, j = 4 * qj + n % 4;
+        acc16[i][j] = mfma_16x16x128(fb16[j], fa16[i], acc16[i][j]);
+      }
+      return;
+    }
+#pragma unroll
+    for (int n = from; n < to; ++n) {
+      const int kh = n / 4, i = 2 * qi + (n / 2) % 2, j = 2 * qj + n % 2;
+      acc[i][j] = mfma_32x32x64(fb[j][kh], fa[i][kh], acc[i][j]);
+    }
+  };
+  using QS = QuarterShape<kMf>;
+  // The last quarter-step's tail (issued after the K loop, before the
+  // epilogue reads the accumulators).
+  auto last_tail = [&]() { quarter_mfma(1, 1, QS::kHead, QS::kMfma); };
+
+  // Two pipeline steps kt0, kt0 + 1 (stages 0, 1).  kFirst: the tile's first
+  // two steps, whose first seven quarter-steps wait past the previous tile's
+  // epilogue stores.
+  auto step_pair = [&](int kt0, auto first) {
+    constexpr bool kFirst = decltype(first)::value;
+    constexpr int w_std = kFirst ? kWaitAfterStores : kWaitSteady;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int kt = kt0 + s;
+      // The first quarter-step of a tile has no previous tail: the previous
+      // tile's was issued before its epilogue.
+      const bool tail = !(kFirst && s == 0);
+      wait_lgkmcnt<0>();
+      wait_vmcnt<w_std>();
+      barrier();  // Q00
+      if (tail) quarter_mfma(1, 1, QS::kHead, QS::kMfma);
+      quarter_mfma(0, 0, 0, QS::kHead);
+      read_tile(1, 1, s);
+      dma_group(kt + 2, s, 1, 0);
+      quarter_schedule<kMf>(tail);
+      wait_lgkmcnt<0>();
+      wait_vmcnt<w_std>();
+      barrier();  // Q01
+      quarter_mfma(0, 0, QS::kHead, QS::kMfma);
+      quarter_mfma(0, 1, 0, QS::kHead);
+      read_tile(0, 1, s);
+      dma_group(kt + 2, s, 1, 1);
+      quarter_schedule<kMf>(true);
+      wait_lgkmcnt<0>();
+      wait_vmcnt<w_std>();
+      barrier();  // Q10
+      quarter_mfma(0, 1, QS::kHead, QS::kMfma);
+      quarter_mfma(1, 0, 0, QS::kHead);
+      read_tile(0, 0, s ^ 1);
+      dma_group(kt + 2, s, 0, 1);
+      quarter_schedule<kMf>(true);
+      wait_lgkmcnt<0>();
+      if (kFirst && s == 0)
+        wait_vmcnt<kWaitAfterStores>();
+      else
+        wait_vmcnt<kWaitSteady>();
+      barrier();  // Q11
+      quarter_mfma(1, 0, QS::kHead, QS::kMfma);
+      quarter_mfma(1, 1, 0, QS::kHead);
+      read_tile(1, 0, s ^ 1);
+      dma_group(kt + 3, s ^ 1, 0, 0);
+      quarter_schedule<kMf>(true);
+    }
+  };
+
+  // Prologue of the first tile: steps 0 and 1 in group order A_lo, B_lo,
+  // B_hi, A_hi; a_lo(0), b_lo(0) into registers; the A_lo group of step 2;
+  // then every DMA landed, so the relaxed waits of the first steps hold.
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    dma_group(st, st, 0, 0);
+    dma_group(st, st, 1, 0);
+    dma_group(st, st, 1, 1);
+    dma_group(st, st, 0, 1);
+  }
+  wait_vmcnt<kWaitSteady>();
+  barrier();
+  read_tile(0, 0, 0);
+  read_tile(1, 0, 0);
+  wait_lgkmcnt<0>();
+  barrier();
+  dma_group(2, 0, 0, 0);
+  wait_vmcnt<0>();
+  barrier();
+
+  // Lane-derived epilogue values hang off an opaque copy of the lane id so
+  // the optimiser cannot hoist them out of the tile loop, where they would
+  // stay live through the K loop and spill.
+  for (;;) {
+    if constexpr (k16) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc16[i][j] = f32x4{};
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+    }
+
+    step_pair(0, std::true_type{});
+    for (int kt0 = 2; kt0 < kt_pad; kt0 += 2) step_pair(kt0, std::false_type{});
+
+    last_tail();
+    sched_fence();
 
     // ---- epilogue --------------------------------------------------------
+    // The accumulators are read by explicit v_accvgpr_read (acc_read), which
+    // the compiler's hazard tracking does not see: give the last MFMA its
+    // result latency first.
+    mfma_drain();
     // acc[i][j] holds D = B_blk . A_blk^T, i.e. C^T for the 32x32 block:
     // lane l, register r -> C row (l % 32), C column 8*(r/4) + 4*(l/32) + r%4,
     // so each lane holds 4 consecutive bf16 (8 bytes) per (i, j, r/4).
@@ -291,15 +439,13 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     auto oob_unless = [](int x, int limit) -> uint32_t {
       return (uint32_t)((limit - 1 - x) >> 31) & kOobOffset;
     };
+    int elane = lane;
+    asm volatile("" : "+v"(elane));
+    const TileCoord tc = grouped_tile(t, tiles_m, tiles_n, g.group_m);
+    const int rows_c = min(Cfg::kBM, M - tc.m * Cfg::kBM);
     // Every store is a buffer store over this tile's window of C; a lane
     // whose row or columns fall outside M x N gets an out-of-range offset and
     // its write is dropped by the hardware range check -- no branches.
-    // Lane-derived epilogue values hang off an opaque copy of the lane id so
-    // the optimiser cannot hoist them out of the tile loop, where they would
-    // stay live through the K loop and spill.
-    int elane = lane;
-    asm volatile("" : "+v"(elane));
-    const int rows_c = min(Cfg::kBM, M - tc.m * Cfg::kBM);
     const __amdgpu_buffer_rsrc_t rsrc_c = make_rsrc(
         g.C + (size_t)tc.m * Cfg::kBM * g.ldc + (size_t)tc.n * Cfg::kBN,
         (uint32_t)(((rows_c - 1) * g.ldc + Cfg::kBN) * 2));
@@ -307,86 +453,160 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     const int cols_left = N - tc.n * Cfg::kBN - wn * 128;  // from wave col 0
 
     if constexpr (kVecStore) {
-      // Through LDS: each wave stages its 128 x 128 bf16 quadrant (32 KiB) in
-      // its own quarter of the now idle stage buffers, then stores 16 bytes
-      // per lane row-major -- 4 rows x 256 B per instruction, whole 128-byte
-      // lines.  Staging layout: row r at 256 r, 16-byte chunk k of the row
-      // at slot k ^ (r % 16): conflict-free for the 8-byte writes (16 rows,
-      // one chunk) and for the 16-byte reads (one row, 16 chunks).
-      wait_vmcnt<0>();   // no DMA (real or padding) still landing in LDS
-      barrier();         // every wave is done reading the stages
-      lds_u8* stage_c = lds + wave * (128 * 256);
-      const uint32_t wlane = (elane & 31) * 256 + 8 * (elane >> 5);
-      const uint32_t xr16 = (elane & 15) * 16;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            lds_write8(stage_c + wlane + 32 * i * 256 + (((4 * j + q) * 16) ^ xr16),
-                       cvt4(acc[i][j], q));
-          sched_fence();  // bound the live range: one block at a time
-        }
-      wait_lgkmcnt<0>();  // own quadrant only: no cross-wave hand-off
-      // read: lane l takes row 4p + l/16, chunk l % 16
+      // 32 rows (one accumulator block row i) at a time through the wave's
+      // own 8 KiB: row r at 256 r; the 8-byte piece x (0..31) of the row at
+      // slot x ^ r.  Writes: lanes 0-31 (one 8-byte piece each of rows
+      // 0-31) hit 32 distinct slots; reads (two 8-byte pieces per lane, 16
+      // lanes per row, two rows per 32 lanes) likewise -- no bank conflicts
+      // with 64 four-byte banks.  No barrier: the region is the wave's own,
+      // and one wave's LDS operations complete in order.
+      lds_u8* stg = lds + Cfg::kStoreBase + wave * Cfg::kStoreStage;
+      // read: store p (0..7) covers rows 4p + l/16, 16-byte chunk l % 16
       const int rsub = elane >> 4, chunk = elane & 15;
-      const uint32_t rlane_base = rsub * 256;
-      uint32_t rx[4];
-#pragma unroll
-      for (int x = 0; x < 4; ++x)
-        rx[x] = rlane_base + ((chunk ^ ((4 * x + rsub) & 15)) * 16);
       const uint32_t vcol = (uint32_t)((rsub * g.ldc + wn * 128 + 8 * chunk) * 2);
       const uint32_t col_oob = oob_unless(8 * chunk, cols_left);
+      auto store_chunk = [&](int i, const i32x4 (&v)[8]) {
 #pragma unroll
-      for (int p0 = 0; p0 < 32; p0 += 8) {
-        i32x4 v[8];
-#pragma unroll
-        for (int p = p0; p < p0 + 8; ++p)
-          v[p - p0] = lds_read16(stage_c + rx[p & 3] + 1024 * p);
-#pragma unroll
-        for (int p = p0; p < p0 + 8; ++p) {
-          int row4 = 4 * p;
+        for (int p = 0; p < 8; ++p) {
+          int row4 = 32 * i + 4 * p;
           asm volatile("" : "+s"(row4));  // recompute per store, never hoist
           const int srow =
               __builtin_amdgcn_readfirstlane((wm * 128 + row4) * g.ldc * 2);
           __builtin_amdgcn_raw_buffer_store_b128(
-              v[p - p0], rsrc_c,
-              vcol | col_oob | oob_unless(row4 + rsub, rows_left), srow, 0);
+              v[p], rsrc_c, vcol | col_oob | oob_unless(row4 + rsub, rows_left),
+              srow, 0);
         }
-        sched_fence();  // at most 8 rows (32 VGPRs) in flight
+      };
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        i32x4 v[8];
+        if constexpr (k16) {
+          // Blocks (2i + ii, j): lane l holds row 16 ii + l%16, 8-byte piece
+          // 4j + l/16; piece x of row r at 8-byte slot x ^ 2(r % 16).  A
+          // 16-byte chunk keeps its two halves in order (the XOR is even), so
+          // each lane reads its chunk k of row r with one ds_read_b128 at
+          // chunk k ^ (r % 16).  Writes: each half-wave covers 32 distinct
+          // slots; reads: each row's 16 lanes cover 16 distinct chunks.
+          const int wr = elane & 15, wg = elane >> 4;
+#pragma unroll
+          for (int ii = 0; ii < 2; ++ii) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const f32x4& a = acc16[2 * i + ii][j];
+              lds_write8(stg + (16 * ii + wr) * 256 + (((4 * j + wg) ^ (2 * wr)) * 8),
+                         u32x2{pack_bf16x2(acc_read(a[0]) * scale,
+                                           acc_read(a[1]) * scale),
+                               pack_bf16x2(acc_read(a[2]) * scale,
+                                           acc_read(a[3]) * scale)});
+            }
+            sched_fence();  // bound the live range
+          }
+          compiler_fence();
+#pragma unroll
+          for (int p = 0; p < 8; ++p) {
+            const int r = 4 * p + rsub;
+            v[p] = lds_read16(stg + r * 256 + ((chunk ^ (r & 15)) * 16));
+          }
+        } else {
+          // 32 rows (one accumulator block row i) through the wave's own
+          // 8 KiB: row r at 256 r; the 8-byte piece x (0..31) of the row at
+          // slot x ^ r.  Writes: lanes 0-31 (one 8-byte piece each of rows
+          // 0-31) hit 32 distinct slots; reads (two 8-byte pieces per lane,
+          // 16 lanes per row, two rows per 32 lanes) likewise -- no bank
+          // conflicts with 64 four-byte banks.
+          const int wr = elane & 31, wh = elane >> 5;
+          const uint32_t wbase = wr * 256;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              lds_write8(stg + wbase + (((2 * (4 * j + q) + wh) ^ wr) * 8),
+                         cvt4(acc[i][j], q));
+            sched_fence();  // bound the live range: one block at a time
+          }
+          compiler_fence();
+#pragma unroll
+          for (int p = 0; p < 8; ++p) {
+            const int r = 4 * p + rsub;
+            const u32x2 lo = lds_read8(stg + r * 256 + (((2 * chunk) ^ r) * 8));
+            const u32x2 hi = lds_read8(stg + r * 256 + (((2 * chunk + 1) ^ r) * 8));
+            v[p] = i32x4{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+          }
+        }
+        // all reads of the chunk first (above), then its 8 stores; no
+        // barrier: the region is the wave's own, and one wave's LDS
+        // operations complete in order
+        store_chunk(i, v);
+        compiler_fence();
+        sched_fence();
       }
     } else {
       // N, ldc or C's alignment rule out 16-byte stores: 2-byte stores
       // straight from the accumulators, lane masks as out-of-range offsets.
-      const uint32_t vlane =
-          (uint32_t)(((elane & 31) * g.ldc + wn * 128 + 4 * (elane >> 5)) * 2);
+      if constexpr (k16) {
+        // block (i, j): lane l -> row 16 i + l%16, columns 16 j + 4(l/16) + r
+        const uint32_t vlane =
+            (uint32_t)(((elane & 15) * g.ldc + wn * 128 + 4 * (elane >> 4)) * 2);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int srow =
-            __builtin_amdgcn_readfirstlane((wm * 128 + 32 * i) * g.ldc * 2);
-        const uint32_t vrow = vlane | oob_unless(32 * i + (elane & 31), rows_left);
+        for (int i = 0; i < 8; ++i) {
+          const int srow =
+              __builtin_amdgcn_readfirstlane((wm * 128 + 16 * i) * g.ldc * 2);
+          const uint32_t vrow =
+              vlane | oob_unless(16 * i + (elane & 15), rows_left);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int c = 32 * j + 8 * q + 4 * (elane >> 5);
-            const u32x2 v = cvt4(acc[i][j], q);
+          for (int j = 0; j < 8; ++j) {
+            const int c = 16 * j + 4 * (elane >> 4);
+            const f32x4& a = acc16[i][j];
+            const u32x2 v{pack_bf16x2(acc_read(a[0]) * scale, acc_read(a[1]) * scale),
+                          pack_bf16x2(acc_read(a[2]) * scale, acc_read(a[3]) * scale)};
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const uint32_t w = (r < 2 ? v.x : v.y) >> (16 * (r & 1));
               __builtin_amdgcn_raw_buffer_store_b16(
                   (unsigned short)w, rsrc_c,
-                  (vrow | oob_unless(c + r, cols_left)) +
-                      (32 * j + 8 * q + r) * 2,
+                  (vrow | oob_unless(c + r, cols_left)) + (16 * j + r) * 2,
                   srow, 0);
             }
+            sched_fence();  // bound the live range: one block at a time
           }
-          sched_fence();  // bound the live range: one block at a time
+        }
+      } else {
+        const uint32_t vlane =
+            (uint32_t)(((elane & 31) * g.ldc + wn * 128 + 4 * (elane >> 5)) * 2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int srow =
+              __builtin_amdgcn_readfirstlane((wm * 128 + 32 * i) * g.ldc * 2);
+          const uint32_t vrow = vlane | oob_unless(32 * i + (elane & 31), rows_left);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int c = 32 * j + 8 * q + 4 * (elane >> 5);
+              const u32x2 v = cvt4(acc[i][j], q);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const uint32_t w = (r < 2 ? v.x : v.y) >> (16 * (r & 1));
+                __builtin_amdgcn_raw_buffer_store_b16(
+                    (unsigned short)w, rsrc_c,
+                    (vrow | oob_unless(c + r, cols_left)) +
+                        (32 * j + 8 * q + r) * 2,
+                    srow, 0);
+              }
+            }
+            sched_fence();  // bound the live range: one block at a time
+          }
         }
       }
     }
+
+    t += workers;
+    if (t >= tiles) break;
+    cur = nxt;
+    nxt = tile_src(g, t + workers, tiles, tiles_m, tiles_n);
   }
+  // The last tile's look-ahead DMA (all zeros) still lands in LDS: let it
+  // finish before the workgroup's LDS can be handed to another workgroup.
   wait_vmcnt<0>();
 }
 

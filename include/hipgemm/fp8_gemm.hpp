@@ -15,9 +15,10 @@
 //     contiguous), C M x N row-major bf16, fp32 accumulation.
 //
 // Behavioural differences, all on inputs where the reference is wrong or
-// undefined: any grid size >= 1 is correct (the kernel loops over 256 x 256
-// tiles), M and N need not be multiples of 256, and K only needs to be a
-// multiple of 16 (16-byte rows for the vector loads).  Output rounding is
+// undefined: any grid size >= 1 is correct (the first min(grid, 256)
+// workgroups loop over the 256 x 256 tiles, the rest return at once), M and
+// N need not be multiples of 256, and K only needs to be a multiple of 16
+// (16-byte rows for the vector loads).  Output rounding is
 // round-to-nearest-even (the reference kernel truncates, fp8_4wave.hpp:214;
 // the reference's CPU check rounds to nearest even, test.cpp:27).
 //
@@ -56,8 +57,9 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4wave_256x256x128(
                       K,
                       K,
                       N,
-                      default_group_m(tiles_m, tiles_n)};
+                      default_group_m(tiles_m, tiles_n),
+                      Cfg4w::kDropinWorkers};
   // 16-byte epilogue stores: N a multiple of 8 (C itself must be 16-byte
   // aligned, as every hipMalloc'd buffer is).
-  gemm_4wave_body<N % 8 == 0>(args, (lds_u8*)lds);
+  gemm_4wave_body<N % 8 == 0, 16>(args, (lds_u8*)lds);
 }

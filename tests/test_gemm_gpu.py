@@ -25,6 +25,14 @@ pytestmark = pytest.mark.gpu
 
 CANARY = 0x7FA5  # a NaN bit pattern no epilogue produces
 
+# Both MFMA shapes of the 4-wave schedule (include/hipgemm.h variants).
+SCHEDULES = [pytest.param(1, id="mfma32"), pytest.param(2, id="mfma16")]
+
+
+@pytest.fixture(params=SCHEDULES)
+def variant(request):
+    return request.param
+
 
 def gen(oracle, M, N, K, seed, dist, p0, p1):
     return (oracle.fill((M, K), 1000 * seed + 1, dist, p0, p1),
@@ -95,37 +103,37 @@ def sample_rows(M, seed, n=256):
 
 # ------------------------------------------------------ BASELINE configs ---
 
-def test_config1_512_uniform(gpu, oracle):
+def test_config1_512_uniform(gpu, oracle, variant):
     M = N = K = 512
-    say(f"case config1 M=N=K={M} U[-1,1] seed=1 scale=1")
+    say(f"case [v{variant}] config1 M=N=K={M} U[-1,1] seed=1 scale=1")
     A, B = gen(oracle, M, N, K, 1, po.UNIFORM, -1.0, 1.0)
-    C = run_gpu(gpu, A, B)
+    C = run_gpu(gpu, A, B, variant=variant)
     check_full(oracle, C, A, B, None, None)
 
 
-def test_config1_512_ternary_bit_exact(gpu, oracle):
+def test_config1_512_ternary_bit_exact(gpu, oracle, variant):
     M = N = K = 512
-    say(f"case config1-ternary M=N=K={M} seed=101")
+    say(f"case [v{variant}] config1-ternary M=N=K={M} seed=101")
     A, B = gen_ternary(M, N, K, 101)
-    C = run_gpu(gpu, A, B)
+    C = run_gpu(gpu, A, B, variant=variant)
     check_full(oracle, C, A, B, None, None, exact=True)
 
 
-def test_config2_4096_normal_scaled(gpu, oracle):
+def test_config2_4096_normal_scaled(gpu, oracle, variant):
     M = N = K = 4096
     sa, sb = oracle.draw_scale(21), oracle.draw_scale(22)
-    say(f"case config2 M=N=K={M} N(0,1) seed=2 sa={sa} sb={sb}")
+    say(f"case [v{variant}] config2 M=N=K={M} N(0,1) seed=2 sa={sa} sb={sb}")
     A, B = gen(oracle, M, N, K, 2, po.NORMAL, 0.0, 1.0)
-    C = run_gpu(gpu, A, B, sa, sb)
+    C = run_gpu(gpu, A, B, sa, sb, variant=variant)
     check_full(oracle, C, A, B, sa, sb)
 
 
-def test_config3_8192_normal_scaled(gpu, oracle):
+def test_config3_8192_normal_scaled(gpu, oracle, variant):
     M = N = K = 8192
     sa, sb = oracle.draw_scale(31), oracle.draw_scale(32)
-    say(f"case config3 M=N=K={M} N(0,1) seed=3 sa={sa} sb={sb}")
+    say(f"case [v{variant}] config3 M=N=K={M} N(0,1) seed=3 sa={sa} sb={sb}")
     A, B = gen(oracle, M, N, K, 3, po.NORMAL, 0.0, 1.0)
-    C = run_gpu(gpu, A, B, sa, sb)
+    C = run_gpu(gpu, A, B, sa, sb, variant=variant)
     check_full(oracle, C, A, B, sa, sb)
 
 
@@ -141,10 +149,10 @@ def test_config4_llm_shapes(gpu, oracle, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(16, 8192, 8192), (128, 8192, 8192),
                                    (4000, 5000, 3584)])
-def test_config5_skinny_and_ragged(gpu, oracle, M, N, K):
-    say(f"case config5 M={M} N={N} K={K} U[-1,1] seed=5")
+def test_config5_skinny_and_ragged(gpu, oracle, M, N, K, variant):
+    say(f"case [v{variant}] config5 M={M} N={N} K={K} U[-1,1] seed=5")
     A, B = gen(oracle, M, N, K, 5, po.UNIFORM, -1.0, 1.0)
-    C = run_gpu(gpu, A, B)
+    C = run_gpu(gpu, A, B, variant=variant)
     check_full(oracle, C, A, B, None, None)
 
 
@@ -153,10 +161,10 @@ def test_config5_skinny_and_ragged(gpu, oracle, M, N, K):
 @pytest.mark.parametrize("M,N,K", [(300, 260, 208), (1, 1, 16), (257, 255, 80),
                                    (17, 513, 48), (513, 17, 1040),
                                    (256, 256, 16), (4000, 5000, 64)])
-def test_canaries_no_write_outside(gpu, oracle, M, N, K):
+def test_canaries_no_write_outside(gpu, oracle, M, N, K, variant):
     """C lives inside a larger buffer (2 guard rows above and below, 24 guard
     columns right); every guard element must keep its canary bit-exactly."""
-    say(f"case canary M={M} N={N} K={K} seed=6")
+    say(f"case [v{variant}] canary M={M} N={N} K={K} seed=6")
     torch = gpu
     A, B = gen_ternary(M, N, K, 6)
     ldc = N + 24
@@ -165,7 +173,7 @@ def test_canaries_no_write_outside(gpu, oracle, M, N, K):
     a, b = to_dev(torch, A), to_dev(torch, B)
     base = dev.data_ptr() + 2 * ldc * 2
     code = hg.gemm_raw(a.data_ptr(), b.data_ptr(), base, M, N, K, K, K, ldc,
-                       0, 0, 0, torch.cuda.current_stream().cuda_stream)
+                       0, 0, variant, torch.cuda.current_stream().cuda_stream)
     assert code == 0
     torch.cuda.synchronize()
     got = dev.cpu().numpy().view(np.uint16)
@@ -176,22 +184,37 @@ def test_canaries_no_write_outside(gpu, oracle, M, N, K):
 
 
 @pytest.mark.parametrize("K", [16, 32, 48, 64, 80, 112, 144, 208, 272, 4112])
-def test_k_tails(gpu, oracle, K):
+def test_k_tails(gpu, oracle, K, variant):
     M, N = 260, 300
-    say(f"case ktail M={M} N={N} K={K} seed=7")
+    say(f"case [v{variant}] ktail M={M} N={N} K={K} seed=7")
     A, B = gen_ternary(M, N, K, 7)
-    C = run_gpu(gpu, A, B, 1.5, 0.5)
+    C = run_gpu(gpu, A, B, 1.5, 0.5, variant=variant)
     check_full(oracle, C, A, B, 1.5, 0.5, exact=True)
     A, B = gen(oracle, M, N, K, 7, po.UNIFORM, -1.0, 1.0)
-    C = run_gpu(gpu, A, B, 1.5, 0.5)
+    C = run_gpu(gpu, A, B, 1.5, 0.5, variant=variant)
     check_full(oracle, C, A, B, 1.5, 0.5)
 
 
-def test_strided_operands(gpu, oracle):
+@pytest.mark.parametrize("N,K", [(4352, 272), (4350, 144), (4352, 1040),
+                                 (4350, 16)])
+def test_persistent_multi_tile(gpu, oracle, N, K, variant):
+    """More tiles (17 x 17 = 289) than CUs, so workgroups run a second tile
+    whose first steps were prefetched by the first tile's last steps, with
+    the first tile's stores in flight.  Odd step counts (272, 1040 -> 3, 9
+    steps) add an all-zero padding step; N = 4350 takes the 2-byte-store
+    epilogue.  Ternary inputs: bit-exact."""
+    M = 4352
+    say(f"case [v{variant}] persistent M={M} N={N} K={K} seed=13")
+    A, B = gen_ternary(M, N, K, 13)
+    C = run_gpu(gpu, A, B, 0.5, 2.0, variant=variant)
+    check_full(oracle, C, A, B, 0.5, 2.0, exact=True)
+
+
+def test_strided_operands(gpu, oracle, variant):
     """lda, ldb > K with garbage in the padding: padding must never be read."""
     torch = gpu
     M, N, K, lda, ldb = 300, 200, 96, 160, 128
-    say(f"case strided M={M} N={N} K={K} lda={lda} ldb={ldb}")
+    say(f"case [v{variant}] strided M={M} N={N} K={K} lda={lda} ldb={ldb}")
     A, B = gen_ternary(M, N, K, 8)
     Ap = np.full((M, lda), 0x7F, np.uint8)  # NaN padding
     Bp = np.full((N, ldb), 0x7F, np.uint8)
@@ -199,7 +222,7 @@ def test_strided_operands(gpu, oracle):
     a, b = to_dev(torch, Ap), to_dev(torch, Bp)
     out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     code = hg.gemm_raw(a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K,
-                       lda, ldb, N, 0, 0, 0,
+                       lda, ldb, N, 0, 0, variant,
                        torch.cuda.current_stream().cuda_stream)
     assert code == 0
     torch.cuda.synchronize()
@@ -217,37 +240,37 @@ def test_k_zero_writes_zero(gpu):
     assert torch.count_nonzero(out).item() == 0
 
 
-def test_closed_forms_permutation_and_ones(gpu, oracle):
+def test_closed_forms_permutation_and_ones(gpu, oracle, variant):
     torch = gpu
     K, N = 512, 384
-    say(f"case closed-forms K={K} N={N}")
+    say(f"case [v{variant}] closed-forms K={K} N={N}")
     B = oracle.fill((N, K), 91, po.NORMAL, 0.0, 1.0)
     rng = np.random.default_rng(9)
     perm = rng.permutation(K)[:300]
     A = np.zeros((300, K), np.uint8)
     A[np.arange(300), perm] = 0x38
-    C = run_gpu(torch, A, B)
+    C = run_gpu(torch, A, B, variant=variant)
     # C rows are exact columns of B (a sum that starts at +0 turns -0 into +0)
     want = oracle.f32_to_bf16(oracle.e4m3_to_f32(B)[:, perm].T + np.float32(0))
     assert np.array_equal(want, oracle.gemm(A, B))
     assert np.array_equal(C, want)
     ones = np.full((33, K), 0x38, np.uint8)
     Bu = gen_ternary(N, 1, K, 92)[0]
-    C = run_gpu(torch, ones, Bu)
+    C = run_gpu(torch, ones, Bu, variant=variant)
     sums = oracle.e4m3_to_f32(Bu).astype(np.float64).sum(axis=1)
     assert np.array_equal(C, np.tile(oracle.f32_to_bf16(sums.astype(np.float32)),
                                      (33, 1)))
 
 
-def test_nan_and_saturation(gpu, oracle):
+def test_nan_and_saturation(gpu, oracle, variant):
     torch = gpu
     K = 256
-    say(f"case nan-sat K={K}")
+    say(f"case [v{variant}] nan-sat K={K}")
     A = np.full((260, K), 0x7E, np.uint8)
     B = np.full((300, K), 0xFE, np.uint8)  # -448
     A[5, 17] = 0x7F
     B[299, 0] = 0xFF
-    C = run_gpu(torch, A, B)
+    C = run_gpu(torch, A, B, variant=variant)
     want = oracle.gemm(A, B)
     nan = np.isnan(bf16_to_f32(C))
     assert np.array_equal(nan, np.isnan(bf16_to_f32(want)))
@@ -255,13 +278,13 @@ def test_nan_and_saturation(gpu, oracle):
     assert np.array_equal(C[~nan], want[~nan])
 
 
-def test_scales_bit_exact_on_exact_sums(gpu, oracle):
+def test_scales_bit_exact_on_exact_sums(gpu, oracle, variant):
     torch = gpu
     M, N, K = 512, 512, 256
-    say("case scales-exact")
+    say(f"case [v{variant}] scales-exact")
     A, B = gen_ternary(M, N, K, 10)
     for sa, sb in ((2.0, 0.25), (0.75, 1.3), (-1.0, 3.0), (1.0, None)):
-        C = run_gpu(torch, A, B, sa, sb)
+        C = run_gpu(torch, A, B, sa, sb, variant=variant)
         want = oracle.gemm(A, B, sa, 1.0 if sb is None else sb)
         assert np.array_equal(C, want), (sa, sb)
 
@@ -294,12 +317,29 @@ def test_dropin_entry_matches(gpu, oracle):
     check_full(oracle, from_dev_bf16(c), A, B, None, None, exact=True)
 
 
-def test_repeat_deterministic(gpu, oracle):
+def test_reference_harness_on_dropin_header(gpu):
+    """The reference's own test.cpp (4096^3, its RNG, its CPU gemm_cpu and its
+    1% check), compiled unchanged against include/fp8_4wave.hpp into
+    oracle/_ref/dropin_test_4096 by `make -C oracle ref`; it launches the
+    drop-in template exactly as the reference does (test.cpp:79)."""
+    import os
+    import subprocess
+    exe = os.path.join(os.path.dirname(po.__file__), "_ref", "dropin_test_4096")
+    if not os.path.exists(exe):
+        pytest.skip("oracle/_ref/dropin_test_4096 not built")
+    say("case reference-harness dropin_test_4096")
+    out = subprocess.run([exe], capture_output=True, text=True, timeout=240)
+    say("    " + out.stdout.strip().splitlines()[-1] if out.stdout else "")
+    assert out.returncode == 0, out.stderr[-2000:]
+    assert "Test passed: 1" in out.stdout
+
+
+def test_repeat_deterministic(gpu, oracle, variant):
     torch = gpu
     M = N = K = 2048
-    say("case determinism 2048^3 x3")
+    say(f"case [v{variant}] determinism 2048^3 x3")
     A, B = gen(oracle, M, N, K, 12, po.NORMAL, 0.0, 1.0)
     a, b = to_dev(torch, A), to_dev(torch, B)
-    outs = [from_dev_bf16(hg.fp8_gemm_bf16(a, b)) for _ in range(3)]
+    outs = [from_dev_bf16(hg.fp8_gemm_bf16(a, b, variant=variant)) for _ in range(3)]
     torch.cuda.synchronize()
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
