@@ -29,7 +29,7 @@ __all__ = [
     "HipGemmError", "lib", "lib_path", "fp8_gemm_bf16", "fp8_gemm",
     "fp8_gemm_4wave_256x256x128", "gemm_raw", "select_variant",
     "variant_name", "version", "tile_order", "lds_slot", "VARIANTS",
-    "declared_symbols",
+    "declared_symbols", "gemm_raw_ws", "workspace_size",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -37,7 +37,7 @@ _ROOT = os.path.dirname(_HERE)
 _LIB_PATH = os.path.join(_HERE, "libhipgemm.so")
 _HEADER = os.path.join(_ROOT, "include", "hipgemm.h")
 
-VARIANTS = {"auto": 0, "4wave": 1, "4wave_mfma16": 2}
+VARIANTS = {"auto": 0, "4wave": 1, "4wave_mfma16": 2, "skinny": 3}
 
 hipSuccess = 0
 hipErrorInvalidValue = 1
@@ -75,6 +75,12 @@ def lib() -> ctypes.CDLL:
     L.hipgemm_fp8_gemm_bf16.argtypes = [vp, vp, vp, ci, ci, ci, ci, ci, ci,
                                         vp, vp, ci, vp]
     L.hipgemm_fp8_gemm_bf16.restype = ci
+    L.hipgemm_fp8_gemm_bf16_ws.argtypes = [vp, vp, vp, ci, ci, ci, ci, ci,
+                                           ci, vp, vp, ci, vp, ctypes.c_size_t,
+                                           vp]
+    L.hipgemm_fp8_gemm_bf16_ws.restype = ci
+    L.hipgemm_workspace_size.argtypes = [ci, ci, ci, ci]
+    L.hipgemm_workspace_size.restype = ctypes.c_size_t
     L.hipgemm_fp8_gemm_4wave_256x256x128.argtypes = [vp, vp, vp, ci, ci, ci,
                                                      vp]
     L.hipgemm_fp8_gemm_4wave_256x256x128.restype = ci
@@ -112,6 +118,22 @@ def gemm_raw(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int,
     return int(lib().hipgemm_fp8_gemm_bf16(
         a_ptr or None, b_ptr or None, c_ptr or None, M, N, K, lda, ldb, ldc,
         scale_a_ptr or None, scale_b_ptr or None, variant, stream or None))
+
+
+def gemm_raw_ws(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int,
+                lda: int, ldb: int, ldc: int, scale_a_ptr: int, scale_b_ptr: int,
+                variant: int, ws_ptr: int, ws_bytes: int,
+                stream: int = 0) -> int:
+    """Call hipgemm_fp8_gemm_bf16_ws on raw device pointers."""
+    return int(lib().hipgemm_fp8_gemm_bf16_ws(
+        a_ptr or None, b_ptr or None, c_ptr or None, M, N, K, lda, ldb, ldc,
+        scale_a_ptr or None, scale_b_ptr or None, variant, ws_ptr or None,
+        ws_bytes, stream or None))
+
+
+def workspace_size(M: int, N: int, K: int, variant: int = 0) -> int:
+    """Workspace bytes hipgemm_fp8_gemm_bf16_ws needs (0 = none)."""
+    return int(lib().hipgemm_workspace_size(M, N, K, variant))
 
 
 def select_variant(M: int, N: int, K: int) -> int:
@@ -208,12 +230,32 @@ def fp8_gemm_bf16(a, b_t, scale_a=None, scale_b=None, out=None,
     lda = a.stride(0) if (M > 1 and K > 0) else max(K, 16)
     ldb = b_t.stride(0) if (N > 1 and K > 0) else max(K, 16)
     ldc = out.stride(0) if M > 1 else max(N, 1)
-    code = gemm_raw(a.data_ptr(), b_t.data_ptr(), out.data_ptr(), M, N, K,
-                    lda, ldb, ldc, _scale_ptr(scale_a, "scale_a"),
-                    _scale_ptr(scale_b, "scale_b"), variant,
-                    stream.cuda_stream)
-    _check(code, "hipgemm_fp8_gemm_bf16")
+    nbytes = workspace_size(M, N, K, variant) if M > 0 and N > 0 else 0
+    ws = _workspace(a.device, stream, nbytes) if nbytes else None
+    code = gemm_raw_ws(a.data_ptr(), b_t.data_ptr(), out.data_ptr(), M, N, K,
+                       lda, ldb, ldc, _scale_ptr(scale_a, "scale_a"),
+                       _scale_ptr(scale_b, "scale_b"), variant,
+                       ws.data_ptr() if ws is not None else 0, nbytes,
+                       stream.cuda_stream)
+    _check(code, "hipgemm_fp8_gemm_bf16_ws")
     return out
+
+
+# Zero-filled workspaces for the split-K schedule, one per (device, stream):
+# calls on one stream are ordered, so they may share one; every call leaves
+# it zero-filled again.
+_workspaces: dict = {}
+
+
+def _workspace(device, stream, nbytes: int):
+    torch = _torch()
+    key = (device.index, stream.cuda_stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        with torch.cuda.stream(stream):
+            ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
 
 
 fp8_gemm = fp8_gemm_bf16

@@ -8,6 +8,7 @@
 #include <atomic>
 #include <cstdint>
 
+#include "hipgemm/detail/gemm_skinny.hpp"
 #include "hipgemm/fp8_gemm.hpp"
 
 namespace {
@@ -18,6 +19,11 @@ template <bool kVecStore, int kMf>
 __global__ __launch_bounds__(256, 1) void k_fp8_gemm_4wave(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg4w::kLdsBytes];
   gemm_4wave_body<kVecStore, kMf>(g, (lds_u8*)lds);
+}
+
+template <int kMB, bool kVec8>
+__global__ __launch_bounds__(256, 1) void k_fp8_gemm_skinny(SkinnyArgs g) {
+  gemm_skinny_body<kMB, kVec8>(g);
 }
 
 constexpr int kMaxLd = 1 << 23;  // 256 rows * ld (bytes) must stay below 2^31
@@ -84,27 +90,79 @@ hipError_t launch_4wave(GemmArgs g, hipStream_t stream) {
                          stream);
 }
 
-}  // namespace
+// Split-K plan of the skinny schedule: 16-row blocks of M, K-slices per
+// 256-column tile (enough workgroups to give every CU one), and the
+// workspace it needs (arrival counters, then the partial tiles).
+struct SkinnyPlan {
+  int kmb, tiles_n, slices, slice_steps;
+  size_t counter_bytes, ws_bytes;
+};
 
-extern "C" {
-
-int hipgemm_select_variant(int M, int N, int K) {
-  (void)M;
-  (void)N;
-  (void)K;
-  // 16x16x128 sustains a higher clock than 32x32x64 under the power limit
-  // that caps long GEMMs on MI355X (same work per step).
-  return HIPGEMM_VARIANT_4WAVE_MFMA16;
+SkinnyPlan plan_skinny(int M, int N, int K) {
+  SkinnyPlan p{};
+  p.kmb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+  p.tiles_n = (N + CfgSkinny::kBN - 1) / CfgSkinny::kBN;
+  const int steps = (K + CfgSkinny::kBK - 1) / CfgSkinny::kBK;
+  const int target = cu_count();
+  int slices = (target + p.tiles_n - 1) / p.tiles_n;
+  if (slices > steps) slices = steps;
+  if (slices < 1) slices = 1;
+  p.slice_steps = steps > 0 ? (steps + slices - 1) / slices : 0;
+  p.slices = p.slice_steps > 0 ? (steps + p.slice_steps - 1) / p.slice_steps : 1;
+  if (p.slices > 1) {
+    p.counter_bytes = ((size_t)p.tiles_n * sizeof(int) + 255) / 256 * 256;
+    p.ws_bytes = p.counter_bytes + (size_t)p.tiles_n * p.slices * p.kmb * 16 *
+                                       CfgSkinny::kBN * sizeof(float);
+  }
+  return p;
 }
 
-hipError_t hipgemm_fp8_gemm_bf16(const void* A, const void* B_T, void* C,
-                                 int M, int N, int K, int lda, int ldb,
-                                 int ldc, const float* scale_a,
-                                 const float* scale_b, int variant,
-                                 hipStream_t stream) {
+template <int kMB>
+hipError_t launch_skinny_mb(const SkinnyArgs& g, bool vec8, int grid,
+                            hipStream_t stream) {
+  void* args[] = {const_cast<SkinnyArgs*>(&g)};
+  const void* fn =
+      vec8 ? reinterpret_cast<const void*>(&k_fp8_gemm_skinny<kMB, true>)
+           : reinterpret_cast<const void*>(&k_fp8_gemm_skinny<kMB, false>);
+  return hipLaunchKernel(fn, dim3(grid), dim3(CfgSkinny::kThreads), args, 0,
+                         stream);
+}
+
+hipError_t launch_skinny(const GemmArgs& a, const SkinnyPlan& p, void* ws,
+                         hipStream_t stream) {
+  SkinnyArgs g{a.A, a.B, a.C, a.scale_a, a.scale_b, a.M, a.N, a.K,
+               a.lda, a.ldb, a.ldc, p.slices, p.slice_steps, nullptr, nullptr};
+  if (p.slices > 1) {
+    g.arrivals = static_cast<int*>(ws);
+    g.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + p.counter_bytes);
+  }
+  const bool vec8 = (a.N % 4 == 0) && (a.ldc % 4 == 0) && aligned(a.C, 8);
+  const int grid = p.tiles_n * p.slices;
+  switch (p.kmb) {
+    case 1: return launch_skinny_mb<1>(g, vec8, grid, stream);
+    case 2: return launch_skinny_mb<2>(g, vec8, grid, stream);
+    case 4: return launch_skinny_mb<4>(g, vec8, grid, stream);
+    default: return launch_skinny_mb<8>(g, vec8, grid, stream);
+  }
+}
+
+int resolve_variant(int variant, int M, int N, int K);
+
+// Shared body of the two GEMM entry points.  `ws` may be null when
+// `ws_given` is false: a schedule that needs a workspace then takes a
+// stream-ordered allocation for the call.
+hipError_t run_gemm(const void* A, const void* B_T, void* C, int M, int N,
+                    int K, int lda, int ldb, int ldc, const float* scale_a,
+                    const float* scale_b, int variant, bool ws_given, void* ws,
+                    size_t ws_bytes, hipStream_t stream) {
   hipError_t e = validate(A, B_T, C, M, N, K, lda, ldb, ldc, variant);
-  if (e != hipSuccess || M == 0 || N == 0) return e;
-  if (variant == HIPGEMM_VARIANT_AUTO) variant = hipgemm_select_variant(M, N, K);
+  if (e != hipSuccess) return e;
+  if (variant == HIPGEMM_VARIANT_SKINNY && M > CfgSkinny::kMaxM)
+    return hipErrorInvalidValue;
+  if (ws_given && ws_bytes > 0 && (!ws || !aligned(ws, 256)))
+    return hipErrorInvalidValue;
+  if (M == 0 || N == 0) return hipSuccess;
+  variant = resolve_variant(variant, M, N, K);
   if (K == 0) lda = ldb = 16;  // nothing is read; keep the offset math inert
   const int tiles_m = (M + Cfg4w::kBM - 1) / Cfg4w::kBM;
   const int tiles_n = (N + Cfg4w::kBN - 1) / Cfg4w::kBN;
@@ -122,12 +180,72 @@ hipError_t hipgemm_fp8_gemm_bf16(const void* A, const void* B_T, void* C,
              default_group_m(tiles_m, tiles_n),
              0};
   switch (variant) {
+    case HIPGEMM_VARIANT_SKINNY: {
+      const SkinnyPlan p = plan_skinny(M, N, K);
+      if (p.ws_bytes == 0) return launch_skinny(g, p, nullptr, stream);
+      if (ws_given) {
+        if (ws_bytes < p.ws_bytes) return hipErrorInvalidValue;
+        return launch_skinny(g, p, ws, stream);
+      }
+      void* tmp = nullptr;
+      if ((e = hipMallocAsync(&tmp, p.ws_bytes, stream)) != hipSuccess) return e;
+      e = hipMemsetAsync(tmp, 0, p.counter_bytes, stream);
+      if (e == hipSuccess) e = launch_skinny(g, p, tmp, stream);
+      const hipError_t f = hipFreeAsync(tmp, stream);
+      return e != hipSuccess ? e : f;
+    }
     case HIPGEMM_VARIANT_4WAVE_MFMA16:
       return launch_4wave<16>(g, stream);
     case HIPGEMM_VARIANT_4WAVE:
     default:
       return launch_4wave<32>(g, stream);
   }
+}
+
+int resolve_variant(int variant, int M, int N, int K) {
+  return variant == HIPGEMM_VARIANT_AUTO ? hipgemm_select_variant(M, N, K)
+                                         : variant;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hipgemm_select_variant(int M, int N, int K) {
+  (void)N;
+  (void)K;
+  // Up to 128 rows the GEMM is a stream over B_T: the split-K schedule
+  // spreads it over every CU.  Above, 16x16x128 sustains a higher clock
+  // than 32x32x64 under the power limit that caps long GEMMs on MI355X
+  // (same work per step).
+  if (M <= CfgSkinny::kMaxM) return HIPGEMM_VARIANT_SKINNY;
+  return HIPGEMM_VARIANT_4WAVE_MFMA16;
+}
+
+hipError_t hipgemm_fp8_gemm_bf16(const void* A, const void* B_T, void* C,
+                                 int M, int N, int K, int lda, int ldb,
+                                 int ldc, const float* scale_a,
+                                 const float* scale_b, int variant,
+                                 hipStream_t stream) {
+  return run_gemm(A, B_T, C, M, N, K, lda, ldb, ldc, scale_a, scale_b, variant,
+                  false, nullptr, 0, stream);
+}
+
+hipError_t hipgemm_fp8_gemm_bf16_ws(const void* A, const void* B_T, void* C,
+                                    int M, int N, int K, int lda, int ldb,
+                                    int ldc, const float* scale_a,
+                                    const float* scale_b, int variant,
+                                    void* workspace, size_t workspace_bytes,
+                                    hipStream_t stream) {
+  return run_gemm(A, B_T, C, M, N, K, lda, ldb, ldc, scale_a, scale_b, variant,
+                  true, workspace, workspace_bytes, stream);
+}
+
+size_t hipgemm_workspace_size(int M, int N, int K, int variant) {
+  if (M <= 0 || N <= 0 || K < 0) return 0;
+  if (resolve_variant(variant, M, N, K) != HIPGEMM_VARIANT_SKINNY) return 0;
+  if (M > CfgSkinny::kMaxM) return 0;
+  return plan_skinny(M, N, K).ws_bytes;
 }
 
 hipError_t hipgemm_fp8_gemm_4wave_256x256x128(const void* A, const void* B_T,
@@ -145,6 +263,8 @@ const char* hipgemm_variant_name(int variant) {
       return "4wave_256x256x128_mfma32";
     case HIPGEMM_VARIANT_4WAVE_MFMA16:
       return "4wave_256x256x128_mfma16";
+    case HIPGEMM_VARIANT_SKINNY:
+      return "skinny_splitk_256";
     default:
       return nullptr;
   }

@@ -52,7 +52,12 @@ enum {
   /* The same schedule on v_mfma_f32_16x16x128_f8f6f4.  AUTO's choice, and
    * the schedule behind the drop-in template. */
   HIPGEMM_VARIANT_4WAVE_MFMA16 = 2,
-  HIPGEMM_VARIANT_COUNT = 3
+  /* M <= 128 only: split-K over every CU for the HBM-bound skinny shapes,
+   * operands streamed straight into registers, a deterministic in-kernel
+   * reduction of the K-slices.  AUTO's choice for M <= 128.  Needs a
+   * workspace (hipgemm_workspace_size) when it splits K. */
+  HIPGEMM_VARIANT_SKINNY = 3,
+  HIPGEMM_VARIANT_COUNT = 4
 };
 
 /*
@@ -67,6 +72,31 @@ hipError_t hipgemm_fp8_gemm_bf16(const void *A, const void *B_T, void *C,
                                  int ldc, const float *scale_a,
                                  const float *scale_b, int variant,
                                  hipStream_t stream);
+
+/*
+ * hipgemm_fp8_gemm_bf16 with a caller-provided workspace.  A schedule that
+ * needs scratch memory (hipgemm_workspace_size(M, N, K, variant) > 0: the
+ * skinny split-K schedule keeps its per-tile arrival counters and fp32
+ * partial tiles there) uses `workspace` instead of taking a stream-ordered
+ * allocation (hipMallocAsync / hipFreeAsync) on `stream` for the call, as
+ * hipgemm_fp8_gemm_bf16 does.  The workspace must be 256-byte aligned,
+ * zero-filled before its first use, and at least that size; every call
+ * leaves it zero-filled again.  Calls that may run concurrently must not
+ * share a workspace.  Returns hipErrorInvalidValue if it is missing or too
+ * small when needed.
+ * Replaces: the same reference launch (the reference has no workspace and no
+ * split-K path).
+ */
+hipError_t hipgemm_fp8_gemm_bf16_ws(const void *A, const void *B_T, void *C,
+                                    int M, int N, int K, int lda, int ldb,
+                                    int ldc, const float *scale_a,
+                                    const float *scale_b, int variant,
+                                    void *workspace, size_t workspace_bytes,
+                                    hipStream_t stream);
+
+/* Workspace bytes hipgemm_fp8_gemm_bf16_ws needs for this shape and variant
+ * on the current device (0: none).  No GPU work.  No reference counterpart. */
+size_t hipgemm_workspace_size(int M, int N, int K, int variant);
 
 /*
  * The reference launch with runtime shapes: packed strides (lda = ldb = K,

@@ -1,0 +1,263 @@
+// hipgemm -- split-K FP8 GEMM for skinny M (gfx950).
+//
+// C[M x N] (bf16) = scale_a * scale_b * A[M x K] . B_T[N x K]^T for M <= 128,
+// where the work is reading B_T once from HBM (16 x 8192 x 8192 moves 64 MiB
+// of B_T against 2 GFLOP).  No reference counterpart: the reference kernel
+// (fp8_4wave.hpp:334-567) is only valid for M a multiple of 256.
+//
+// Decomposition: workgroup (n, s) of a (tiles_n x slices) grid computes the
+// fp32 partial C[0:M, 256n : 256n + 256] over K-slice s (`slice_steps` steps
+// of 128).  Slices make the grid fill the GPU although tiles_n is small.
+//   * Wave w owns columns 64w .. 64w + 63 of the tile as 4 x kMB blocks of
+//     16 x 16 (v_mfma_f32_16x16x128_f8f6f4, one per block per step).
+//   * No LDS: every wave streams its 64 B_T rows and the (at most 128) A
+//     rows straight into registers with buffer_load_dwordx4, up to three
+//     steps ahead.  A lane holds, for its row, the K-bytes
+//     16g .. 16g + 15 and 64 + 16g .. 64 + 16g + 15 of each 128-byte step
+//     (g = lane / 16): any K order is valid as long as A and B_T use the
+//     same one, and this one makes each load instruction read 64 contiguous
+//     bytes of each of 16 rows.
+//   * Every slice stores its partial tile (fp32, 16 bytes per lane, whole
+//     1 KiB per instruction) into the workspace, then bumps the tile's
+//     arrival counter (a relaxed agent-scope atomic).  The workgroup that
+//     arrives last sums the slices in slice order 0, 1, ... (so the result
+//     does not depend on arrival order), applies the scales, writes bf16 C
+//     and resets the counter to zero for the next call.
+//
+// Buffer resources cover only the valid rows of A and B_T, and K-pieces past
+// the slice end read zero, so nothing outside A or B_T is addressed; C is
+// written through a buffer resource over its M x N window with out-of-range
+// offsets for lanes outside it.
+#pragma once
+
+#include "arch.hpp"
+
+namespace hipgemm {
+namespace detail {
+
+struct SkinnyArgs {
+  const uint8_t* A;      // M x K e4m3, row stride lda bytes
+  const uint8_t* B;      // N x K e4m3 (B_T), row stride ldb bytes
+  uint16_t* C;           // M x N bf16, row stride ldc elements
+  const float* scale_a;  // device scalar, nullptr = 1.0
+  const float* scale_b;  // device scalar, nullptr = 1.0
+  int M, N, K;
+  int lda, ldb, ldc;
+  int slices;       // K-slices per column tile (grid = tiles_n * slices)
+  int slice_steps;  // 128-byte K-steps per slice
+  float* partial;   // tiles_n * slices * kMB * 16 * 256 floats
+  int* arrivals;    // tiles_n counters, zero between calls
+};
+
+struct CfgSkinny {
+  static constexpr int kThreads = 256;
+  static constexpr int kBN = 256, kBK = 128;
+  static constexpr int kMaxM = 128;
+  // Floats of one slice's partial tile.
+  template <int kMB>
+  static constexpr int partial_floats() { return kMB * 16 * kBN; }
+};
+
+// kMB: 16-row blocks of M (M <= 16 kMB).  kVec8: C rows allow 8-byte stores
+// (N % 4 == 0, ldc % 4 == 0, C 8-byte aligned).
+template <int kMB, bool kVec8>
+__device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
+  using Cfg = CfgSkinny;
+  // Register sets: kDepth - 1 steps of loads stay in flight per wave (the
+  // whole GPU's worth of in-flight loads is about half of a 64 MiB B_T, so
+  // the look-ahead is as deep as the registers allow).
+  constexpr int kDepth = kMB <= 2 ? 4 : kMB <= 4 ? 3 : 2;
+  constexpr int kLoads = 8 + 2 * kMB;  // buffer loads per wave per step
+  static_assert((kDepth - 1) * kLoads < 64, "vmcnt range");
+  const int lane = lane_id();
+  const int wave = wave_id();
+  const int M = g.M, N = g.N, K = g.K;
+  const int tiles_n = (N + Cfg::kBN - 1) / Cfg::kBN;
+  const int nt = blockIdx.x % tiles_n;
+  const int s = blockIdx.x / tiles_n;
+  const int k_begin = s * g.slice_steps * Cfg::kBK;
+  const int k_end = min(K, k_begin + g.slice_steps * Cfg::kBK);
+  const int steps = (k_end - k_begin + Cfg::kBK - 1) / Cfg::kBK;
+  const int steps_pad = (steps + kDepth - 1) / kDepth * kDepth;
+
+  const int n0 = nt * Cfg::kBN;
+  const int rows_b = min(Cfg::kBN, N - n0);
+  const __amdgpu_buffer_rsrc_t rsrc_a =
+      make_rsrc(g.A, (uint32_t)M * (uint32_t)g.lda);
+  const __amdgpu_buffer_rsrc_t rsrc_b =
+      make_rsrc(g.B + (size_t)n0 * g.ldb, (uint32_t)rows_b * (uint32_t)g.ldb);
+
+  const int r16 = lane & 15, grp = lane >> 4;
+  // Lane row offsets: B_T rows 64w + 16f + r16 (f = 0..3), A rows 16m + r16.
+  uint32_t voff_b[4], voff_a[kMB];
+#pragma unroll
+  for (int f = 0; f < 4; ++f)
+    voff_b[f] = (uint32_t)(wave * 64 + 16 * f + r16) * (uint32_t)g.ldb + 16 * grp;
+#pragma unroll
+  for (int m = 0; m < kMB; ++m)
+    voff_a[m] = (uint32_t)(16 * m + r16) * (uint32_t)g.lda + 16 * grp;
+
+  i32x4 bq[kDepth][4][2], aq[kDepth][kMB][2];
+  // Loads of step kb into register set d; pieces past the slice end read 0.
+  auto load_step = [&](int kb, int d) {
+    uint32_t k0 = (uint32_t)(k_begin + kb * Cfg::kBK);
+    asm volatile("" : "+s"(k0));
+    const int lim = k_end - (int)k0;  // bytes of this step inside the slice
+    const uint32_t oob0 = (16 * grp < lim) ? 0u : kOobOffset;
+    const uint32_t oob1 = (64 + 16 * grp < lim) ? 0u : kOobOffset;
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      bq[d][f][0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_b, voff_b[f] | oob0, k0, 0);
+      bq[d][f][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_b, voff_b[f] | oob1, k0 + 64, 0);
+    }
+#pragma unroll
+    for (int m = 0; m < kMB; ++m) {
+      aq[d][m][0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a[m] | oob0, k0, 0);
+      aq[d][m][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a[m] | oob1, k0 + 64, 0);
+    }
+  };
+
+  f32x4 acc[kMB][4];
+#pragma unroll
+  for (int m = 0; m < kMB; ++m)
+#pragma unroll
+    for (int f = 0; f < 4; ++f) acc[m][f] = f32x4{};
+
+  auto mfma_step = [&](int d) {
+#pragma unroll
+    for (int m = 0; m < kMB; ++m)
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+        acc[m][f] = mfma_16x16x128(join(bq[d][f][0], bq[d][f][1]),
+                                   join(aq[d][m][0], aq[d][m][1]), acc[m][f]);
+  };
+
+#pragma unroll
+  for (int d = 0; d < kDepth - 1; ++d) load_step(d, d);
+  for (int k0 = 0; k0 < steps_pad; k0 += kDepth) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+      load_step(k0 + d + kDepth - 1, (d + kDepth - 1) % kDepth);
+      wait_vmcnt<(kDepth - 1) * kLoads>();  // step k0 + d landed
+      mfma_step(d);
+    }
+  }
+  wait_vmcnt<0>();  // the last look-ahead loads (zeros) are done with
+  mfma_drain();
+
+  // ---- partial tile out, arrival count ------------------------------------
+  // Partial tiles cross XCDs, whose L2s are not coherent with each other:
+  // they are stored with sc1 (written through to the coherent level) and
+  // read back with sc1 (fetched from there), which needs no L2 write-back or
+  // invalidate.  The counter is a relaxed agent-scope atomic; ordering comes
+  // from waiting for the stores' completion (vmcnt 0) in every wave before
+  // the workgroup barrier that precedes the increment.
+  constexpr int kCoherent = 16;  // cache policy: sc1
+  const int tile_floats = Cfg::partial_floats<kMB>();
+  const __amdgpu_buffer_rsrc_t rsrc_p = make_rsrc(
+      g.partial + (size_t)nt * g.slices * tile_floats,
+      (uint32_t)(g.slices * tile_floats * sizeof(float)));
+  // layout: float4 (m, f, wave, lane) at byte ((m*4 + f)*256 + 64 w + l)*16
+  auto slot = [&](int m, int f) {
+    return (uint32_t)(((m * 4 + f) * Cfg::kThreads + wave * 64 + lane) * 16);
+  };
+  const uint32_t mine = (uint32_t)(s * tile_floats * sizeof(float));
+  __shared__ int last;
+  if (g.slices > 1) {
+#pragma unroll
+    for (int m = 0; m < kMB; ++m)
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const f32x4 v{acc_read(acc[m][f][0]), acc_read(acc[m][f][1]),
+                      acc_read(acc[m][f][2]), acc_read(acc[m][f][3])};
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(i32x4, v), rsrc_p, slot(m, f), mine, kCoherent);
+      }
+    wait_vmcnt<0>();
+    barrier();
+    if (threadIdx.x == 0) {
+      const int before = __hip_atomic_fetch_add(
+          g.arrivals + nt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = before == g.slices - 1;
+    }
+    barrier();
+    if (!last) return;
+  }
+
+  // ---- last arrival: sum the slices in order, scale, bf16, store ----------
+  const float sa = g.scale_a ? *g.scale_a : 1.0f;
+  const float sb = g.scale_b ? *g.scale_b : 1.0f;
+  const float scale = sa * sb;
+  const __amdgpu_buffer_rsrc_t rsrc_c =
+      make_rsrc(g.C + n0, (uint32_t)(((M - 1) * g.ldc + rows_b) * 2));
+  auto oob_unless = [](int x, int limit) -> uint32_t {
+    return (uint32_t)((limit - 1 - x) >> 31) & kOobOffset;
+  };
+  // Sums over the slices, in slice order; the loads of kBatch slices (all
+  // kMB x 4 blocks each, 32 loads) are issued before any is consumed.
+  constexpr int kBatch = 8 / kMB;
+  f32x4 sum[kMB][4];
+#pragma unroll
+  for (int m = 0; m < kMB; ++m)
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+      sum[m][f] = g.slices > 1
+                      ? f32x4{}
+                      : f32x4{acc_read(acc[m][f][0]), acc_read(acc[m][f][1]),
+                              acc_read(acc[m][f][2]), acc_read(acc[m][f][3])};
+  if (g.slices > 1) {
+    const uint32_t stride = (uint32_t)(tile_floats * sizeof(float));
+    for (int q0 = 0; q0 < g.slices; q0 += kBatch) {
+      f32x4 v[kBatch][kMB][4];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+        for (int m = 0; m < kMB; ++m)
+#pragma unroll
+          for (int f = 0; f < 4; ++f)
+            v[u][m][f] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           rsrc_p, slot(m, f),
+                           (uint32_t)min(q0 + u, g.slices - 1) * stride,
+                           kCoherent));
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (q0 + u < g.slices)
+#pragma unroll
+          for (int m = 0; m < kMB; ++m)
+#pragma unroll
+            for (int f = 0; f < 4; ++f) sum[m][f] += v[u][m][f];
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < kMB; ++m)
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      // D = B_blk . A_blk^T: lane l, element i -> C row 16m + l%16,
+      // column 64w + 16f + 4(l/16) + i (4 consecutive columns).
+      const int row = 16 * m + r16;
+      const int col = wave * 64 + 16 * f + 4 * grp;
+      const uint32_t base = (uint32_t)((row * g.ldc + col) * 2) |
+                            oob_unless(row, M);
+      const uint32_t lo = pack_bf16x2(sum[m][f][0] * scale, sum[m][f][1] * scale);
+      const uint32_t hi = pack_bf16x2(sum[m][f][2] * scale, sum[m][f][3] * scale);
+      if constexpr (kVec8) {
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc_c,
+                                              base | oob_unless(col, rows_b), 0, 0);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t w = (i < 2 ? lo : hi) >> (16 * (i & 1));
+          __builtin_amdgcn_raw_buffer_store_b16(
+              (unsigned short)w, rsrc_c,
+              (base | oob_unless(col + i, rows_b)) + 2 * i, 0, 0);
+        }
+      }
+    }
+  if (g.slices > 1 && threadIdx.x == 0)
+    __hip_atomic_store(g.arrivals + nt, 0, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace detail
+}  // namespace hipgemm

@@ -74,6 +74,29 @@ def test_k_zero_needs_only_c():
     assert hg.gemm_raw(0, 0, FAKE, 64, 64, 0, 0, 0, 63) == INVALID
 
 
+def test_workspace_size_and_validation():
+    """The split-K schedule (M <= 128) needs a workspace when it splits K;
+    the workspace entry point rejects a missing, misaligned or short one
+    before launching anything."""
+    skinny = hg.VARIANTS["skinny"]
+    assert hg.select_variant(16, 8192, 8192) == skinny
+    assert hg.select_variant(129, 8192, 8192) != skinny
+    need = hg.workspace_size(16, 8192, 8192, 0)
+    assert need > 0 and need % 256 == 0
+    assert hg.workspace_size(16, 8192, 8192, skinny) == need
+    assert hg.workspace_size(512, 8192, 8192, 0) == 0   # 4-wave: none
+    assert hg.workspace_size(16, 300, 64, 0) == 0       # one K-step: no split
+    assert hg.workspace_size(0, 8192, 8192, 0) == 0
+    args = (FAKE, FAKE, FAKE, 16, 8192, 8192, 8192, 8192, 8192, 0, 0)
+    assert hg.gemm_raw_ws(*args, 0, 0, need) == INVALID          # no workspace
+    assert hg.gemm_raw_ws(*args, 0, FAKE, need - 256) == INVALID  # too small
+    assert hg.gemm_raw_ws(*args, 0, FAKE + 64, need) == INVALID   # misaligned
+    assert hg.gemm_raw_ws(*args[:3], 129, *args[4:], skinny, FAKE,
+                          need) == INVALID                       # M > 128
+    assert hg.gemm_raw_ws(0, 0, 0, 0, 8192, 8192, 8192, 8192, 8192, 0, 0, 0,
+                          0, 0) == 0                             # empty: no-op
+
+
 def test_dropin_entry_validates_too():
     L = hg.lib()
     assert L.hipgemm_fp8_gemm_4wave_256x256x128(None, None, None, 64, 64, 64,
