@@ -21,7 +21,8 @@ from util import say
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(8192, 8192, 8192), (4096, 4096, 4096)]
+SHAPES = [(8192, 8192, 8192), (4096, 4096, 4096), (8192, 28672, 8192),
+          (8192, 8192, 28672)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
