@@ -26,6 +26,12 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm_skinny(SkinnyArgs g) {
   gemm_skinny_body<kMB, kVec8>(g);
 }
 
+template <bool kVec8>
+__global__ __launch_bounds__(256, 1) void k_fp8_gemm_skinny_reduce(SkinnyArgs g,
+                                                                    int kmb) {
+  gemm_skinny_reduce_body<kVec8>(g, kmb);
+}
+
 constexpr int kMaxLd = 1 << 23;  // 256 rows * ld (bytes) must stay below 2^31
 
 bool aligned(const void* p, uintptr_t a) {
@@ -130,20 +136,34 @@ hipError_t launch_skinny_mb(const SkinnyArgs& g, bool vec8, int grid,
 
 hipError_t launch_skinny(const GemmArgs& a, const SkinnyPlan& p, void* ws,
                          hipStream_t stream) {
+  // From 4 row blocks up, one workgroup per column tile summing every slice
+  // (1 MiB of partials per tile at M = 128) is the long pole: a second
+  // kernel sums them over tiles_n x kmb workgroups instead.
+  const int reduce_pass = p.slices > 1 && p.kmb >= 4;
   SkinnyArgs g{a.A, a.B, a.C, a.scale_a, a.scale_b, a.M, a.N, a.K,
-               a.lda, a.ldb, a.ldc, p.slices, p.slice_steps, nullptr, nullptr};
+               a.lda, a.ldb, a.ldc, p.slices, p.slice_steps, nullptr, nullptr,
+               reduce_pass};
   if (p.slices > 1) {
     g.arrivals = static_cast<int*>(ws);
     g.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + p.counter_bytes);
   }
   const bool vec8 = (a.N % 4 == 0) && (a.ldc % 4 == 0) && aligned(a.C, 8);
   const int grid = p.tiles_n * p.slices;
+  hipError_t e;
   switch (p.kmb) {
-    case 1: return launch_skinny_mb<1>(g, vec8, grid, stream);
-    case 2: return launch_skinny_mb<2>(g, vec8, grid, stream);
-    case 4: return launch_skinny_mb<4>(g, vec8, grid, stream);
-    default: return launch_skinny_mb<8>(g, vec8, grid, stream);
+    case 1: e = launch_skinny_mb<1>(g, vec8, grid, stream); break;
+    case 2: e = launch_skinny_mb<2>(g, vec8, grid, stream); break;
+    case 4: e = launch_skinny_mb<4>(g, vec8, grid, stream); break;
+    default: e = launch_skinny_mb<8>(g, vec8, grid, stream); break;
   }
+  if (e != hipSuccess || !reduce_pass) return e;
+  int kmb = p.kmb;
+  void* args[] = {&g, &kmb};
+  const void* fn =
+      vec8 ? reinterpret_cast<const void*>(&k_fp8_gemm_skinny_reduce<true>)
+           : reinterpret_cast<const void*>(&k_fp8_gemm_skinny_reduce<false>);
+  return hipLaunchKernel(fn, dim3(p.tiles_n * p.kmb), dim3(CfgSkinny::kThreads),
+                         args, 0, stream);
 }
 
 int resolve_variant(int variant, int M, int N, int K);

@@ -10,9 +10,9 @@
 // of 128).  Slices make the grid fill the GPU although tiles_n is small.
 //   * Wave w owns columns 64w .. 64w + 63 of the tile as 4 x kMB blocks of
 //     16 x 16 (v_mfma_f32_16x16x128_f8f6f4, one per block per step).
-//   * No LDS: every wave streams its 64 B_T rows and the (at most 128) A
-//     rows straight into registers with buffer_load_dwordx4, up to three
-//     steps ahead.  A lane holds, for its row, the K-bytes
+//   * Every wave streams its 64 B_T rows straight into registers with
+//     buffer_load_dwordx4, three steps ahead; A (at most 128 rows) too for
+//     M <= 32, else the workgroup stages A once per step through LDS.  A lane holds, for its row, the K-bytes
 //     16g .. 16g + 15 and 64 + 16g .. 64 + 16g + 15 of each 128-byte step
 //     (g = lane / 16): any K order is valid as long as A and B_T use the
 //     same one, and this one makes each load instruction read 64 contiguous
@@ -31,6 +31,7 @@
 #pragma once
 
 #include "arch.hpp"
+#include "layout.hpp"
 
 namespace hipgemm {
 namespace detail {
@@ -47,6 +48,7 @@ struct SkinnyArgs {
   int slice_steps;  // 128-byte K-steps per slice
   float* partial;   // tiles_n * slices * kMB * 16 * 256 floats
   int* arrivals;    // tiles_n counters, zero between calls
+  int reduce_pass;  // 1: a separate kernel sums the slices (no counters)
 };
 
 struct CfgSkinny {
@@ -63,11 +65,17 @@ struct CfgSkinny {
 template <int kMB, bool kVec8>
 __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   using Cfg = CfgSkinny;
-  // Register sets: kDepth - 1 steps of loads stay in flight per wave (the
-  // whole GPU's worth of in-flight loads is about half of a 64 MiB B_T, so
-  // the look-ahead is as deep as the registers allow).
-  constexpr int kDepth = kMB <= 2 ? 4 : kMB <= 4 ? 3 : 2;
-  constexpr int kLoads = 8 + 2 * kMB;  // buffer loads per wave per step
+  // A (at most 128 rows) is shared by the four waves: up to 32 rows each
+  // wave loads its own copy into registers; above, the workgroup stages it
+  // through LDS once (DMA, one barrier per step) so A costs no more HBM or
+  // L2 traffic than its share.
+  constexpr bool kLdsA = kMB >= 4;
+  // Register sets / LDS stages: kDepth - 1 steps of loads stay in flight per
+  // wave (the whole GPU's worth of in-flight loads is about half of a
+  // 64 MiB B_T, so the look-ahead is as deep as the registers allow).
+  constexpr int kDepth = kLdsA ? 4 : kMB <= 2 ? 4 : 3;
+  constexpr int kDmaA = kLdsA ? kMB / 2 : 0;  // A DMA per wave per step
+  constexpr int kLoads = kLdsA ? 8 + kDmaA : 8 + 2 * kMB;  // per wave per step
   static_assert((kDepth - 1) * kLoads < 64, "vmcnt range");
   const int lane = lane_id();
   const int wave = wave_id();
@@ -89,16 +97,37 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
 
   const int r16 = lane & 15, grp = lane >> 4;
   // Lane row offsets: B_T rows 64w + 16f + r16 (f = 0..3), A rows 16m + r16.
-  uint32_t voff_b[4], voff_a[kMB];
+  uint32_t voff_b[4], voff_a[kLdsA ? 1 : kMB];
 #pragma unroll
   for (int f = 0; f < 4; ++f)
     voff_b[f] = (uint32_t)(wave * 64 + 16 * f + r16) * (uint32_t)g.ldb + 16 * grp;
+  if constexpr (!kLdsA) {
 #pragma unroll
-  for (int m = 0; m < kMB; ++m)
-    voff_a[m] = (uint32_t)(16 * m + r16) * (uint32_t)g.lda + 16 * grp;
+    for (int m = 0; m < kMB; ++m)
+      voff_a[m] = (uint32_t)(16 * m + r16) * (uint32_t)g.lda + 16 * grp;
+  }
 
-  i32x4 bq[kDepth][4][2], aq[kDepth][kMB][2];
-  // Loads of step kb into register set d; pieces past the slice end read 0.
+  // LDS A stages (kLdsA): BM rows x 128 B each, row r at 128 r, 16-byte slot
+  // x of the row holding K-chunk x ^ slot_xor(r) (conflict-free 16-row
+  // fragment reads).  DMA instruction q (8 rows) belongs to wave q % 4; its
+  // lane l fetches row 8q + l/8, chunk (l%8) ^ slot_xor(row) from global.
+  constexpr int kStageA = kMB * 16 * Cfg::kBK;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_a[kLdsA ? kDepth * kStageA : 16];
+  const int drow = lane >> 3;
+  uint32_t voff_dma[kDmaA > 0 ? kDmaA : 1];
+  if constexpr (kLdsA) {
+#pragma unroll
+    for (int i = 0; i < kDmaA; ++i) {
+      const int row = 8 * (4 * i + wave) + drow;
+      voff_dma[i] = (uint32_t)row * (uint32_t)g.lda +
+                    (uint32_t)(((lane & 7) ^ slot_xor(row & 15)) * 16);
+    }
+  }
+  const int sx16 = slot_xor(r16);
+
+  i32x4 bq[kDepth][4][2], aq[kLdsA ? 1 : kDepth][kMB][2];
+  // Loads of step kb into register set / LDS stage d; pieces past the slice
+  // end read 0.
   auto load_step = [&](int kb, int d) {
     uint32_t k0 = (uint32_t)(k_begin + kb * Cfg::kBK);
     asm volatile("" : "+s"(k0));
@@ -110,10 +139,22 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
       bq[d][f][0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_b, voff_b[f] | oob0, k0, 0);
       bq[d][f][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_b, voff_b[f] | oob1, k0 + 64, 0);
     }
+    if constexpr (kLdsA) {
+      const uint32_t oobd = (16 * ((lane & 7) ^ slot_xor((8 * wave + drow) & 15)) < lim)
+                                ? 0u : kOobOffset;
 #pragma unroll
-    for (int m = 0; m < kMB; ++m) {
-      aq[d][m][0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a[m] | oob0, k0, 0);
-      aq[d][m][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a[m] | oob1, k0 + 64, 0);
+      for (int i = 0; i < kDmaA; ++i) {
+        // rows 8(4i + w) + l/8: slot_xor depends on row % 16 = 8(w % 2) + l/8
+        dma16(rsrc_a,
+              (lds_u8*)lds_a + d * kStageA + (4 * i + wave) * 1024,
+              voff_dma[i] | oobd, k0);
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < kMB; ++m) {
+        aq[d][m][0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a[m] | oob0, k0, 0);
+        aq[d][m][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a[m] | oob1, k0 + 64, 0);
+      }
     }
   };
 
@@ -125,11 +166,19 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
 
   auto mfma_step = [&](int d) {
 #pragma unroll
-    for (int m = 0; m < kMB; ++m)
+    for (int m = 0; m < kMB; ++m) {
+      i32x8 a;
+      if constexpr (kLdsA) {
+        const lds_u8* row = (const lds_u8*)lds_a + d * kStageA + (16 * m + r16) * Cfg::kBK;
+        a = join(lds_read16(row + ((grp ^ sx16) * 16)),
+                 lds_read16(row + (((4 + grp) ^ sx16) * 16)));
+      } else {
+        a = join(aq[d][m][0], aq[d][m][1]);
+      }
 #pragma unroll
       for (int f = 0; f < 4; ++f)
-        acc[m][f] = mfma_16x16x128(join(bq[d][f][0], bq[d][f][1]),
-                                   join(aq[d][m][0], aq[d][m][1]), acc[m][f]);
+        acc[m][f] = mfma_16x16x128(join(bq[d][f][0], bq[d][f][1]), a, acc[m][f]);
+    }
   };
 
 #pragma unroll
@@ -137,8 +186,18 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   for (int k0 = 0; k0 < steps_pad; k0 += kDepth) {
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) {
-      load_step(k0 + d + kDepth - 1, (d + kDepth - 1) % kDepth);
-      wait_vmcnt<(kDepth - 1) * kLoads>();  // step k0 + d landed
+      if constexpr (kLdsA) {
+        // step k0 + d landed (own part), every wave's part landed and every
+        // wave done with the stage refilled below (the one step k0 + d - 1
+        // read); then the refill, then this step's A from LDS.
+        wait_vmcnt<(kDepth - 2) * kLoads>();
+        wait_lgkmcnt<0>();
+        barrier();
+        load_step(k0 + d + kDepth - 1, (d + kDepth - 1) % kDepth);
+      } else {
+        load_step(k0 + d + kDepth - 1, (d + kDepth - 1) % kDepth);
+        wait_vmcnt<(kDepth - 1) * kLoads>();  // step k0 + d landed
+      }
       mfma_step(d);
     }
   }
@@ -173,6 +232,7 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
         __builtin_amdgcn_raw_buffer_store_b128(
             __builtin_bit_cast(i32x4, v), rsrc_p, slot(m, f), mine, kCoherent);
       }
+    if (g.reduce_pass) return;
     wait_vmcnt<0>();
     barrier();
     if (threadIdx.x == 0) {
@@ -257,6 +317,81 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   if (g.slices > 1 && threadIdx.x == 0)
     __hip_atomic_store(g.arrivals + nt, 0, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Separate slice reduction (reduce_pass): workgroup (nt, m) sums 16-row
+// block m of column tile nt over the slices in slice order, applies the
+// scales and writes bf16 C -- the same arithmetic and the same C mapping as
+// the in-kernel reduction, spread over tiles_n x kMB workgroups instead of
+// one per tile.  Launched on the same stream right after the split kernel,
+// so its partial tiles are visible without any fence.
+template <bool kVec8>
+__device__ __forceinline__ void gemm_skinny_reduce_body(const SkinnyArgs& g,
+                                                        int kmb) {
+  using Cfg = CfgSkinny;
+  const int lane = lane_id();
+  const int wave = wave_id();
+  const int M = g.M, N = g.N;
+  const int tiles_n = (N + Cfg::kBN - 1) / Cfg::kBN;
+  const int nt = blockIdx.x % tiles_n;
+  const int m = blockIdx.x / tiles_n;
+  const int n0 = nt * Cfg::kBN;
+  const int rows_b = min(Cfg::kBN, N - n0);
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int tile_floats = kmb * 16 * Cfg::kBN;
+  const __amdgpu_buffer_rsrc_t rsrc_p = make_rsrc(
+      g.partial + (size_t)nt * g.slices * tile_floats,
+      (uint32_t)(g.slices * tile_floats * sizeof(float)));
+  const uint32_t stride = (uint32_t)(tile_floats * sizeof(float));
+  auto slot = [&](int f) {
+    return (uint32_t)(((m * 4 + f) * Cfg::kThreads + wave * 64 + lane) * 16);
+  };
+  constexpr int kBatch = 8;  // slices whose loads are in flight together
+  f32x4 sum[4] = {};
+  for (int q0 = 0; q0 < g.slices; q0 += kBatch) {
+    f32x4 v[kBatch][4];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+        v[u][f] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rsrc_p, slot(f),
+                       (uint32_t)min(q0 + u, g.slices - 1) * stride, 0));
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (q0 + u < g.slices)
+#pragma unroll
+        for (int f = 0; f < 4; ++f) sum[f] += v[u][f];
+  }
+  const float sa = g.scale_a ? *g.scale_a : 1.0f;
+  const float sb = g.scale_b ? *g.scale_b : 1.0f;
+  const float scale = sa * sb;
+  const __amdgpu_buffer_rsrc_t rsrc_c =
+      make_rsrc(g.C + n0, (uint32_t)(((M - 1) * g.ldc + rows_b) * 2));
+  auto oob_unless = [](int x, int limit) -> uint32_t {
+    return (uint32_t)((limit - 1 - x) >> 31) & kOobOffset;
+  };
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    const int row = 16 * m + r16;
+    const int col = wave * 64 + 16 * f + 4 * grp;
+    const uint32_t base = (uint32_t)((row * g.ldc + col) * 2) | oob_unless(row, M);
+    const uint32_t lo = pack_bf16x2(sum[f][0] * scale, sum[f][1] * scale);
+    const uint32_t hi = pack_bf16x2(sum[f][2] * scale, sum[f][3] * scale);
+    if constexpr (kVec8) {
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc_c,
+                                            base | oob_unless(col, rows_b), 0, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w = (i < 2 ? lo : hi) >> (16 * (i & 1));
+        __builtin_amdgcn_raw_buffer_store_b16(
+            (unsigned short)w, rsrc_c,
+            (base | oob_unless(col + i, rows_b)) + 2 * i, 0, 0);
+      }
+    }
+  }
 }
 
 }  // namespace detail
