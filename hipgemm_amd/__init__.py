@@ -37,7 +37,7 @@ _ROOT = os.path.dirname(_HERE)
 _LIB_PATH = os.path.join(_HERE, "libhipgemm.so")
 _HEADER = os.path.join(_ROOT, "include", "hipgemm.h")
 
-VARIANTS = {"auto": 0, "4wave": 1, "4wave_mfma16": 2, "skinny": 3}
+VARIANTS = {"auto": 0, "4wave": 1, "4wave_mfma16": 2, "skinny": 3, "8wave": 4}
 
 hipSuccess = 0
 hipErrorInvalidValue = 1

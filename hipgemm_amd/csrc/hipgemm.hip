@@ -8,6 +8,7 @@
 #include <atomic>
 #include <cstdint>
 
+#include "hipgemm/detail/gemm_8wave.hpp"
 #include "hipgemm/detail/gemm_skinny.hpp"
 #include "hipgemm/fp8_gemm.hpp"
 
@@ -21,6 +22,12 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm_4wave(GemmArgs g) {
   gemm_4wave_body<kVecStore, kMf>(g, (lds_u8*)lds);
 }
 
+template <bool kVecStore>
+__global__ __launch_bounds__(512, 1) void k_fp8_gemm_8wave(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg8w::kLdsBytes];
+  gemm_8wave_body<kVecStore>(g, (lds_u8*)lds);
+}
+
 template <int kMB, bool kVec8>
 __global__ __launch_bounds__(256, 1) void k_fp8_gemm_skinny(SkinnyArgs g) {
   gemm_skinny_body<kMB, kVec8>(g);
@@ -32,7 +39,10 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm_skinny_reduce(SkinnyArgs g,
   gemm_skinny_reduce_body<kVec8>(g, kmb);
 }
 
-constexpr int kMaxLd = 1 << 23;  // 256 rows * ld (bytes) must stay below 2^31
+// 32-bit buffer offsets: 256 rows of A or B_T (1-byte elements) span at most
+// 2^31 bytes, 256 rows of C (2-byte elements) likewise.
+constexpr int kMaxLd = 1 << 23;
+constexpr int kMaxLdc = 1 << 22;
 
 bool aligned(const void* p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
@@ -44,7 +54,7 @@ hipError_t validate(const void* A, const void* B_T, void* C, int M, int N,
   if (variant < 0 || variant >= HIPGEMM_VARIANT_COUNT)
     return hipErrorInvalidValue;
   if (M == 0 || N == 0) return hipSuccess;
-  if (!C || !aligned(C, 2) || ldc < N || ldc > kMaxLd)
+  if (!C || !aligned(C, 2) || ldc < N || ldc > kMaxLdc)
     return hipErrorInvalidValue;
   if (K == 0) return hipSuccess;  // A and B_T are not read
   if (!A || !B_T) return hipErrorInvalidValue;
@@ -94,6 +104,20 @@ hipError_t launch_4wave(GemmArgs g, hipStream_t stream) {
           : reinterpret_cast<const void*>(&k_fp8_gemm_4wave<false, kMf>);
   return hipLaunchKernel(fn, dim3(grid), dim3(Cfg4w::kThreads), args, 0,
                          stream);
+}
+
+hipError_t launch_8wave(GemmArgs g, hipStream_t stream) {
+  // Same persistent grid as the 4-wave kernel (160 KiB of LDS: one
+  // workgroup per CU).
+  const int tiles = tiles_of(g.M, g.N);
+  const int cus = cu_count();
+  const int grid = tiles < cus ? tiles : cus;
+  g.workers = grid;
+  const bool vec = (g.N % 8 == 0) && (g.ldc % 8 == 0) && aligned(g.C, 16);
+  void* args[] = {&g};
+  const void* fn = vec ? reinterpret_cast<const void*>(&k_fp8_gemm_8wave<true>)
+                       : reinterpret_cast<const void*>(&k_fp8_gemm_8wave<false>);
+  return hipLaunchKernel(fn, dim3(grid), dim3(Cfg8w::kThreads), args, 0, stream);
 }
 
 // Split-K plan of the skinny schedule: 16-row blocks of M, K-slices per
@@ -216,6 +240,8 @@ hipError_t run_gemm(const void* A, const void* B_T, void* C, int M, int N,
     }
     case HIPGEMM_VARIANT_4WAVE_MFMA16:
       return launch_4wave<16>(g, stream);
+    case HIPGEMM_VARIANT_8WAVE:
+      return launch_8wave(g, stream);
     case HIPGEMM_VARIANT_4WAVE:
     default:
       return launch_4wave<32>(g, stream);
@@ -285,6 +311,8 @@ const char* hipgemm_variant_name(int variant) {
       return "4wave_256x256x128_mfma16";
     case HIPGEMM_VARIANT_SKINNY:
       return "skinny_splitk_256";
+    case HIPGEMM_VARIANT_8WAVE:
+      return "8wave_256x256x128_mfma16";
     default:
       return nullptr;
   }

@@ -20,7 +20,7 @@
  * Errors: every entry point returns a hipError_t and never exits the
  * process.  Argument errors return hipErrorInvalidValue before any HIP call,
  * so they can be checked on a machine without a GPU.  Requirements:
- *   M, N, K >= 0;  C non-NULL, 2-byte aligned, N <= ldc <= 2^23;
+ *   M, N, K >= 0;  C non-NULL, 2-byte aligned, N <= ldc <= 2^22;
  *   A, B_T non-NULL and 16-byte aligned;  K % 16 == 0;
  *   lda >= K, ldb >= K, lda % 16 == 0, ldb % 16 == 0, lda, ldb <= 2^23.
  * M == 0 or N == 0 is a no-op (nothing is checked or written).  K == 0
@@ -57,7 +57,11 @@ enum {
    * reduction of the K-slices.  AUTO's choice for M <= 128.  Needs a
    * workspace (hipgemm_workspace_size) when it splits K. */
   HIPGEMM_VARIANT_SKINNY = 3,
-  HIPGEMM_VARIANT_COUNT = 4
+  /* 512 threads (8 waves, two per SIMD), 256 x 256 tile, each wave 128 x 64
+   * of it, 2 LDS stages, persistent grid, v_mfma_f32_16x16x128_f8f6f4.  The
+   * reference's kernels are 4-wave only; no reference counterpart. */
+  HIPGEMM_VARIANT_8WAVE = 4,
+  HIPGEMM_VARIANT_COUNT = 5
 };
 
 /*

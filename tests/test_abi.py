@@ -33,6 +33,9 @@ def test_version_and_variants():
     assert hg.variant_name(1).startswith("4wave")
     assert hg.variant_name(99) is None
     assert hg.variant_name(2).startswith("4wave")
+    assert hg.variant_name(3).startswith("skinny")
+    assert hg.variant_name(4).startswith("8wave")
+    assert hg.variant_name(5) is None
     assert hg.select_variant(8192, 8192, 8192) in (1, 2)
 
 
@@ -50,7 +53,7 @@ def test_version_and_variants():
     dict(B=FAKE + 4),                  # B_T not 16-byte aligned
     dict(C=FAKE + 1),                  # C not 2-byte aligned
     dict(lda=(1 << 23) + 16),          # lda too large for 32-bit offsets
-    dict(ldc=(1 << 23) + 4),           # ldc too large for 32-bit offsets
+    dict(ldc=(1 << 22) + 4),           # ldc too large for 32-bit offsets
     dict(variant=7), dict(variant=-1),
 ])
 def test_argument_validation(args):

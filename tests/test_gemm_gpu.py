@@ -25,8 +25,10 @@ pytestmark = pytest.mark.gpu
 
 CANARY = 0x7FA5  # a NaN bit pattern no epilogue produces
 
-# Both MFMA shapes of the 4-wave schedule (include/hipgemm.h variants).
-SCHEDULES = [pytest.param(1, id="mfma32"), pytest.param(2, id="mfma16")]
+# The tiled schedules of include/hipgemm.h: the 4-wave one on both MFMA
+# shapes, and the 8-wave one.
+SCHEDULES = [pytest.param(1, id="mfma32"), pytest.param(2, id="mfma16"),
+             pytest.param(4, id="8wave")]
 
 
 @pytest.fixture(params=SCHEDULES)
