@@ -11,9 +11,9 @@
 //     those: 8 x 4 blocks of 16 x 16, 128 AGPRs.  One step's operands (A 128
 //     rows + B 64 rows, 96 VGPRs) fit once per wave.
 //   * The groups alternate, half a step apart, between a memory phase (read
-//     the step's operands from LDS, then issue 8 DMAs of later steps) and a
-//     compute phase (32 MFMAs at raised wave priority, nothing else), every
-//     phase closed by one workgroup barrier.  Phase 2j: group 0 reads step j while group 1
+//     the step's operands from LDS, with 8 DMAs of later steps in between)
+//     and a compute phase (32 MFMAs at raised wave priority, nothing else),
+//     every phase closed by one workgroup barrier.  Phase 2j: group 0 reads step j while group 1
 //     computes step j - 1; phase 2j + 1: group 0 computes step j while group
 //     1 reads it.  Each SIMD's MFMA pipe thus alternates between its two
 //     waves and never waits for an LDS read.
@@ -149,40 +149,48 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
 
     int bs = 0;  // B stage of step j (j % 3)
     for (int j = 0; j < kt; ++j) {
-      // ---- memory phase of step j: LDS -> registers, then 8 DMAs ---------
-      {
-        const uint32_t pa = off_a + (j & 1) * Cfg::kAStage;
-        const uint32_t pb = off_b + bs * Cfg::kBStage;
-#pragma unroll
-        for (int f = 0; f < 8; ++f) {
-          const uint32_t p = pa + f * 16 * Cfg::kBK;
-          fa[f] = join(lds_read16(lds + p), lds_read16(lds + (p ^ 16u)));
+      // ---- memory phase of step j: LDS -> registers and 8 DMAs ------------
+      // Group 0: A rows 128-255 of step j + 1 (into the stage of step j - 1,
+      // last read by group 1 in phase 2j - 1) and B rows 128-255 of step
+      // j + 2.  Group 1: A rows 0-127 of step j + 2 (into the stage of step
+      // j, read by group 0 in phase 2j) and B rows 0-127 of step j + 2.  B
+      // of step j + 2 goes into the stage of step j - 1.  Steps past the end
+      // are fetched as zeros (out-of-range offsets, no memory traffic), which
+      // keeps every wait count exact.  One DMA after every 3 ds_reads: a
+      // wave issues in order, so alternating keeps both the LDS and the
+      // vector memory path busy instead of one after the other.
+      const uint32_t pa = off_a + (j & 1) * Cfg::kAStage;
+      const uint32_t pb = off_b + bs * Cfg::kBStage;
+      const int kba = grp == 0 ? j + 1 : j + 2, kbb = j + 2;
+      const bool oka = k_ok(kba), okb = k_ok(kbb);
+      const uint32_t dsta = grp == 0 ? a_stage(j + 1) : a_stage(j);
+      const uint32_t dstb = Cfg::kBBase + (bs == 0 ? 2 : bs - 1) * Cfg::kBStage;
+      const int q0 = (grp == 0 ? 16 : 0) + wn;
+      i32x4 ra[8][2], rb[4][2];
+      auto rd = [&](int k) {
+        if (k < 16) {
+          const uint32_t p = pa + (k / 2) * 16 * Cfg::kBK;
+          ra[k / 2][k % 2] = lds_read16(lds + ((k % 2) ? (p ^ 16u) : p));
+        } else {
+          const int kk = k - 16;
+          const uint32_t p = pb + (kk / 2) * 16 * Cfg::kBK;
+          rb[kk / 2][kk % 2] = lds_read16(lds + ((kk % 2) ? (p ^ 16u) : p));
         }
+      };
+      auto dm = [&](int s) {
+        if (s < 4) dma(0, dsta, q0 + 4 * s, kba, oka);
+        else dma(1, dstb, q0 + 4 * (s - 4), kbb, okb);
+      };
 #pragma unroll
-        for (int f = 0; f < 4; ++f) {
-          const uint32_t p = pb + f * 16 * Cfg::kBK;
-          fb[f] = join(lds_read16(lds + p), lds_read16(lds + (p ^ 16u)));
-        }
+      for (int s = 0; s < 8; ++s) {
+        rd(3 * s); rd(3 * s + 1); rd(3 * s + 2);
+        dm(s);
+        sched_fence();
       }
-      {
-        // Group 0: A rows 128-255 of step j + 1 (into the stage of step j - 1,
-        // last read by group 1 in phase 2j - 1) and B rows 128-255 of step
-        // j + 2.  Group 1: A rows 0-127 of step j + 2 (into the stage of step
-        // j, read by group 0 in phase 2j) and B rows 0-127 of step j + 2.  B
-        // of step j + 2 goes into the stage of step j - 1.  Steps past the
-        // end are fetched as zeros (out-of-range offsets, no memory traffic),
-        // which keeps every wait count exact.
-        const int kba = grp == 0 ? j + 1 : j + 2, kbb = j + 2;
-        const bool oka = k_ok(kba), okb = k_ok(kbb);
-        const uint32_t dsta = grp == 0 ? a_stage(j + 1) : a_stage(j);
-        const uint32_t dstb = Cfg::kBBase + (bs == 0 ? 2 : bs - 1) * Cfg::kBStage;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          dma(0, dsta, (grp == 0 ? 16 : 0) + wn + 4 * i, kba, oka);
+      for (int f = 0; f < 8; ++f) fa[f] = join(ra[f][0], ra[f][1]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          dma(1, dstb, (grp == 0 ? 16 : 0) + wn + 4 * i, kbb, okb);
-      }
+      for (int f = 0; f < 4; ++f) fb[f] = join(rb[f][0], rb[f][1]);
       wait_lgkmcnt<0>();
       // Group 0: its A rows of step j (issued in its previous memory phase)
       // landed for group 1's next phase; newer: B of step j + 1, then this
