@@ -261,11 +261,12 @@ int hipgemm_select_variant(int M, int N, int K) {
   (void)N;
   (void)K;
   // Up to 128 rows the GEMM is a stream over B_T: the split-K schedule
-  // spreads it over every CU.  Above, 16x16x128 sustains a higher clock
-  // than 32x32x64 under the power limit that caps long GEMMs on MI355X
-  // (same work per step).
+  // spreads it over every CU.  Above, the 8-wave ping-pong schedule: as fast
+  // as the 4-wave one at the long shapes (8192^3, 8192 x 28672 x 8192, K =
+  // 28672) and up to 1.16x on shapes with fewer steps per tile or fewer
+  // tiles than CUs, measured on MI355X in one process each.
   if (M <= CfgSkinny::kMaxM) return HIPGEMM_VARIANT_SKINNY;
-  return HIPGEMM_VARIANT_4WAVE_MFMA16;
+  return HIPGEMM_VARIANT_8WAVE;
 }
 
 hipError_t hipgemm_fp8_gemm_bf16(const void* A, const void* B_T, void* C,
@@ -329,7 +330,8 @@ int hipgemm_tile_order(int grid, int tiles_m, int tiles_n, int group_m,
   const int tiles = tiles_m * tiles_n;
   int w = 0;
   for (int b = 0; b < grid && w < cap; ++b) {
-    for (int t = xcd_contiguous(b, grid); t < tiles && w < cap; t += grid) {
+    const TileWalk walk = tile_walk(b, grid, tiles);
+    for (int t = walk.first; t < walk.end && w < cap; t += walk.stride) {
       const TileCoord tc = grouped_tile(t, tiles_m, tiles_n, group_m);
       tile_m[w] = tc.m;
       tile_n[w] = tc.n;

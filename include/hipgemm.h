@@ -49,17 +49,19 @@ enum {
   /* 256 threads (4 waves, one per SIMD), 256 x 256 tile, 2 LDS stages,
    * persistent grid, v_mfma_f32_32x32x64_f8f6f4. */
   HIPGEMM_VARIANT_4WAVE = 1,
-  /* The same schedule on v_mfma_f32_16x16x128_f8f6f4.  AUTO's choice, and
-   * the schedule behind the drop-in template. */
+  /* The same schedule on v_mfma_f32_16x16x128_f8f6f4: the schedule behind
+   * the drop-in template. */
   HIPGEMM_VARIANT_4WAVE_MFMA16 = 2,
   /* M <= 128 only: split-K over every CU for the HBM-bound skinny shapes,
    * operands streamed straight into registers, a deterministic in-kernel
    * reduction of the K-slices.  AUTO's choice for M <= 128.  Needs a
    * workspace (hipgemm_workspace_size) when it splits K. */
   HIPGEMM_VARIANT_SKINNY = 3,
-  /* 512 threads (8 waves, two per SIMD), 256 x 256 tile, each wave 128 x 64
-   * of it, 2 LDS stages, persistent grid, v_mfma_f32_16x16x128_f8f6f4.  The
-   * reference's kernels are 4-wave only; no reference counterpart. */
+  /* 512 threads (8 waves, two per SIMD, in two groups that alternate
+   * between LDS/DMA work and MFMAs), 256 x 256 tile, each wave 128 x 64 of
+   * it, persistent grid, v_mfma_f32_16x16x128_f8f6f4.  AUTO's choice for
+   * M > 128.  The reference's kernels are 4-wave only; no reference
+   * counterpart. */
   HIPGEMM_VARIANT_8WAVE = 4,
   HIPGEMM_VARIANT_COUNT = 5
 };

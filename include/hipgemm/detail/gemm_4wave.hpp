@@ -7,8 +7,9 @@
 // Work decomposition
 //   * One workgroup = 256 threads = 4 waves (one per SIMD).  The grid is
 //     persistent: `workers` workgroups (at most one per CU) walk the 256 x 256
-//     output tiles t = w, w + workers, w + 2 * workers, ...  Workgroups with
-//     blockIdx.x >= workers return at once, so any launch grid >= 1 is
+//     output tiles, the workgroups of each XCD striding through one
+//     contiguous band of tile indices (tile_walk, layout.hpp).  Workgroups
+//     with blockIdx.x >= workers return at once, so any launch grid >= 1 is
 //     correct.
 //   * Wave w owns the contiguous 128 x 128 quadrant (w / 2, w % 2) of a tile
 //     as 4 x 4 blocks of 32 x 32 fp32 accumulators (256 AGPRs per lane).
@@ -158,10 +159,11 @@ struct TileSrc {
   __amdgpu_buffer_rsrc_t a, b;
 };
 
+// `end`: one past the last tile index the caller may visit.
 __device__ __forceinline__ TileSrc tile_src(const GemmArgs& g, int t,
-                                            int tiles, int tiles_m,
+                                            int end, int tiles_m,
                                             int tiles_n) {
-  if (t >= tiles) return TileSrc{make_rsrc(g.A, 0), make_rsrc(g.B, 0)};
+  if (t >= end) return TileSrc{make_rsrc(g.A, 0), make_rsrc(g.B, 0)};
   const TileCoord tc = grouped_tile(t, tiles_m, tiles_n, g.group_m);
   const int rows_a = min(Cfg4w::kBM, g.M - tc.m * Cfg4w::kBM);
   const int rows_b = min(Cfg4w::kBN, g.N - tc.n * Cfg4w::kBN);
@@ -198,8 +200,9 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   const int workers = g.workers > 0 ? min((int)gridDim.x, g.workers)
                                     : (int)gridDim.x;
   if ((int)blockIdx.x >= workers) return;
-  int t = xcd_contiguous(blockIdx.x, workers);
-  if (t >= tiles) return;
+  const TileWalk walk = tile_walk(blockIdx.x, workers, tiles);
+  int t = walk.first;
+  if (t >= walk.end) return;
 
   const float sa = g.scale_a ? *g.scale_a : 1.0f;
   const float sb = g.scale_b ? *g.scale_b : 1.0f;
@@ -241,8 +244,8 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   const lds_u8* pa16[2] = {lds + off16_a, lds + (off16_a ^ 16u)};
   const lds_u8* pb16[2] = {lds + off16_b, lds + (off16_b ^ 16u)};
 
-  TileSrc cur = tile_src(g, t, tiles, tiles_m, tiles_n);
-  TileSrc nxt = tile_src(g, t + workers, tiles, tiles_m, tiles_n);
+  TileSrc cur = tile_src(g, t, walk.end, tiles_m, tiles_n);
+  TileSrc nxt = tile_src(g, t + walk.stride, walk.end, tiles_m, tiles_n);
 
   // DMA of one sub-buffer group of pipeline step kb into `stage`: operand op
   // (0 = A, 1 = B), half hi (0 = lo group, 1 = hi group).  Steps kb >= kt_pad
@@ -600,10 +603,10 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       }
     }
 
-    t += workers;
-    if (t >= tiles) break;
+    t += walk.stride;
+    if (t >= walk.end) break;
     cur = nxt;
-    nxt = tile_src(g, t + workers, tiles, tiles_m, tiles_n);
+    nxt = tile_src(g, t + walk.stride, walk.end, tiles_m, tiles_n);
   }
   // The last tile's look-ahead DMA (all zeros) still lands in LDS: let it
   // finish before the workgroup's LDS can be handed to another workgroup.

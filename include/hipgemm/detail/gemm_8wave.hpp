@@ -29,7 +29,8 @@
 //     takes ~15-25 cycles per 1 KiB DMA instruction, so a DMA issued between
 //     MFMAs stalls the MFMA stream (measured: ~90 cycles each); the memory
 //     phase, which waits for the other group's MFMAs anyway, absorbs them.
-//   * Tiles: persistent grid (tiles w, w + G, ...).  Each tile starts with a
+//   * Tiles: persistent grid, each XCD's workgroups striding through one
+//     contiguous band of tiles (tile_walk).  Each tile starts with a
 //     full-workgroup prologue (steps 0 and 1, B rows 0-127 of step 2) and
 //     ends with both groups' epilogues; the C staging of the epilogue reuses
 //     the A stages.
@@ -107,8 +108,9 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
     return (uint32_t)((limit - 1 - x) >> 31) & kOobOffset;
   };
 
-  for (int t = xcd_contiguous(blockIdx.x, workers); t < tiles; t += workers) {
-    const TileSrc src = tile_src(g, t, tiles, tiles_m, tiles_n);
+  const TileWalk walk = tile_walk(blockIdx.x, workers, tiles);
+  for (int t = walk.first; t < walk.end; t += walk.stride) {
+    const TileSrc src = tile_src(g, t, walk.end, tiles_m, tiles_n);
     // K-step kb's bytes of this lane's chunk exist (wave-uniform per step).
     auto k_ok = [&](int kb) {
       uint32_t k0 = (uint32_t)kb * Cfg::kBK;

@@ -45,13 +45,26 @@ struct TileCoord {
   int m, n;
 };
 
-// Logical position of workgroup `b` once each XCD's workgroups are made
-// contiguous: XCD x receives blocks x, x+8, x+16, ...; it owns logical
-// indices [start(x), start(x) + count(x)).
-__host__ __device__ inline int xcd_contiguous(int b, int grid) {
-  const int x = b % kNumXcds, j = b / kNumXcds;
-  const int per = grid / kNumXcds, extra = grid % kNumXcds;
-  return x * per + (x < extra ? x : extra) + j;
+// Tiles of persistent workgroup b among `workers`: first, first + stride,
+// ... while < end.  The workgroups of XCD x (blocks b = x mod G, G =
+// min(8, workers)) share one contiguous range of tile indices, sized in
+// proportion to their number, and stride through it; the ranges of all XCDs
+// partition [0, tiles), so every tile is visited exactly once.  Each XCD thus
+// sweeps one band of consecutive tiles for the whole run (grouped_tile maps
+// it to a few row panels, all columns) instead of a new band every round:
+// its L2 keeps serving the same A panels.
+struct TileWalk {
+  int first, stride, end;
+};
+__host__ __device__ inline TileWalk tile_walk(int b, int workers, int tiles) {
+  const int G = workers < kNumXcds ? workers : kNumXcds;
+  const int x = b % G, l = b / G;
+  const int per = workers / G, extra = workers % G;
+  const int n = per + (x < extra ? 1 : 0);
+  const int before = x * per + (x < extra ? x : extra);
+  const int start = (int)((long long)tiles * before / workers);
+  const int end = (int)((long long)tiles * (before + n) / workers);
+  return TileWalk{start + l, n, end};
 }
 
 // Tile (m, n) for logical tile index t in [0, tiles_m * tiles_n).

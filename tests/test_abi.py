@@ -36,7 +36,8 @@ def test_version_and_variants():
     assert hg.variant_name(3).startswith("skinny")
     assert hg.variant_name(4).startswith("8wave")
     assert hg.variant_name(5) is None
-    assert hg.select_variant(8192, 8192, 8192) in (1, 2)
+    assert hg.select_variant(8192, 8192, 8192) == 4
+    assert hg.select_variant(128, 8192, 8192) == 3
 
 
 @pytest.mark.parametrize("args", [
