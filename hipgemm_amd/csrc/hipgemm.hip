@@ -258,15 +258,15 @@ int resolve_variant(int variant, int M, int N, int K) {
 extern "C" {
 
 int hipgemm_select_variant(int M, int N, int K) {
-  (void)N;
-  (void)K;
   // Up to 128 rows the GEMM is a stream over B_T: the split-K schedule
-  // spreads it over every CU.  Above, the 8-wave ping-pong schedule: as fast
-  // as the 4-wave one at the long shapes (8192^3, 8192 x 28672 x 8192, K =
-  // 28672) and up to 1.16x on shapes with fewer steps per tile or fewer
-  // tiles than CUs, measured on MI355X in one process each.
+  // spreads it over every CU.  Above, the 4-wave 16x16x128 schedule (1-2 %
+  // ahead of the 8-wave one from 4096^3 up, and at 4000 x 5000 x 3584),
+  // except for short K on few tiles (a fraction of one round over the CUs),
+  // where the 8-wave one is 3-12 % ahead (2048^3, 512^3).  Measured on
+  // MI355X, schedules compared in one process.
   if (M <= CfgSkinny::kMaxM) return HIPGEMM_VARIANT_SKINNY;
-  return HIPGEMM_VARIANT_8WAVE;
+  if (K <= 2048 && tiles_of(M, N) <= 128) return HIPGEMM_VARIANT_8WAVE;
+  return HIPGEMM_VARIANT_4WAVE_MFMA16;
 }
 
 hipError_t hipgemm_fp8_gemm_bf16(const void* A, const void* B_T, void* C,

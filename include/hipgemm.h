@@ -49,8 +49,8 @@ enum {
   /* 256 threads (4 waves, one per SIMD), 256 x 256 tile, 2 LDS stages,
    * persistent grid, v_mfma_f32_32x32x64_f8f6f4. */
   HIPGEMM_VARIANT_4WAVE = 1,
-  /* The same schedule on v_mfma_f32_16x16x128_f8f6f4: the schedule behind
-   * the drop-in template. */
+  /* The same schedule on v_mfma_f32_16x16x128_f8f6f4: AUTO's choice for
+   * M > 128 (but see 8WAVE), and the schedule behind the drop-in template. */
   HIPGEMM_VARIANT_4WAVE_MFMA16 = 2,
   /* M <= 128 only: split-K over every CU for the HBM-bound skinny shapes,
    * operands streamed straight into registers, a deterministic in-kernel
@@ -60,8 +60,8 @@ enum {
   /* 512 threads (8 waves, two per SIMD, in two groups that alternate
    * between LDS/DMA work and MFMAs), 256 x 256 tile, each wave 128 x 64 of
    * it, persistent grid, v_mfma_f32_16x16x128_f8f6f4.  AUTO's choice for
-   * M > 128.  The reference's kernels are 4-wave only; no reference
-   * counterpart. */
+   * M > 128 with K <= 2048 on at most 128 tiles of 256 x 256.  The
+   * reference's kernels are 4-wave only; no reference counterpart. */
   HIPGEMM_VARIANT_8WAVE = 4,
   HIPGEMM_VARIANT_COUNT = 5
 };

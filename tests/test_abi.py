@@ -36,7 +36,10 @@ def test_version_and_variants():
     assert hg.variant_name(3).startswith("skinny")
     assert hg.variant_name(4).startswith("8wave")
     assert hg.variant_name(5) is None
-    assert hg.select_variant(8192, 8192, 8192) == 4
+    assert hg.select_variant(8192, 8192, 8192) == 2
+    assert hg.select_variant(4000, 5000, 3584) == 2
+    assert hg.select_variant(2048, 2048, 2048) == 4
+    assert hg.select_variant(512, 512, 512) == 4
     assert hg.select_variant(128, 8192, 8192) == 3
 
 
