@@ -113,12 +113,12 @@ struct Cfg4w {
 // the next quarter-step's waits (and barrier, at Q00 and Q10) instead of
 // before them.  MFMA read only registers, so they may straddle the barrier;
 // the tail keeps the matrix unit busy while the waves meet, which hides the
-// skew between them (one 64-cycle MFMA for 32x32x64, two 32-cycle ones for
-// 16x16x128).
+// skew between them (one MFMA; for 16x16x128 two measured 1 % slower at
+// 8192^3, none 3 % slower).
 template <int kMf>
 struct QuarterShape {
   static constexpr int kMfma = kMf == 16 ? 16 : 8;
-  static constexpr int kTail = kMf == 16 ? 2 : 1;
+  static constexpr int kTail = 1;
   static constexpr int kHead = kMfma - kTail;
 };
 
@@ -126,7 +126,8 @@ struct QuarterShape {
 // quarter's tail MFMA (0x008) first, then this quarter's head MFMA with its
 // 8 LDS reads (0x100) in the first half and its 4 DMA (0x020) after.
 // 32x32x64: [M R R] x 4, [M D] x 2, [M D D].  16x16x128: [M R] x 8,
-// [M D] x 4, [M] x 2.
+// [M D] x 4, [M] x 3 (spreading the DMAs between the reads, or issuing them
+// first, measured 9-10 % slower).
 template <int kMf>
 __device__ __forceinline__ void quarter_schedule(bool tail) {
   if (tail)
@@ -140,7 +141,7 @@ __device__ __forceinline__ void quarter_schedule(bool tail) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
   } else {
     for (int x = 0; x < 4; ++x) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
