@@ -474,40 +474,72 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
               __builtin_amdgcn_readfirstlane((wm * 128 + row4) * g.ldc * 2);
           __builtin_amdgcn_raw_buffer_store_b128(
               v[p], rsrc_c, vcol | col_oob | oob_unless(row4 + rsub, rows_left),
-              srow, 0);
+              srow, kStoreC);
         }
       };
+      if constexpr (k16) {
+        // Blocks (2i + ii, j): lane l holds row 16 ii + l%16, 8-byte piece
+        // 4j + l/16; piece x of row r at 8-byte slot x ^ 2(r % 16).  A
+        // 16-byte chunk keeps its two halves in order (the XOR is even), so
+        // each lane reads its chunk k of row r with one ds_read_b128 at
+        // chunk k ^ (r % 16).  Writes: each half-wave covers 32 distinct
+        // slots; reads: each row's 16 lanes cover 16 distinct chunks.
+        //
+        // Software-pipelined over the four 32-row chunks: chunk i is read
+        // back, then chunk i + 1 is converted and written into the same
+        // 8 KiB between chunk i's 8 stores.  One wave's LDS operations
+        // complete in issue order, so the reads of chunk i return it before
+        // the writes of chunk i + 1 land; the conversions overlap the
+        // stores instead of waiting for them.
+        const int wr = elane & 15, wg = elane >> 4;
+        auto write_blk = [&](int i, int ii, int j) {
+          const f32x4& a = acc16[2 * i + ii][j];
+          lds_write8(stg + (16 * ii + wr) * 256 + (((4 * j + wg) ^ (2 * wr)) * 8),
+                     u32x2{pack_bf16x2(acc_read(a[0]) * scale,
+                                       acc_read(a[1]) * scale),
+                           pack_bf16x2(acc_read(a[2]) * scale,
+                                       acc_read(a[3]) * scale)});
+        };
+        auto store_one = [&](int i, int p, const i32x4& v) {
+          int row4 = 32 * i + 4 * p;
+          asm volatile("" : "+s"(row4));  // recompute per store, never hoist
+          const int srow =
+              __builtin_amdgcn_readfirstlane((wm * 128 + row4) * g.ldc * 2);
+          __builtin_amdgcn_raw_buffer_store_b128(
+              v, rsrc_c, vcol | col_oob | oob_unless(row4 + rsub, rows_left),
+              srow, kStoreC);
+        };
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        i32x4 v[8];
-        if constexpr (k16) {
-          // Blocks (2i + ii, j): lane l holds row 16 ii + l%16, 8-byte piece
-          // 4j + l/16; piece x of row r at 8-byte slot x ^ 2(r % 16).  A
-          // 16-byte chunk keeps its two halves in order (the XOR is even), so
-          // each lane reads its chunk k of row r with one ds_read_b128 at
-          // chunk k ^ (r % 16).  Writes: each half-wave covers 32 distinct
-          // slots; reads: each row's 16 lanes cover 16 distinct chunks.
-          const int wr = elane & 15, wg = elane >> 4;
+        for (int ii = 0; ii < 2; ++ii) {
 #pragma unroll
-          for (int ii = 0; ii < 2; ++ii) {
+          for (int j = 0; j < 8; ++j) write_blk(0, ii, j);
+          sched_fence();  // bound the live range
+        }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const f32x4& a = acc16[2 * i + ii][j];
-              lds_write8(stg + (16 * ii + wr) * 256 + (((4 * j + wg) ^ (2 * wr)) * 8),
-                         u32x2{pack_bf16x2(acc_read(a[0]) * scale,
-                                           acc_read(a[1]) * scale),
-                               pack_bf16x2(acc_read(a[2]) * scale,
-                                           acc_read(a[3]) * scale)});
-            }
-            sched_fence();  // bound the live range
-          }
+        for (int i = 0; i < 4; ++i) {
           compiler_fence();
+          i32x4 v[8];
 #pragma unroll
           for (int p = 0; p < 8; ++p) {
             const int r = 4 * p + rsub;
             v[p] = lds_read16(stg + r * 256 + ((chunk ^ (r & 15)) * 16));
           }
-        } else {
+          compiler_fence();
+#pragma unroll
+          for (int p = 0; p < 8; ++p) {
+            store_one(i, p, v[p]);
+            if (i < 3) {
+              write_blk(i + 1, p / 4, 2 * (p % 4));
+              write_blk(i + 1, p / 4, 2 * (p % 4) + 1);
+            }
+            sched_fence();
+          }
+        }
+      } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        i32x4 v[8];
+        {
           // 32 rows (one accumulator block row i) through the wave's own
           // 8 KiB: row r at 256 r; the 8-byte piece x (0..31) of the row at
           // slot x ^ r.  Writes: lanes 0-31 (one 8-byte piece each of rows
@@ -540,6 +572,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
         compiler_fence();
         sched_fence();
       }
+      }
     } else {
       // N, ldc or C's alignment rule out 16-byte stores: 2-byte stores
       // straight from the accumulators, lane masks as out-of-range offsets.
@@ -565,7 +598,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
               __builtin_amdgcn_raw_buffer_store_b16(
                   (unsigned short)w, rsrc_c,
                   (vrow | oob_unless(c + r, cols_left)) + (16 * j + r) * 2,
-                  srow, 0);
+                  srow, kStoreC);
             }
             sched_fence();  // bound the live range: one block at a time
           }
@@ -591,7 +624,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                     (unsigned short)w, rsrc_c,
                     (vrow | oob_unless(c + r, cols_left)) +
                         (32 * j + 8 * q + r) * 2,
-                    srow, 0);
+                    srow, kStoreC);
               }
             }
             sched_fence();  // bound the live range: one block at a time

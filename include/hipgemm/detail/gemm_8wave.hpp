@@ -272,7 +272,7 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
               __builtin_amdgcn_readfirstlane((wm * 128 + row8) * g.ldc * 2);
           __builtin_amdgcn_raw_buffer_store_b128(
               v[p], rsrc_c, vcol | col_oob | oob_unless(row8 + rsub, rows_left),
-              srow, 0);
+              srow, kStoreC);
         }
         compiler_fence();
         sched_fence();
@@ -294,7 +294,7 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
             const uint32_t w = (q < 2 ? v.x : v.y) >> (16 * (q & 1));
             __builtin_amdgcn_raw_buffer_store_b16(
                 (unsigned short)w, rsrc_c,
-                (vrow | oob_unless(col + q, cols_left)) + (16 * j + q) * 2, srow, 0);
+                (vrow | oob_unless(col + q, cols_left)) + (16 * j + q) * 2, srow, kStoreC);
           }
           sched_fence();
         }
