@@ -30,6 +30,7 @@ __all__ = [
     "fp8_gemm_4wave_256x256x128", "gemm_raw", "select_variant",
     "variant_name", "version", "tile_order", "lds_slot", "VARIANTS",
     "declared_symbols", "gemm_raw_ws", "workspace_size",
+    "fp8_gemm_bf16_rowcol", "gemm_raw_rowcol",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -79,6 +80,10 @@ def lib() -> ctypes.CDLL:
                                            ci, vp, vp, ci, vp, ctypes.c_size_t,
                                            vp]
     L.hipgemm_fp8_gemm_bf16_ws.restype = ci
+    L.hipgemm_fp8_gemm_bf16_rowcol.argtypes = [vp, vp, vp, ci, ci, ci, ci, ci,
+                                               ci, vp, vp, ci, vp,
+                                               ctypes.c_size_t, vp]
+    L.hipgemm_fp8_gemm_bf16_rowcol.restype = ci
     L.hipgemm_workspace_size.argtypes = [ci, ci, ci, ci]
     L.hipgemm_workspace_size.restype = ctypes.c_size_t
     L.hipgemm_fp8_gemm_4wave_256x256x128.argtypes = [vp, vp, vp, ci, ci, ci,
@@ -129,6 +134,18 @@ def gemm_raw_ws(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int, K: int,
         a_ptr or None, b_ptr or None, c_ptr or None, M, N, K, lda, ldb, ldc,
         scale_a_ptr or None, scale_b_ptr or None, variant, ws_ptr or None,
         ws_bytes, stream or None))
+
+
+def gemm_raw_rowcol(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int,
+                    K: int, lda: int, ldb: int, ldc: int, rows_ptr: int,
+                    cols_ptr: int, variant: int = 0, ws_ptr: int = 0,
+                    ws_bytes: int = 0, stream: int = 0) -> int:
+    """Call hipgemm_fp8_gemm_bf16_rowcol on raw device pointers (rows_ptr: M
+    floats, cols_ptr: N floats, 0 = all ones)."""
+    return int(lib().hipgemm_fp8_gemm_bf16_rowcol(
+        a_ptr or None, b_ptr or None, c_ptr or None, M, N, K, lda, ldb, ldc,
+        rows_ptr or None, cols_ptr or None, variant, ws_ptr or None, ws_bytes,
+        stream or None))
 
 
 def workspace_size(M: int, N: int, K: int, variant: int = 0) -> int:
@@ -201,16 +218,21 @@ def _scale_ptr(s, name):
     return s.data_ptr()
 
 
-def fp8_gemm_bf16(a, b_t, scale_a=None, scale_b=None, out=None,
-                  variant: int = 0, stream=None):
-    """out[M, N] (bf16) = scale_a * scale_b * a[M, K] @ b_t[N, K].T.
+def _vector_ptr(s, n, name):
+    if s is None:
+        return 0
+    torch = _torch()
+    if not (isinstance(s, torch.Tensor) and s.is_cuda and
+            s.dtype == torch.float32 and s.dim() == 1 and s.numel() == n and
+            (n <= 1 or s.stride(0) == 1)):
+        raise HipGemmError(f"{name} must be a contiguous float32 device vector "
+                           f"of {n} elements", hipErrorInvalidValue)
+    return s.data_ptr()
 
-    a, b_t: device tensors of dtype float8_e4m3fn (or uint8 holding e4m3
-    bytes) with unit stride along K.  scale_a / scale_b: optional 1-element
-    float32 device tensors.  out: optional bf16 device tensor with unit column
-    stride; allocated if None.  Runs on `stream` (a torch.cuda.Stream) or the
-    current stream.
-    """
+
+def _gemm_operands(a, b_t, out, variant, stream):
+    """Shared argument handling of the torch entry points: shapes, strides,
+    output, stream and workspace."""
     torch = _torch()
     a = _as_bytes_2d(a, "a")
     b_t = _as_bytes_2d(b_t, "b_t")
@@ -232,12 +254,47 @@ def fp8_gemm_bf16(a, b_t, scale_a=None, scale_b=None, out=None,
     ldc = out.stride(0) if M > 1 else max(N, 1)
     nbytes = workspace_size(M, N, K, variant) if M > 0 and N > 0 else 0
     ws = _workspace(a.device, stream, nbytes) if nbytes else None
+    return (a, b_t, out, M, N, K, lda, ldb, ldc,
+            ws.data_ptr() if ws is not None else 0, nbytes, stream)
+
+
+def fp8_gemm_bf16(a, b_t, scale_a=None, scale_b=None, out=None,
+                  variant: int = 0, stream=None):
+    """out[M, N] (bf16) = scale_a * scale_b * a[M, K] @ b_t[N, K].T.
+
+    a, b_t: device tensors of dtype float8_e4m3fn (or uint8 holding e4m3
+    bytes) with unit stride along K.  scale_a / scale_b: optional 1-element
+    float32 device tensors.  out: optional bf16 device tensor with unit column
+    stride; allocated if None.  Runs on `stream` (a torch.cuda.Stream) or the
+    current stream.
+    """
+    a, b_t, out, M, N, K, lda, ldb, ldc, ws, nbytes, stream = _gemm_operands(
+        a, b_t, out, variant, stream)
     code = gemm_raw_ws(a.data_ptr(), b_t.data_ptr(), out.data_ptr(), M, N, K,
                        lda, ldb, ldc, _scale_ptr(scale_a, "scale_a"),
-                       _scale_ptr(scale_b, "scale_b"), variant,
-                       ws.data_ptr() if ws is not None else 0, nbytes,
+                       _scale_ptr(scale_b, "scale_b"), variant, ws, nbytes,
                        stream.cuda_stream)
     _check(code, "hipgemm_fp8_gemm_bf16_ws")
+    return out
+
+
+def fp8_gemm_bf16_rowcol(a, b_t, scale_rows=None, scale_cols=None, out=None,
+                         variant: int = 0, stream=None):
+    """out[m, n] (bf16) = scale_rows[m] * scale_cols[n] * (a @ b_t.T)[m, n].
+
+    As fp8_gemm_bf16, with per-row scales of a (a float32 device vector of M
+    elements) and per-column scales of the output (one per row of b_t: N
+    elements); either may be None for all ones.  variant 1 (the 32x32x64
+    schedule) is not available here.
+    """
+    a, b_t, out, M, N, K, lda, ldb, ldc, ws, nbytes, stream = _gemm_operands(
+        a, b_t, out, variant, stream)
+    code = gemm_raw_rowcol(a.data_ptr(), b_t.data_ptr(), out.data_ptr(), M, N,
+                           K, lda, ldb, ldc,
+                           _vector_ptr(scale_rows, M, "scale_rows"),
+                           _vector_ptr(scale_cols, N, "scale_cols"), variant,
+                           ws, nbytes, stream.cuda_stream)
+    _check(code, "hipgemm_fp8_gemm_bf16_rowcol")
     return out
 
 

@@ -16,27 +16,28 @@ namespace {
 
 using namespace hipgemm::detail;
 
-template <bool kVecStore, int kMf>
+// kRowCol: per-row / per-column scale vectors instead of per-tensor scalars.
+template <bool kVecStore, int kMf, bool kRowCol>
 __global__ __launch_bounds__(256, 1) void k_fp8_gemm_4wave(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg4w::kLdsBytes];
-  gemm_4wave_body<kVecStore, kMf>(g, (lds_u8*)lds);
+  gemm_4wave_body<kVecStore, kMf, kRowCol>(g, (lds_u8*)lds);
 }
 
-template <bool kVecStore>
+template <bool kVecStore, bool kRowCol>
 __global__ __launch_bounds__(512, 1) void k_fp8_gemm_8wave(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg8w::kLdsBytes];
-  gemm_8wave_body<kVecStore>(g, (lds_u8*)lds);
+  gemm_8wave_body<kVecStore, kRowCol>(g, (lds_u8*)lds);
 }
 
-template <int kMB, bool kVec8>
+template <int kMB, bool kVec8, bool kRowCol>
 __global__ __launch_bounds__(256, 1) void k_fp8_gemm_skinny(SkinnyArgs g) {
-  gemm_skinny_body<kMB, kVec8>(g);
+  gemm_skinny_body<kMB, kVec8, kRowCol>(g);
 }
 
-template <bool kVec8>
+template <bool kVec8, bool kRowCol>
 __global__ __launch_bounds__(256, 1) void k_fp8_gemm_skinny_reduce(SkinnyArgs g,
                                                                     int kmb) {
-  gemm_skinny_reduce_body<kVec8>(g, kmb);
+  gemm_skinny_reduce_body<kVec8, kRowCol>(g, kmb);
 }
 
 // 32-bit buffer offsets: 256 rows of A or B_T (1-byte elements) span at most
@@ -87,7 +88,7 @@ int cu_count() {
   return n;
 }
 
-template <int kMf>
+template <int kMf, bool kRowCol>
 hipError_t launch_4wave(GemmArgs g, hipStream_t stream) {
   // Persistent grid: one workgroup per CU at most (the kernel's 160 KiB of
   // LDS allows no more), each walking tiles w, w + grid, ...
@@ -100,12 +101,13 @@ hipError_t launch_4wave(GemmArgs g, hipStream_t stream) {
   const bool vec = (g.N % 8 == 0) && (g.ldc % 8 == 0) && aligned(g.C, 16);
   void* args[] = {&g};
   const void* fn =
-      vec ? reinterpret_cast<const void*>(&k_fp8_gemm_4wave<true, kMf>)
-          : reinterpret_cast<const void*>(&k_fp8_gemm_4wave<false, kMf>);
+      vec ? reinterpret_cast<const void*>(&k_fp8_gemm_4wave<true, kMf, kRowCol>)
+          : reinterpret_cast<const void*>(&k_fp8_gemm_4wave<false, kMf, kRowCol>);
   return hipLaunchKernel(fn, dim3(grid), dim3(Cfg4w::kThreads), args, 0,
                          stream);
 }
 
+template <bool kRowCol>
 hipError_t launch_8wave(GemmArgs g, hipStream_t stream) {
   // Same persistent grid as the 4-wave kernel (160 KiB of LDS: one
   // workgroup per CU).
@@ -115,8 +117,9 @@ hipError_t launch_8wave(GemmArgs g, hipStream_t stream) {
   g.workers = grid;
   const bool vec = (g.N % 8 == 0) && (g.ldc % 8 == 0) && aligned(g.C, 16);
   void* args[] = {&g};
-  const void* fn = vec ? reinterpret_cast<const void*>(&k_fp8_gemm_8wave<true>)
-                       : reinterpret_cast<const void*>(&k_fp8_gemm_8wave<false>);
+  const void* fn =
+      vec ? reinterpret_cast<const void*>(&k_fp8_gemm_8wave<true, kRowCol>)
+          : reinterpret_cast<const void*>(&k_fp8_gemm_8wave<false, kRowCol>);
   return hipLaunchKernel(fn, dim3(grid), dim3(Cfg8w::kThreads), args, 0, stream);
 }
 
@@ -147,17 +150,18 @@ SkinnyPlan plan_skinny(int M, int N, int K) {
   return p;
 }
 
-template <int kMB>
+template <int kMB, bool kRowCol>
 hipError_t launch_skinny_mb(const SkinnyArgs& g, bool vec8, int grid,
                             hipStream_t stream) {
   void* args[] = {const_cast<SkinnyArgs*>(&g)};
   const void* fn =
-      vec8 ? reinterpret_cast<const void*>(&k_fp8_gemm_skinny<kMB, true>)
-           : reinterpret_cast<const void*>(&k_fp8_gemm_skinny<kMB, false>);
+      vec8 ? reinterpret_cast<const void*>(&k_fp8_gemm_skinny<kMB, true, kRowCol>)
+           : reinterpret_cast<const void*>(&k_fp8_gemm_skinny<kMB, false, kRowCol>);
   return hipLaunchKernel(fn, dim3(grid), dim3(CfgSkinny::kThreads), args, 0,
                          stream);
 }
 
+template <bool kRowCol>
 hipError_t launch_skinny(const GemmArgs& a, const SkinnyPlan& p, void* ws,
                          hipStream_t stream) {
   // From 4 row blocks up, one workgroup per column tile summing every slice
@@ -175,26 +179,28 @@ hipError_t launch_skinny(const GemmArgs& a, const SkinnyPlan& p, void* ws,
   const int grid = p.tiles_n * p.slices;
   hipError_t e;
   switch (p.kmb) {
-    case 1: e = launch_skinny_mb<1>(g, vec8, grid, stream); break;
-    case 2: e = launch_skinny_mb<2>(g, vec8, grid, stream); break;
-    case 4: e = launch_skinny_mb<4>(g, vec8, grid, stream); break;
-    default: e = launch_skinny_mb<8>(g, vec8, grid, stream); break;
+    case 1: e = launch_skinny_mb<1, kRowCol>(g, vec8, grid, stream); break;
+    case 2: e = launch_skinny_mb<2, kRowCol>(g, vec8, grid, stream); break;
+    case 4: e = launch_skinny_mb<4, kRowCol>(g, vec8, grid, stream); break;
+    default: e = launch_skinny_mb<8, kRowCol>(g, vec8, grid, stream); break;
   }
   if (e != hipSuccess || !reduce_pass) return e;
   int kmb = p.kmb;
   void* args[] = {&g, &kmb};
   const void* fn =
-      vec8 ? reinterpret_cast<const void*>(&k_fp8_gemm_skinny_reduce<true>)
-           : reinterpret_cast<const void*>(&k_fp8_gemm_skinny_reduce<false>);
+      vec8 ? reinterpret_cast<const void*>(&k_fp8_gemm_skinny_reduce<true, kRowCol>)
+           : reinterpret_cast<const void*>(&k_fp8_gemm_skinny_reduce<false, kRowCol>);
   return hipLaunchKernel(fn, dim3(p.tiles_n * p.kmb), dim3(CfgSkinny::kThreads),
                          args, 0, stream);
 }
 
 int resolve_variant(int variant, int M, int N, int K);
 
-// Shared body of the two GEMM entry points.  `ws` may be null when
-// `ws_given` is false: a schedule that needs a workspace then takes a
-// stream-ordered allocation for the call.
+// Shared body of the GEMM entry points.  `ws` may be null when `ws_given` is
+// false: a schedule that needs a workspace then takes a stream-ordered
+// allocation for the call.  With `rowcol`, scale_a / scale_b are vectors of M
+// / N floats (or null for all ones) applied per row of C / per column of C.
+template <bool kRowCol>
 hipError_t run_gemm(const void* A, const void* B_T, void* C, int M, int N,
                     int K, int lda, int ldb, int ldc, const float* scale_a,
                     const float* scale_b, int variant, bool ws_given, void* ws,
@@ -206,6 +212,11 @@ hipError_t run_gemm(const void* A, const void* B_T, void* C, int M, int N,
   if (ws_given && ws_bytes > 0 && (!ws || !aligned(ws, 256)))
     return hipErrorInvalidValue;
   if (M == 0 || N == 0) return hipSuccess;
+  // Scale vectors are read with 4-byte loads; the 32x32x64 schedule has no
+  // per-row/per-column epilogue.
+  if (kRowCol && (!aligned(scale_a, 4) || !aligned(scale_b, 4) ||
+                  variant == HIPGEMM_VARIANT_4WAVE))
+    return hipErrorInvalidValue;
   variant = resolve_variant(variant, M, N, K);
   if (K == 0) lda = ldb = 16;  // nothing is read; keep the offset math inert
   const int tiles_m = (M + Cfg4w::kBM - 1) / Cfg4w::kBM;
@@ -226,25 +237,26 @@ hipError_t run_gemm(const void* A, const void* B_T, void* C, int M, int N,
   switch (variant) {
     case HIPGEMM_VARIANT_SKINNY: {
       const SkinnyPlan p = plan_skinny(M, N, K);
-      if (p.ws_bytes == 0) return launch_skinny(g, p, nullptr, stream);
+      if (p.ws_bytes == 0) return launch_skinny<kRowCol>(g, p, nullptr, stream);
       if (ws_given) {
         if (ws_bytes < p.ws_bytes) return hipErrorInvalidValue;
-        return launch_skinny(g, p, ws, stream);
+        return launch_skinny<kRowCol>(g, p, ws, stream);
       }
       void* tmp = nullptr;
       if ((e = hipMallocAsync(&tmp, p.ws_bytes, stream)) != hipSuccess) return e;
       e = hipMemsetAsync(tmp, 0, p.counter_bytes, stream);
-      if (e == hipSuccess) e = launch_skinny(g, p, tmp, stream);
+      if (e == hipSuccess) e = launch_skinny<kRowCol>(g, p, tmp, stream);
       const hipError_t f = hipFreeAsync(tmp, stream);
       return e != hipSuccess ? e : f;
     }
     case HIPGEMM_VARIANT_4WAVE_MFMA16:
-      return launch_4wave<16>(g, stream);
+      return launch_4wave<16, kRowCol>(g, stream);
     case HIPGEMM_VARIANT_8WAVE:
-      return launch_8wave(g, stream);
+      return launch_8wave<kRowCol>(g, stream);
     case HIPGEMM_VARIANT_4WAVE:
     default:
-      return launch_4wave<32>(g, stream);
+      if constexpr (kRowCol) return hipErrorInvalidValue;  // rejected above
+      else return launch_4wave<32, false>(g, stream);
   }
 }
 
@@ -274,8 +286,8 @@ hipError_t hipgemm_fp8_gemm_bf16(const void* A, const void* B_T, void* C,
                                  int ldc, const float* scale_a,
                                  const float* scale_b, int variant,
                                  hipStream_t stream) {
-  return run_gemm(A, B_T, C, M, N, K, lda, ldb, ldc, scale_a, scale_b, variant,
-                  false, nullptr, 0, stream);
+  return run_gemm<false>(A, B_T, C, M, N, K, lda, ldb, ldc, scale_a, scale_b,
+                         variant, false, nullptr, 0, stream);
 }
 
 hipError_t hipgemm_fp8_gemm_bf16_ws(const void* A, const void* B_T, void* C,
@@ -284,8 +296,22 @@ hipError_t hipgemm_fp8_gemm_bf16_ws(const void* A, const void* B_T, void* C,
                                     const float* scale_b, int variant,
                                     void* workspace, size_t workspace_bytes,
                                     hipStream_t stream) {
-  return run_gemm(A, B_T, C, M, N, K, lda, ldb, ldc, scale_a, scale_b, variant,
-                  true, workspace, workspace_bytes, stream);
+  return run_gemm<false>(A, B_T, C, M, N, K, lda, ldb, ldc, scale_a, scale_b,
+                         variant, true, workspace, workspace_bytes, stream);
+}
+
+hipError_t hipgemm_fp8_gemm_bf16_rowcol(const void* A, const void* B_T, void* C,
+                                        int M, int N, int K, int lda, int ldb,
+                                        int ldc, const float* scale_rows,
+                                        const float* scale_cols, int variant,
+                                        void* workspace, size_t workspace_bytes,
+                                        hipStream_t stream) {
+  // A null workspace with a zero size lets the call allocate one when the
+  // split-K schedule needs it, like hipgemm_fp8_gemm_bf16.
+  const bool ws_given = workspace != nullptr || workspace_bytes != 0;
+  return run_gemm<true>(A, B_T, C, M, N, K, lda, ldb, ldc, scale_rows,
+                        scale_cols, variant, ws_given, workspace,
+                        workspace_bytes, stream);
 }
 
 size_t hipgemm_workspace_size(int M, int N, int K, int variant) {

@@ -100,6 +100,32 @@ hipError_t hipgemm_fp8_gemm_bf16_ws(const void *A, const void *B_T, void *C,
                                     void *workspace, size_t workspace_bytes,
                                     hipStream_t stream);
 
+/*
+ * Per-row / per-column scaled GEMM:
+ *
+ *   C[m, n] = bf16_rne( (scale_rows[m] * scale_cols[n]) * sum_k A[m,k] B_T[n,k] )
+ *
+ * scale_rows is a DEVICE vector of M fp32 (one per row of A and C),
+ * scale_cols one of N fp32 (one per row of B_T, i.e. column of C); either may
+ * be NULL for all ones.  The product of the two scales is formed in fp32 and
+ * applied to the fp32 accumulator before rounding, as in
+ * hipgemm_fp8_gemm_bf16 (which is this call with constant vectors).  Both
+ * vectors must be 4-byte aligned.  Accepts AUTO, SKINNY, 4WAVE_MFMA16 and
+ * 8WAVE; HIPGEMM_VARIANT_4WAVE returns hipErrorInvalidValue.  Workspace as in
+ * hipgemm_fp8_gemm_bf16_ws, except that workspace == NULL with
+ * workspace_bytes == 0 takes a stream-ordered allocation when one is needed,
+ * as hipgemm_fp8_gemm_bf16 does.
+ * No reference counterpart: the reference applies no scales at all
+ * (store_rt, fp8_4wave.hpp:214-238, converts the accumulator straight to
+ * bf16).
+ */
+hipError_t hipgemm_fp8_gemm_bf16_rowcol(const void *A, const void *B_T, void *C,
+                                        int M, int N, int K, int lda, int ldb,
+                                        int ldc, const float *scale_rows,
+                                        const float *scale_cols, int variant,
+                                        void *workspace, size_t workspace_bytes,
+                                        hipStream_t stream);
+
 /* Workspace bytes hipgemm_fp8_gemm_bf16_ws needs for this shape and variant
  * on the current device (0: none).  No GPU work.  No reference counterpart. */
 size_t hipgemm_workspace_size(int M, int N, int K, int variant);

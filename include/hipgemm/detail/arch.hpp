@@ -66,8 +66,21 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc,
       (int)voffset, (int)soffset, 0, 0);
 }
 
+// 4 bytes per lane, global (rsrc + voffset) -> LDS (lds_wave_base + 4 * lane);
+// each lane's range check covers exactly its own 4 bytes.
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rsrc,
+                                     lds_u8* lds_wave_base, uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rsrc, (__attribute__((address_space(3))) void*)lds_wave_base, 4,
+      (int)voffset, 0, 0, 0);
+}
+
 __device__ __forceinline__ i32x4 lds_read16(const lds_u8* p) {
   return *reinterpret_cast<const __attribute__((address_space(3))) i32x4*>(p);
+}
+
+__device__ __forceinline__ uint32_t lds_read4(const lds_u8* p) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) uint32_t*>(p);
 }
 
 __device__ __forceinline__ u32x2 lds_read8(const lds_u8* p) {

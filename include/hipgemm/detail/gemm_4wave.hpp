@@ -82,6 +82,17 @@ struct GemmArgs {
   int workers;  // persistent workgroups (<= grid); 0 = the whole grid
 };
 
+// The GemmArgs of a kernel whose only argument is a GemmArgs, read again
+// from the kernel-argument segment (scalar loads) at the point of use, so
+// that values needed once per tile occupy no registers across the K loop.
+__device__ __forceinline__ const __attribute__((address_space(4))) GemmArgs*
+kernel_args() {
+  auto p = (const __attribute__((address_space(4))) GemmArgs*)
+      __builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  return p;
+}
+
 __host__ __device__ constexpr int default_group_m(int tiles_m, int tiles_n) {
   // 32 CUs per XCD: make the 32 co-resident tiles of an XCD about 4 x 8.
   const int cols = tiles_n < 8 ? tiles_n : 8;
@@ -176,15 +187,90 @@ __device__ __forceinline__ TileSrc tile_src(const GemmArgs& g, int t,
                            (uint32_t)rows_b * (uint32_t)g.ldb)};
 }
 
+// Per-row / per-column scales (scale mode "rowcol": scale_a holds M floats,
+// scale_b N floats, either may be null = 1.0) for a wave's 16 x 16
+// accumulator blocks: lane l needs, for block row bi, the scale of row
+// row0 + 16 bi + l % 16 and, for block column bj, those of columns
+// col0 + 16 bj + 4 (l / 16) + e, e < 4.  Rows or columns past M or N load
+// 0 (their results are never stored).  The loads count in vmcnt; the
+// caller waits for them.
+template <int kBR, int kBC>
+struct RowColScales {
+  float r[kBR];
+  float c[kBC][4];
+  __device__ __forceinline__ void load(const GemmArgs& g, int row0, int col0,
+                                       int lane) {
+    const int lr = lane & 15, lc = 4 * (lane >> 4);
+    if (g.scale_a) {
+      const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.scale_a, (uint32_t)g.M * 4);
+#pragma unroll
+      for (int bi = 0; bi < kBR; ++bi)
+        r[bi] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(
+                       ra, (uint32_t)(row0 + 16 * bi + lr) * 4u, 0, 0));
+    } else {
+#pragma unroll
+      for (int bi = 0; bi < kBR; ++bi) r[bi] = 1.0f;
+    }
+    if (g.scale_b) {
+      const __amdgpu_buffer_rsrc_t rb = make_rsrc(g.scale_b, (uint32_t)g.N * 4);
+#pragma unroll
+      for (int bj = 0; bj < kBC; ++bj)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          c[bj][e] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(
+                         rb, (uint32_t)(col0 + 16 * bj + lc + e) * 4u, 0, 0));
+    } else {
+#pragma unroll
+      for (int bj = 0; bj < kBC; ++bj)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) c[bj][e] = 1.0f;
+    }
+  }
+  // The same from LDS: row scales at base + 4 r, column scales at
+  // base + 512 + 4 c (r, c relative to row0, col0); `has_rows` /
+  // `has_cols` false = all ones.  Read as integers, like the epilogue's own
+  // LDS traffic, and fenced: type-based alias analysis must not let a float
+  // read move past the staging writes that overwrite the scales.
+  __device__ __forceinline__ void read_lds(const lds_u8* base, bool has_rows,
+                                           bool has_cols, int lane) {
+    const int lr = lane & 15, lc = 4 * (lane >> 4);
+    // (The 16-byte read is bit-cast as a whole vector: __builtin_bit_cast of
+    // one element of a vector, v[e], yields element 0 with this compiler.)
+#pragma unroll
+    for (int bi = 0; bi < kBR; ++bi) {
+      const float x = __builtin_bit_cast(float, lds_read4(base + 4 * (16 * bi + lr)));
+      r[bi] = has_rows ? x : 1.0f;
+    }
+#pragma unroll
+    for (int bj = 0; bj < kBC; ++bj) {
+      const f32x4 v =
+          __builtin_bit_cast(f32x4, lds_read16(base + 512 + 4 * (16 * bj + lc)));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) c[bj][e] = has_cols ? v[e] : 1.0f;
+    }
+    compiler_fence();
+  }
+  // The scale of element e of block (bi, bj): row scale times column scale,
+  // one fp32 product (the per-tensor path's scale_a * scale_b, per element).
+  __device__ __forceinline__ float at(int bi, int bj, int e) const {
+    return r[bi] * c[bj][e];
+  }
+};
+
 // kMf selects the MFMA: 32 = v_mfma_f32_32x32x64_f8f6f4 (4 x 4 blocks of
 // 32 x 32 per wave, two MFMA per block per step), 16 =
 // v_mfma_f32_16x16x128_f8f6f4 (8 x 8 blocks of 16 x 16, one per block per
 // step).  Same data flow and the same 2048 MFMA cycles per step either way.
-template <bool kVecStore, int kMf = 32>
+// kRowCol: per-row / per-column scales (RowColScales) instead of the
+// per-tensor pair; 16x16x128 only.
+template <bool kVecStore, int kMf = 32, bool kRowCol = false>
 __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                                                 lds_u8* lds) {
   using Cfg = Cfg4w;
   static_assert(kMf == 32 || kMf == 16, "MFMA shape");
+  static_assert(!kRowCol || kMf == 16, "row/column scales: 16x16x128 only");
   constexpr bool k16 = kMf == 16;
   constexpr int kDmaPerGroup = 4;  // per wave
   constexpr int kWaitSteady = 4 * kDmaPerGroup;
@@ -207,8 +293,10 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   int t = walk.first;
   if (t >= walk.end) return;
 
-  const float sa = g.scale_a ? *g.scale_a : 1.0f;
-  const float sb = g.scale_b ? *g.scale_b : 1.0f;
+  // Per-tensor scales (with kRowCol the pointers are vectors, read in the
+  // epilogue instead).
+  const float sa = !kRowCol && g.scale_a ? *g.scale_a : 1.0f;
+  const float sb = !kRowCol && g.scale_b ? *g.scale_b : 1.0f;
   const float scale = sa * sb;
 
   // ---- DMA lane geometry: instruction q of wave w covers rows
@@ -253,31 +341,78 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // DMA of one sub-buffer group of pipeline step kb into `stage`: operand op
   // (0 = A, 1 = B), half hi (0 = lo group, 1 = hi group).  Steps kb >= kt_pad
   // are steps kb - kt_pad of the next tile.  4 instructions per wave.
-  auto dma_group = [&](int kb, int stage, int op, int hi) {
+  struct DmaSrc {
+    __amdgpu_buffer_rsrc_t src;
+    uint32_t k0;
+    bool ok;
+  };
+  auto dma_src = [&](int kb, int op) {
     const bool next = kb >= kt_pad;  // wave-uniform
     uint32_t k0 = (uint32_t)(next ? kb - kt_pad : kb) * Cfg::kBK;
     // Opaque to the optimiser: keeps the per-step lane masks from being
     // hoisted out of the tile loop (they would pin VGPRs and spill).
     asm volatile("" : "+s"(k0));
-    const bool ok = (int)(k0 + dchunk * 16) < K;
-    const __amdgpu_buffer_rsrc_t src =
-        op == 0 ? (next ? nxt.a : cur.a) : (next ? nxt.b : cur.b);
+    return DmaSrc{op == 0 ? (next ? nxt.a : cur.a) : (next ? nxt.b : cur.b), k0,
+                  (int)(k0 + dchunk * 16) < K};
+  };
+  // Instruction qq (0..3) of the group.
+  auto dma_one = [&](const DmaSrc& d, int stage, int op, int hi, int qq) {
+    const int q = (qq & 1) + 4 * (qq >> 1) + 2 * hi;
+    if (op == 0)
+      dma16(d.src, lds + Cfg::kABase + stage * Cfg::kAStage + (4 * q + wave) * 1024,
+            d.ok ? voff_a[q] : kOobOffset, d.k0);
+    else
+      dma16(d.src, lds + Cfg::kBBase + stage * Cfg::kBStage + (4 * q + wave) * 1024,
+            d.ok ? voff_b[q] : kOobOffset, d.k0);
+  };
+  auto dma_group = [&](int kb, int stage, int op, int hi) {
+    const DmaSrc d = dma_src(kb, op);
 #pragma unroll
-    for (int qq = 0; qq < kDmaPerGroup; ++qq) {
-      const int q = (qq & 1) + 4 * (qq >> 1) + 2 * hi;
-      if (op == 0)
-        dma16(src, lds + Cfg::kABase + stage * Cfg::kAStage + (4 * q + wave) * 1024,
-              ok ? voff_a[q] : kOobOffset, k0);
-      else
-        dma16(src, lds + Cfg::kBBase + stage * Cfg::kBStage + (4 * q + wave) * 1024,
-              ok ? voff_b[q] : kOobOffset, k0);
-    }
+    for (int qq = 0; qq < kDmaPerGroup; ++qq) dma_one(d, stage, op, hi, qq);
+  };
+
+  // kRowCol: the wave's 128 row scales and 128 column scales of tile t, by
+  // DMA into the first 1 KiB of its epilogue stage (rows at +0, columns at
+  // +512), one float per lane (4 loads; rows past M or columns past N read
+  // zero).  Issued at the tile's first barrier, when the previous epilogue's
+  // LDS reads are done; retired by the K loop's own vmcnt waits, so the
+  // epilogue only reads LDS (a load issued there would retire behind the
+  // next tile's prefetch).  A null vector gets an empty range (every lane
+  // reads zero); the epilogue uses 1.0 for it.
+  // The vectors' addresses are reloaded from the kernel arguments (the
+  // kernel's only argument is the GemmArgs) and the lane index goes through
+  // an opaque copy, so that nothing here is hoisted out of the tile loop:
+  // values held across the K loop change how it is scheduled (measured 1-2 %
+  // slower).
+  auto scale_dma = [&](int tile) {
+    const TileCoord sc = grouped_tile(tile, tiles_m, tiles_n, g.group_m);
+    const float* pa = kernel_args()->scale_a;
+    const float* pb = kernel_args()->scale_b;
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    lds_u8* dst = lds + Cfg::kStoreBase + wave * Cfg::kStoreStage;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(pa, pa ? (uint32_t)M * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(pb, pb ? (uint32_t)N * 4u : 0u);
+    const uint32_t ro = (uint32_t)(sc.m * Cfg::kBM + wm * 128 + ln) * 4u;
+    const uint32_t co = (uint32_t)(sc.n * Cfg::kBN + wn * 128 + ln) * 4u;
+    dma4(ra, dst, ro);
+    dma4(ra, dst + 256, ro + 256);
+    dma4(rb, dst + 512, co);
+    dma4(rb, dst + 768, co + 256);
   };
 
   i32x8 fa[4][2], fb[4][2];  // 32x32x64: [32-row fragment][K-half]
   i32x8 fa16[8], fb16[8];    // 16x16x128: [16-row fragment]
   // Register tile (op, hi) of `stage`: rows 64hi .. 64hi + 63 of the wave's
   // 128 A (op 0) or B (op 1) rows, all 128 K-bytes.
+  // 16x16x128: read n (0..7) of register tile (op, hi): fragment
+  // 4 hi + n / 2, K-half n % 2.
+  auto read16_one = [&](int op, int hi, int stage, int n) -> i32x4 {
+    const int f = 4 * hi + n / 2;
+    if (op == 0)
+      return lds_read16(pa16[n % 2] + stage * Cfg::kAStage + f * 16 * Cfg::kBK);
+    return lds_read16(pb16[n % 2] + stage * Cfg::kBStage + f * 16 * Cfg::kBK);
+  };
   auto read_tile = [&](int op, int hi, int stage) {
     if constexpr (k16) {
 #pragma unroll
@@ -332,6 +467,55 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // epilogue reads the accumulators).
   auto last_tail = [&]() { quarter_mfma(1, 1, QS::kHead, QS::kMfma); };
 
+  // One quarter-step: the previous quarter's tail MFMA (quarter tq) if
+  // `tail`, the head MFMA of quarter q, the LDS reads of register tile
+  // (rop, rhi) of stage rst, and DMA group (dop, dhi) of step kb into stage
+  // dst, in the order of quarter_schedule.  The scheduler follows that
+  // pattern for the per-tensor instantiations, but for the row/column one
+  // it clustered the DMAs and the reads instead (4 % slower): there the
+  // order is written out, one scheduling region per pair.  (Written out for
+  // the per-tensor path too, it measured 0.6 % slower than the scheduler's
+  // own placement of the address arithmetic.)
+  auto quarter = [&](bool tail, int tqi, int tqj, int qi, int qj, int rop,
+                     int rhi, int rst, int kb, int dst, int dop, int dhi) {
+    if constexpr (k16 && kRowCol) {
+      if (tail) quarter_mfma(tqi, tqj, QS::kHead, QS::kMfma);
+      const DmaSrc d = dma_src(kb, dop);
+      sched_fence();
+      i32x4 rd[8];
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        quarter_mfma(qi, qj, n, n + 1);
+        rd[n] = read16_one(rop, rhi, rst, n);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        sched_fence();
+      }
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        quarter_mfma(qi, qj, 8 + n, 9 + n);
+        dma_one(d, dst, dop, dhi, n);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        sched_fence();
+      }
+      quarter_mfma(qi, qj, 12, QS::kHead);
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        if (rop == 0)
+          fa16[4 * rhi + f] = join(rd[2 * f], rd[2 * f + 1]);
+        else
+          fb16[4 * rhi + f] = join(rd[2 * f], rd[2 * f + 1]);
+      }
+    } else {
+      if (tail) quarter_mfma(tqi, tqj, QS::kHead, QS::kMfma);
+      quarter_mfma(qi, qj, 0, QS::kHead);
+      read_tile(rop, rhi, rst);
+      dma_group(kb, dst, dop, dhi);
+      quarter_schedule<kMf>(tail);
+    }
+  };
+
   // Two pipeline steps kt0, kt0 + 1 (stages 0, 1).  kFirst: the tile's first
   // two steps, whose first three barriers wait past the previous tile's
   // epilogue stores.
@@ -353,32 +537,21 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       const bool tail = !(kFirst && s == 0);
       wait_lgkmcnt<0>();
       if (kFirst) wait_vmcnt<kWaitAfterStores>(); else wait_vmcnt<kWaitSteady>();
+      // After the wait (which counts only older operations): the four
+      // loads at most make the tile's next two waits retire four more
+      // stores.
+      if constexpr (kRowCol && kFirst)
+        if (s == 0) scale_dma(t);
       barrier();  // Q00
-      if (tail) quarter_mfma(1, 1, QS::kHead, QS::kMfma);
-      quarter_mfma(0, 0, 0, QS::kHead);
-      read_tile(1, 1, s);
-      dma_group(kt + 2, s, 0, 0);
-      quarter_schedule<kMf>(tail);
+      quarter(tail, 1, 1, 0, 0, 1, 1, s, kt + 2, s, 0, 0);
       wait_lgkmcnt<0>();  // Q01
-      quarter_mfma(0, 0, QS::kHead, QS::kMfma);
-      quarter_mfma(0, 1, 0, QS::kHead);
-      read_tile(0, 1, s);
-      dma_group(kt + 2, s, 1, 0);
-      quarter_schedule<kMf>(true);
+      quarter(true, 0, 0, 0, 1, 0, 1, s, kt + 2, s, 1, 0);
       wait_lgkmcnt<0>();
       if (kFirst && s == 0) wait_vmcnt<kWaitAfterStores>(); else wait_vmcnt<kWaitSteady>();
       barrier();  // Q10
-      quarter_mfma(0, 1, QS::kHead, QS::kMfma);
-      quarter_mfma(1, 0, 0, QS::kHead);
-      read_tile(0, 0, s ^ 1);
-      dma_group(kt + 2, s, 1, 1);
-      quarter_schedule<kMf>(true);
+      quarter(true, 0, 1, 1, 0, 0, 0, s ^ 1, kt + 2, s, 1, 1);
       wait_lgkmcnt<0>();  // Q11
-      quarter_mfma(1, 0, QS::kHead, QS::kMfma);
-      quarter_mfma(1, 1, 0, QS::kHead);
-      read_tile(1, 0, s ^ 1);
-      dma_group(kt + 2, s, 0, 1);
-      quarter_schedule<kMf>(true);
+      quarter(true, 1, 0, 1, 1, 1, 0, s ^ 1, kt + 2, s, 0, 1);
     }
   };
 
@@ -451,6 +624,22 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
         (uint32_t)(((rows_c - 1) * g.ldc + Cfg::kBN) * 2));
     const int rows_left = M - tc.m * Cfg::kBM - wm * 128;  // from wave row 0
     const int cols_left = N - tc.n * Cfg::kBN - wn * 128;  // from wave col 0
+    // Scale of element e of 16 x 16 block (bi, bj).  Row / column scales
+    // come from the wave's stage (scale_dma), read before the staging of C
+    // overwrites them.
+    RowColScales<8, 8> rcs;
+    if constexpr (kRowCol) {
+      const float* pa = kernel_args()->scale_a;
+      const float* pb = kernel_args()->scale_b;
+      rcs.read_lds(lds + Cfg::kStoreBase + wave * Cfg::kStoreStage,
+                   pa != nullptr, pb != nullptr, elane);
+    }
+    auto sc16 = [&](int bi, int bj, int e) -> float {
+      if constexpr (kRowCol)
+        return rcs.at(bi, bj, e);
+      else
+        return scale;
+    };
 
     if constexpr (kVecStore) {
       // 32 rows (one accumulator block row i) at a time through the wave's
@@ -493,12 +682,13 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
         // stores instead of waiting for them.
         const int wr = elane & 15, wg = elane >> 4;
         auto write_blk = [&](int i, int ii, int j) {
-          const f32x4& a = acc16[2 * i + ii][j];
+          const int bi = 2 * i + ii;
+          const f32x4& a = acc16[bi][j];
           lds_write8(stg + (16 * ii + wr) * 256 + (((4 * j + wg) ^ (2 * wr)) * 8),
-                     u32x2{pack_bf16x2(acc_read(a[0]) * scale,
-                                       acc_read(a[1]) * scale),
-                           pack_bf16x2(acc_read(a[2]) * scale,
-                                       acc_read(a[3]) * scale)});
+                     u32x2{pack_bf16x2(acc_read(a[0]) * sc16(bi, j, 0),
+                                       acc_read(a[1]) * sc16(bi, j, 1)),
+                           pack_bf16x2(acc_read(a[2]) * sc16(bi, j, 2),
+                                       acc_read(a[3]) * sc16(bi, j, 3))});
         };
         auto store_one = [&](int i, int p, const i32x4& v) {
           int row4 = 32 * i + 4 * p;
@@ -590,8 +780,10 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
           for (int j = 0; j < 8; ++j) {
             const int c = 16 * j + 4 * (elane >> 4);
             const f32x4& a = acc16[i][j];
-            const u32x2 v{pack_bf16x2(acc_read(a[0]) * scale, acc_read(a[1]) * scale),
-                          pack_bf16x2(acc_read(a[2]) * scale, acc_read(a[3]) * scale)};
+            const u32x2 v{pack_bf16x2(acc_read(a[0]) * sc16(i, j, 0),
+                                      acc_read(a[1]) * sc16(i, j, 1)),
+                          pack_bf16x2(acc_read(a[2]) * sc16(i, j, 2),
+                                      acc_read(a[3]) * sc16(i, j, 3))};
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const uint32_t w = (r < 2 ? v.x : v.y) >> (16 * (r & 1));

@@ -64,7 +64,9 @@ static_assert(Cfg8w::kLdsBytes == 160 * 1024, "LDS budget");
 static_assert(8 * Cfg8w::kStoreStage <= Cfg8w::kAStages * Cfg8w::kAStage,
               "epilogue staging fits the A stages");
 
-template <bool kVecStore>
+// kRowCol: per-row / per-column scales (RowColScales) instead of the
+// per-tensor pair.
+template <bool kVecStore, bool kRowCol = false>
 __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) {
   using Cfg = Cfg8w;
   const int lane = lane_id();
@@ -80,8 +82,8 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
                                     : (int)gridDim.x;
   if ((int)blockIdx.x >= workers) return;
 
-  const float sa = g.scale_a ? *g.scale_a : 1.0f;
-  const float sb = g.scale_b ? *g.scale_b : 1.0f;
+  const float sa = !kRowCol && g.scale_a ? *g.scale_a : 1.0f;
+  const float sb = !kRowCol && g.scale_b ? *g.scale_b : 1.0f;
   const float scale = sa * sb;
 
   // DMA lane geometry: instruction q covers operand rows 8q .. 8q + 7; lane l
@@ -231,9 +233,24 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
         (uint32_t)(((rows_c - 1) * g.ldc + Cfg::kBN) * 2));
     const int rows_left = M - tc.m * Cfg::kBM - wm * 128;
     const int cols_left = N - tc.n * Cfg::kBN - wn * 64;
-    auto cvt = [&](const f32x4& v) {
-      return u32x2{pack_bf16x2(acc_read(v[0]) * scale, acc_read(v[1]) * scale),
-                   pack_bf16x2(acc_read(v[2]) * scale, acc_read(v[3]) * scale)};
+    RowColScales<8, 4> rcs;
+    if constexpr (kRowCol) {
+      rcs.load(g, tc.m * Cfg::kBM + wm * 128, tc.n * Cfg::kBN + wn * 64, elane);
+      wait_vmcnt<0>();
+    }
+    auto sc16 = [&](int bi, int bj, int e) -> float {
+      if constexpr (kRowCol)
+        return rcs.at(bi, bj, e);
+      else
+        return scale;
+    };
+    // block (bi, bj) of the wave's 8 x 4, scaled and rounded
+    auto cvt = [&](int bi, int bj) {
+      const f32x4& v = acc[bi][bj];
+      return u32x2{pack_bf16x2(acc_read(v[0]) * sc16(bi, bj, 0),
+                               acc_read(v[1]) * sc16(bi, bj, 1)),
+                   pack_bf16x2(acc_read(v[2]) * sc16(bi, bj, 2),
+                               acc_read(v[3]) * sc16(bi, bj, 3))};
     };
     if constexpr (kVecStore) {
       // Staging: row r (0..31) at 128 r; 8-byte piece x (0..15) at slot
@@ -254,7 +271,7 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
 #pragma unroll
           for (int j = 0; j < 4; ++j)
             lds_write8(stg + r * 128 + (((4 * j + wg) ^ (r & 14)) * 8),
-                       cvt(acc[2 * c + ii][j]));
+                       cvt(2 * c + ii, j));
           sched_fence();
         }
         compiler_fence();
@@ -288,7 +305,7 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int col = 16 * j + 4 * (elane >> 4);
-          const u32x2 v = cvt(acc[i][j]);
+          const u32x2 v = cvt(i, j);
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const uint32_t w = (q < 2 ? v.x : v.y) >> (16 * (q & 1));

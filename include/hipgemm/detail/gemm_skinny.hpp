@@ -60,9 +60,54 @@ struct CfgSkinny {
   static constexpr int partial_floats() { return kMB * 16 * kBN; }
 };
 
+// Scales of the C elements one lane writes: rows 16 m + l % 16 (m <
+// kRows) and columns col0 + 16 f + 4 (l / 16) + i (f, i < 4).  Per-tensor:
+// the product of the two scalars; kRowCol: scale_a holds M floats, scale_b N
+// floats (null = 1.0), the element scale is row scale times column scale, one
+// fp32 product.  Rows or columns past M or N get 0 (never stored).
+template <int kRows, bool kRowCol>
+struct SkinnyScales {
+  float s = 1.0f;
+  float r[kRowCol ? kRows : 1];
+  float c[kRowCol ? 4 : 1][4];
+  __device__ __forceinline__ void load(const SkinnyArgs& g, int m0, int col0,
+                                       int lane) {
+    if constexpr (!kRowCol) {
+      const float sa = g.scale_a ? *g.scale_a : 1.0f;
+      const float sb = g.scale_b ? *g.scale_b : 1.0f;
+      s = sa * sb;
+    } else {
+      const int r16 = lane & 15, c4 = 4 * (lane >> 4);
+      const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.scale_a, (uint32_t)g.M * 4);
+      const __amdgpu_buffer_rsrc_t rb = make_rsrc(g.scale_b, (uint32_t)g.N * 4);
+#pragma unroll
+      for (int m = 0; m < kRows; ++m)
+        r[m] = g.scale_a ? __builtin_bit_cast(
+                               float, __builtin_amdgcn_raw_buffer_load_b32(
+                                          ra, (uint32_t)(16 * (m0 + m) + r16) * 4u, 0, 0))
+                         : 1.0f;
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          c[f][i] = g.scale_b ? __builtin_bit_cast(
+                                    float, __builtin_amdgcn_raw_buffer_load_b32(
+                                               rb, (uint32_t)(col0 + 16 * f + c4 + i) * 4u, 0, 0))
+                              : 1.0f;
+    }
+  }
+  __device__ __forceinline__ float at(int m, int f, int i) const {
+    if constexpr (kRowCol)
+      return r[m] * c[f][i];
+    else
+      return s;
+  }
+};
+
 // kMB: 16-row blocks of M (M <= 16 kMB).  kVec8: C rows allow 8-byte stores
-// (N % 4 == 0, ldc % 4 == 0, C 8-byte aligned).
-template <int kMB, bool kVec8>
+// (N % 4 == 0, ldc % 4 == 0, C 8-byte aligned).  kRowCol: per-row /
+// per-column scales (SkinnyScales).
+template <int kMB, bool kVec8, bool kRowCol = false>
 __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   using Cfg = CfgSkinny;
   // A (at most 128 rows) is shared by the four waves: up to 32 rows each
@@ -245,9 +290,8 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   }
 
   // ---- last arrival: sum the slices in order, scale, bf16, store ----------
-  const float sa = g.scale_a ? *g.scale_a : 1.0f;
-  const float sb = g.scale_b ? *g.scale_b : 1.0f;
-  const float scale = sa * sb;
+  SkinnyScales<kMB, kRowCol> scl;
+  scl.load(g, 0, n0 + wave * 64, lane);
   const __amdgpu_buffer_rsrc_t rsrc_c =
       make_rsrc(g.C + n0, (uint32_t)(((M - 1) * g.ldc + rows_b) * 2));
   auto oob_unless = [](int x, int limit) -> uint32_t {
@@ -280,13 +324,18 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
                            rsrc_p, slot(m, f),
                            (uint32_t)min(q0 + u, g.slices - 1) * stride,
                            kCoherent));
+      // Slices past the last (their loads re-read it) add +0, which leaves
+      // every sum unchanged (a sum started at +0 is never -0).  A branch
+      // here instead lets the compiler sink each load into its branch and
+      // wait for it alone.
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u)
-        if (q0 + u < g.slices)
+      for (int u = 0; u < kBatch; ++u) {
+        const bool live = q0 + u < g.slices;
 #pragma unroll
-          for (int m = 0; m < kMB; ++m)
+        for (int m = 0; m < kMB; ++m)
 #pragma unroll
-            for (int f = 0; f < 4; ++f) sum[m][f] += v[u][m][f];
+          for (int f = 0; f < 4; ++f) sum[m][f] += live ? v[u][m][f] : f32x4{};
+      }
     }
   }
 #pragma unroll
@@ -299,8 +348,10 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
       const int col = wave * 64 + 16 * f + 4 * grp;
       const uint32_t base = (uint32_t)((row * g.ldc + col) * 2) |
                             oob_unless(row, M);
-      const uint32_t lo = pack_bf16x2(sum[m][f][0] * scale, sum[m][f][1] * scale);
-      const uint32_t hi = pack_bf16x2(sum[m][f][2] * scale, sum[m][f][3] * scale);
+      const uint32_t lo = pack_bf16x2(sum[m][f][0] * scl.at(m, f, 0),
+                                      sum[m][f][1] * scl.at(m, f, 1));
+      const uint32_t hi = pack_bf16x2(sum[m][f][2] * scl.at(m, f, 2),
+                                      sum[m][f][3] * scl.at(m, f, 3));
       if constexpr (kVec8) {
         __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc_c,
                                               base | oob_unless(col, rows_b), 0, 0);
@@ -325,7 +376,7 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
 // the in-kernel reduction, spread over tiles_n x kMB workgroups instead of
 // one per tile.  Launched on the same stream right after the split kernel,
 // so its partial tiles are visible without any fence.
-template <bool kVec8>
+template <bool kVec8, bool kRowCol = false>
 __device__ __forceinline__ void gemm_skinny_reduce_body(const SkinnyArgs& g,
                                                         int kmb) {
   using Cfg = CfgSkinny;
@@ -346,6 +397,10 @@ __device__ __forceinline__ void gemm_skinny_reduce_body(const SkinnyArgs& g,
   auto slot = [&](int f) {
     return (uint32_t)(((m * 4 + f) * Cfg::kThreads + wave * 64 + lane) * 16);
   };
+  // Scales first: their latency hides under the slice loads (read after the
+  // loop they cost this short kernel one more memory round trip).
+  SkinnyScales<1, kRowCol> scl;
+  scl.load(g, m, n0 + wave * 64, lane);
   constexpr int kBatch = 8;  // slices whose loads are in flight together
   f32x4 sum[4] = {};
   for (int q0 = 0; q0 < g.slices; q0 += kBatch) {
@@ -358,15 +413,14 @@ __device__ __forceinline__ void gemm_skinny_reduce_body(const SkinnyArgs& g,
             f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                        rsrc_p, slot(f),
                        (uint32_t)min(q0 + u, g.slices - 1) * stride, 0));
+    // As in gemm_skinny_body: +0 for slices past the last, not a branch.
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u)
-      if (q0 + u < g.slices)
+    for (int u = 0; u < kBatch; ++u) {
+      const bool live = q0 + u < g.slices;
 #pragma unroll
-        for (int f = 0; f < 4; ++f) sum[f] += v[u][f];
+      for (int f = 0; f < 4; ++f) sum[f] += live ? v[u][f] : f32x4{};
+    }
   }
-  const float sa = g.scale_a ? *g.scale_a : 1.0f;
-  const float sb = g.scale_b ? *g.scale_b : 1.0f;
-  const float scale = sa * sb;
   const __amdgpu_buffer_rsrc_t rsrc_c =
       make_rsrc(g.C + n0, (uint32_t)(((M - 1) * g.ldc + rows_b) * 2));
   auto oob_unless = [](int x, int limit) -> uint32_t {
@@ -377,8 +431,10 @@ __device__ __forceinline__ void gemm_skinny_reduce_body(const SkinnyArgs& g,
     const int row = 16 * m + r16;
     const int col = wave * 64 + 16 * f + 4 * grp;
     const uint32_t base = (uint32_t)((row * g.ldc + col) * 2) | oob_unless(row, M);
-    const uint32_t lo = pack_bf16x2(sum[f][0] * scale, sum[f][1] * scale);
-    const uint32_t hi = pack_bf16x2(sum[f][2] * scale, sum[f][3] * scale);
+    const uint32_t lo = pack_bf16x2(sum[f][0] * scl.at(0, f, 0),
+                                    sum[f][1] * scl.at(0, f, 1));
+    const uint32_t hi = pack_bf16x2(sum[f][2] * scl.at(0, f, 2),
+                                    sum[f][3] * scl.at(0, f, 3));
     if constexpr (kVec8) {
       __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc_c,
                                             base | oob_unless(col, rows_b), 0, 0);

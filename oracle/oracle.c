@@ -232,9 +232,12 @@ static void block_acc(const uint8_t *A, const float *Bt, const int *rows,
   }
 }
 
+/* mode 0: bf16 of acc * s, or, with sa / sb given (row / column scale
+ * vectors, either may be NULL = 1.0), of acc * (sa[row] * sb[col]); mode 1:
+ * the fp32 acc itself. */
 static void rows_impl(const uint8_t *A, const float *Bt, const int *rows,
                       int nrows, int N, int K, int lda, void *out, int ldo,
-                      int mode, float s) {
+                      int mode, float s, const float *sa, const float *sb) {
   const int nrb = (nrows + RB - 1) / RB, ncb = (N + CB - 1) / CB;
 #pragma omp parallel for collapse(2) schedule(dynamic, 1)
   for (int rb = 0; rb < nrb; ++rb) {
@@ -247,10 +250,15 @@ static void rows_impl(const uint8_t *A, const float *Bt, const int *rows,
       for (int r = 0; r < nr; ++r)
         for (int j = 0; j < nc; ++j) {
           const size_t o = (size_t)(r0 + r) * ldo + n0 + j;
-          if (mode == 0)
+          if (mode == 0 && (sa || sb)) {
+            const float rs = sa ? sa[rows[r0 + r]] : 1.0f;
+            const float cs = sb ? sb[n0 + j] : 1.0f;
+            ((uint16_t *)out)[o] = epilogue(acc[r][j], rs * cs);
+          } else if (mode == 0) {
             ((uint16_t *)out)[o] = epilogue(acc[r][j], s);
-          else
+          } else {
             ((float *)out)[o] = acc[r][j];
+          }
         }
     }
   }
@@ -263,7 +271,21 @@ void hg_gemm_fast(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
   int *rows = (int *)malloc((size_t)(M > 0 ? M : 1) * sizeof(int));
   if (!Bt || !rows) abort();
   for (int i = 0; i < M; ++i) rows[i] = i;
-  rows_impl(A, Bt, rows, M, N, K, lda, C, ldc, 0, scale_a * scale_b);
+  rows_impl(A, Bt, rows, M, N, K, lda, C, ldc, 0, scale_a * scale_b, NULL,
+            NULL);
+  free(rows);
+  free(Bt);
+}
+
+void hg_gemm_rowcol(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
+                    int N, int K, int lda, int ldb, int ldc,
+                    const float *scale_rows, const float *scale_cols) {
+  float *Bt = decode_bt(B_T, N, K, ldb);
+  int *rows = (int *)malloc((size_t)(M > 0 ? M : 1) * sizeof(int));
+  if (!Bt || !rows) abort();
+  for (int i = 0; i < M; ++i) rows[i] = i;
+  rows_impl(A, Bt, rows, M, N, K, lda, C, ldc, 0, 1.0f, scale_rows,
+            scale_cols);
   free(rows);
   free(Bt);
 }
@@ -273,7 +295,8 @@ void hg_gemm_rows(const uint8_t *A, const uint8_t *B_T, uint16_t *C_rows,
                   float scale_a, float scale_b) {
   float *Bt = decode_bt(B_T, N, K, ldb);
   if (!Bt) abort();
-  rows_impl(A, Bt, rows, nrows, N, K, lda, C_rows, N, 0, scale_a * scale_b);
+  rows_impl(A, Bt, rows, nrows, N, K, lda, C_rows, N, 0, scale_a * scale_b,
+            NULL, NULL);
   free(Bt);
 }
 
@@ -282,7 +305,7 @@ void hg_gemm_rows_acc(const uint8_t *A, const uint8_t *B_T, float *acc_rows,
                       int ldb) {
   float *Bt = decode_bt(B_T, N, K, ldb);
   if (!Bt) abort();
-  rows_impl(A, Bt, rows, nrows, N, K, lda, acc_rows, N, 1, 1.0f);
+  rows_impl(A, Bt, rows, nrows, N, K, lda, acc_rows, N, 1, 1.0f, NULL, NULL);
   free(Bt);
 }
 

@@ -83,6 +83,18 @@ void hg_gemm_ref(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
 void hg_gemm_fast(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
                   int N, int K, int lda, int ldb, int ldc, float scale_a,
                   float scale_b);
+/* Per-row / per-column scales (an extension, like the per-tensor ones):
+ *   C[m, n] = bf16_rne(acc[m, n] * (scale_rows[m] * scale_cols[n]))
+ * with acc the same fp32 sequential-K sum as hg_gemm_fast and the product of
+ * the two scales formed in fp32 first.  Either vector may be NULL (1.0).
+ * Pinned by reduction to the pinned per-tensor path: constant vectors equal
+ * hg_gemm_fast with those two scalars; each row with a row scale equals
+ * hg_gemm_rows with that scale_a; column scales likewise through the
+ * transposed product (tests/test_oracle.py). */
+void hg_gemm_rowcol(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
+                    int N, int K, int lda, int ldb, int ldc,
+                    const float *scale_rows, const float *scale_cols);
+
 /* Same as hg_gemm_fast for the listed rows only: output row r of C_rows
  * (row-major, ld = N) is row rows[r] of the full product. */
 void hg_gemm_rows(const uint8_t *A, const uint8_t *B_T, uint16_t *C_rows,

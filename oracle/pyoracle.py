@@ -71,6 +71,9 @@ class Oracle:
         for name in ("hg_gemm_ref", "hg_gemm_fast"):
             getattr(L, name).argtypes = gemm_args
             getattr(L, name).restype = None
+        L.hg_gemm_rowcol.argtypes = [_vp, _vp, _vp] + [ctypes.c_int] * 6 + \
+            [_vp, _vp]
+        L.hg_gemm_rowcol.restype = None
         L.hg_gemm_rows.argtypes = [_vp, _vp, _vp, _vp] + [ctypes.c_int] * 5 + \
             [ctypes.c_float] * 2
         L.hg_gemm_rows.restype = None
@@ -137,6 +140,26 @@ class Oracle:
         C = np.empty((M, N), np.uint16)
         fn = self.lib.hg_gemm_ref if faithful else self.lib.hg_gemm_fast
         fn(_ptr(A), _ptr(B), _ptr(C), M, N, K, K, K, N, scale_a, scale_b)
+        return C
+
+    def gemm_rowcol(self, A: np.ndarray, B: np.ndarray,
+                    scale_rows: Optional[np.ndarray] = None,
+                    scale_cols: Optional[np.ndarray] = None) -> np.ndarray:
+        """bf16 bits of (scale_rows[m] * scale_cols[n]) * (A @ B.T)[m, n];
+        either vector may be None (1.0)."""
+        A = np.ascontiguousarray(A)
+        B = np.ascontiguousarray(B)
+        M, K = A.shape
+        N = B.shape[0]
+        assert B.shape[1] == K
+        sr = None if scale_rows is None else np.ascontiguousarray(scale_rows, np.float32)
+        sc = None if scale_cols is None else np.ascontiguousarray(scale_cols, np.float32)
+        assert sr is None or sr.shape == (M,)
+        assert sc is None or sc.shape == (N,)
+        C = np.empty((M, N), np.uint16)
+        self.lib.hg_gemm_rowcol(_ptr(A), _ptr(B), _ptr(C), M, N, K, K, K, N,
+                                None if sr is None else _ptr(sr),
+                                None if sc is None else _ptr(sc))
         return C
 
     def gemm_rows(self, A: np.ndarray, B: np.ndarray, rows: Sequence[int],

@@ -104,6 +104,34 @@ def test_workspace_size_and_validation():
                           0, 0) == 0                             # empty: no-op
 
 
+def test_rowcol_entry_validation():
+    """The per-row / per-column entry point: the common argument checks, plus
+    4-byte aligned vectors and no 32x32x64 schedule; NULL vectors are
+    accepted (all ones) and empty problems are no-ops."""
+    base = dict(A=FAKE, B=FAKE, C=FAKE, M=300, N=300, K=64, lda=64, ldb=64,
+                ldc=300, rows=FAKE, cols=FAKE, variant=0)
+
+    def call(**kw):
+        p = dict(base)
+        p.update(kw)
+        return hg.gemm_raw_rowcol(p["A"], p["B"], p["C"], p["M"], p["N"],
+                                  p["K"], p["lda"], p["ldb"], p["ldc"],
+                                  p["rows"], p["cols"], p["variant"], 0, 0, 0)
+
+    for bad in (dict(rows=FAKE + 2), dict(cols=FAKE + 1),
+                dict(variant=hg.VARIANTS["4wave"]), dict(variant=5),
+                dict(K=40, lda=48, ldb=48), dict(ldc=299), dict(A=0),
+                dict(variant=hg.VARIANTS["skinny"])):  # M = 300 > 128
+        assert call(**bad) == INVALID, bad
+    assert call(M=0) == 0 and call(N=0, rows=FAKE + 2) == 0
+    args = (FAKE, FAKE, FAKE, 16, 8192, 8192, 8192, 8192, 8192, 0, 0,
+            hg.VARIANTS["skinny"])
+    need = hg.workspace_size(16, 8192, 8192, hg.VARIANTS["skinny"])
+    assert hg.gemm_raw_rowcol(*args, 0, need) == INVALID          # missing
+    assert hg.gemm_raw_rowcol(*args, FAKE, need - 256) == INVALID  # short
+    assert hg.gemm_raw_rowcol(*args, FAKE + 64, need) == INVALID   # misaligned
+
+
 def test_dropin_entry_validates_too():
     L = hg.lib()
     assert L.hipgemm_fp8_gemm_4wave_256x256x128(None, None, None, 64, 64, 64,

@@ -210,6 +210,38 @@ def test_gemm_scale_extension(oracle):
     assert np.array_equal(oracle.gemm(A, B, 1.0, 1.0), oracle.f32_to_bf16(acc))
 
 
+def test_gemm_rowcol_reduces_to_per_tensor(oracle):
+    """Per-row / per-column scales, pinned by reduction to the per-tensor path
+    (itself pinned against the reference's gemm_cpu):
+    * constant vectors equal the two scalars;
+    * element (m, n) equals the per-tensor product with scale_a = sr[m],
+      scale_b = sc[n] (the scale product is formed first, in fp32);
+    * column scales are row scales of the transposed product (same products,
+      same K order, so the same fp32 sums)."""
+    M, N, K = 37, 45, 208
+    A, B = _inputs(oracle, M, N, K, 31)
+    rng = np.random.default_rng(31)
+    sr = rng.uniform(0.25, 4.0, M).astype(np.float32)
+    sc = rng.uniform(0.25, 4.0, N).astype(np.float32)
+    assert np.array_equal(
+        oracle.gemm_rowcol(A, B, np.full(M, 1.7, np.float32),
+                           np.full(N, 0.6, np.float32)),
+        oracle.gemm(A, B, float(np.float32(1.7)), float(np.float32(0.6))))
+    assert np.array_equal(oracle.gemm_rowcol(A, B), oracle.gemm(A, B))
+    C = oracle.gemm_rowcol(A, B, sr, sc)
+    for m in (0, 5, 36):
+        for n in (0, 11, 44):
+            one = oracle.gemm_rows(A, B, [m], float(sr[m]), float(sc[n]))
+            assert C[m, n] == one[0, n], (m, n)
+    Cr = oracle.gemm_rowcol(A, B, sr, None)
+    for m in (0, 20, 36):
+        assert np.array_equal(Cr[m], oracle.gemm_rows(A, B, [m], float(sr[m]))[0])
+    Cc = oracle.gemm_rowcol(A, B, None, sc)
+    assert np.array_equal(Cc, oracle.gemm_rowcol(B, A, sc, None).T)
+    # a wrong column index (here the vector reversed) is caught
+    assert not np.array_equal(C, oracle.gemm_rowcol(A, B, sr, sc[::-1].copy()))
+
+
 def test_gemm_rows_subset(oracle):
     M, N, K = 50, 70, 192
     A, B = _inputs(oracle, M, N, K, 8)
