@@ -30,7 +30,8 @@ __all__ = [
     "fp8_gemm_4wave_256x256x128", "gemm_raw", "select_variant",
     "variant_name", "version", "tile_order", "lds_slot", "VARIANTS",
     "declared_symbols", "gemm_raw_ws", "workspace_size",
-    "fp8_gemm_bf16_rowcol", "gemm_raw_rowcol",
+    "fp8_gemm_bf16_rowcol", "gemm_raw_rowcol", "GemmDesc", "gemm_desc_raw",
+    "gemm", "FMT_E4M3", "FMT_E5M2", "OUT_BF16", "OUT_F16", "ACTIVATIONS",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -40,8 +41,41 @@ _HEADER = os.path.join(_ROOT, "include", "hipgemm.h")
 
 VARIANTS = {"auto": 0, "4wave": 1, "4wave_mfma16": 2, "skinny": 3, "8wave": 4}
 
+# include/hipgemm.h codes
+FMT_E4M3, FMT_E5M2 = 0, 1
+OUT_BF16, OUT_F16 = 0, 1
+ACTIVATIONS = {None: 0, "none": 0, "relu": 1, "gelu_tanh": 2, "silu": 3}
+
 hipSuccess = 0
 hipErrorInvalidValue = 1
+
+
+class GemmDesc(ctypes.Structure):
+    """hipgemm_gemm_desc (include/hipgemm.h)."""
+    _fields_ = [("size", ctypes.c_size_t),
+                ("A", ctypes.c_void_p), ("B_T", ctypes.c_void_p),
+                ("C", ctypes.c_void_p),
+                ("M", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int),
+                ("lda", ctypes.c_int), ("ldb", ctypes.c_int),
+                ("ldc", ctypes.c_int),
+                ("a_format", ctypes.c_int), ("b_format", ctypes.c_int),
+                ("out_dtype", ctypes.c_int), ("activation", ctypes.c_int),
+                ("scale_a", ctypes.c_void_p), ("scale_b", ctypes.c_void_p),
+                ("scale_rows", ctypes.c_void_p),
+                ("scale_cols", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+                ("variant", ctypes.c_int),
+                ("workspace", ctypes.c_void_p),
+                ("workspace_bytes", ctypes.c_size_t)]
+
+    def __init__(self, **kw):
+        super().__init__()
+        self.size = ctypes.sizeof(GemmDesc)
+        for k, v in kw.items():
+            setattr(self, k, v or (None if k in _PTR_FIELDS else 0))
+
+
+_PTR_FIELDS = {"A", "B_T", "C", "scale_a", "scale_b", "scale_rows",
+               "scale_cols", "bias", "workspace"}
 
 
 class HipGemmError(RuntimeError):
@@ -84,6 +118,8 @@ def lib() -> ctypes.CDLL:
                                                ci, vp, vp, ci, vp,
                                                ctypes.c_size_t, vp]
     L.hipgemm_fp8_gemm_bf16_rowcol.restype = ci
+    L.hipgemm_gemm.argtypes = [ctypes.POINTER(GemmDesc), vp]
+    L.hipgemm_gemm.restype = ci
     L.hipgemm_workspace_size.argtypes = [ci, ci, ci, ci]
     L.hipgemm_workspace_size.restype = ctypes.c_size_t
     L.hipgemm_fp8_gemm_4wave_256x256x128.argtypes = [vp, vp, vp, ci, ci, ci,
@@ -146,6 +182,11 @@ def gemm_raw_rowcol(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int,
         a_ptr or None, b_ptr or None, c_ptr or None, M, N, K, lda, ldb, ldc,
         rows_ptr or None, cols_ptr or None, variant, ws_ptr or None, ws_bytes,
         stream or None))
+
+
+def gemm_desc_raw(desc: "GemmDesc", stream: int = 0) -> int:
+    """Call hipgemm_gemm; returns hipError_t."""
+    return int(lib().hipgemm_gemm(ctypes.byref(desc), stream or None))
 
 
 def workspace_size(M: int, N: int, K: int, variant: int = 0) -> int:
@@ -276,6 +317,53 @@ def fp8_gemm_bf16(a, b_t, scale_a=None, scale_b=None, out=None,
                        stream.cuda_stream)
     _check(code, "hipgemm_fp8_gemm_bf16_ws")
     return out
+
+
+def gemm(a, b_t, *, a_format: int = FMT_E4M3, b_format: int = FMT_E4M3,
+         out_dtype=None, scale_a=None, scale_b=None, scale_rows=None,
+         scale_cols=None, bias=None, activation=None, out=None,
+         variant: int = 0, stream=None):
+    """The general entry point (hipgemm_gemm): out[m, n] =
+    round(act(fma(acc, scale_rows[m] * (scale_cols[n] * (scale_a *
+    scale_b)), bias[n]))), acc = a @ b_t.T with a in a_format and b_t in
+    b_format (FMT_E4M3 / FMT_E5M2; float8_e4m3fn / float8_e5m2 tensors set
+    it from their dtype).  out_dtype: torch.bfloat16 (default) or
+    torch.float16.  activation: None, "relu", "gelu_tanh" or "silu".
+    scale_a / scale_b: 1-element float32 device tensors; scale_rows (M),
+    scale_cols (N), bias (N): float32 device vectors; any may be None."""
+    torch = _torch()
+    fmts = {torch.float8_e4m3fn: FMT_E4M3, torch.float8_e5m2: FMT_E5M2}
+    a_format = fmts.get(a.dtype, a_format)
+    b_format = fmts.get(b_t.dtype, b_format)
+    out_dtype = out_dtype or (out.dtype if out is not None else torch.bfloat16)
+    if out_dtype not in (torch.bfloat16, torch.float16):
+        raise HipGemmError("out_dtype must be bfloat16 or float16",
+                           hipErrorInvalidValue)
+    if activation not in ACTIVATIONS:
+        raise HipGemmError(f"activation must be one of {sorted(k for k in ACTIVATIONS if k)}",
+                           hipErrorInvalidValue)
+    if out is None:
+        out = torch.empty((a.shape[0], b_t.shape[0]), dtype=out_dtype,
+                          device=a.device)
+    elif out.dtype != out_dtype:
+        raise HipGemmError("out has the wrong dtype", hipErrorInvalidValue)
+    a, b_t, out, M, N, K, lda, ldb, ldc, ws, nbytes, stream = _gemm_operands(
+        a.view(torch.uint8) if a.dtype == torch.float8_e5m2 else a,
+        b_t.view(torch.uint8) if b_t.dtype == torch.float8_e5m2 else b_t,
+        out.view(torch.bfloat16), variant, stream)
+    d = GemmDesc(A=a.data_ptr(), B_T=b_t.data_ptr(), C=out.data_ptr(), M=M,
+                 N=N, K=K, lda=lda, ldb=ldb, ldc=ldc, a_format=a_format,
+                 b_format=b_format,
+                 out_dtype=OUT_F16 if out_dtype == torch.float16 else OUT_BF16,
+                 activation=ACTIVATIONS[activation],
+                 scale_a=_scale_ptr(scale_a, "scale_a"),
+                 scale_b=_scale_ptr(scale_b, "scale_b"),
+                 scale_rows=_vector_ptr(scale_rows, M, "scale_rows"),
+                 scale_cols=_vector_ptr(scale_cols, N, "scale_cols"),
+                 bias=_vector_ptr(bias, N, "bias"), variant=variant,
+                 workspace=ws, workspace_bytes=nbytes)
+    _check(gemm_desc_raw(d, stream.cuda_stream), "hipgemm_gemm")
+    return out.view(out_dtype)
 
 
 def fp8_gemm_bf16_rowcol(a, b_t, scale_rows=None, scale_cols=None, out=None,

@@ -2,43 +2,28 @@
 //
 // Argument validation, variant selection and kernel launches over
 // hipLaunchKernel.  The kernels are the header schedules of
-// include/hipgemm/detail/, instantiated here with runtime shapes.
+// include/hipgemm/detail/, instantiated with runtime shapes in the k*.hip
+// files of this directory (kernels.hpp looks them up by configuration).
 #include "hipgemm.h"
 
 #include <atomic>
 #include <cstdint>
 
-#include "hipgemm/detail/gemm_8wave.hpp"
-#include "hipgemm/detail/gemm_skinny.hpp"
-#include "hipgemm/fp8_gemm.hpp"
+#include "kernels.hpp"
 
 namespace {
 
 using namespace hipgemm::detail;
+namespace hk = hipgemm::kernels;
 
-// kRowCol: per-row / per-column scale vectors instead of per-tensor scalars.
-template <bool kVecStore, int kMf, bool kRowCol>
-__global__ __launch_bounds__(256, 1) void k_fp8_gemm_4wave(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg4w::kLdsBytes];
-  gemm_4wave_body<kVecStore, kMf, kRowCol>(g, (lds_u8*)lds);
-}
-
-template <bool kVecStore, bool kRowCol>
-__global__ __launch_bounds__(512, 1) void k_fp8_gemm_8wave(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg8w::kLdsBytes];
-  gemm_8wave_body<kVecStore, kRowCol>(g, (lds_u8*)lds);
-}
-
-template <int kMB, bool kVec8, bool kRowCol>
-__global__ __launch_bounds__(256, 1) void k_fp8_gemm_skinny(SkinnyArgs g) {
-  gemm_skinny_body<kMB, kVec8, kRowCol>(g);
-}
-
-template <bool kVec8, bool kRowCol>
-__global__ __launch_bounds__(256, 1) void k_fp8_gemm_skinny_reduce(SkinnyArgs g,
-                                                                    int kmb) {
-  gemm_skinny_reduce_body<kVec8, kRowCol>(g, kmb);
-}
+static_assert(HIPGEMM_ACT_NONE == kActNone && HIPGEMM_ACT_RELU == kActRelu &&
+                  HIPGEMM_ACT_GELU_TANH == kActGeluTanh &&
+                  HIPGEMM_ACT_SILU == kActSilu,
+              "activation codes");
+static_assert(HIPGEMM_OUT_BF16 == kOutBf16 && HIPGEMM_OUT_F16 == kOutF16,
+              "output codes");
+static_assert(HIPGEMM_FMT_E4M3 == kFmtE4M3 && HIPGEMM_FMT_E5M2 == kFmtE5M2,
+              "format codes");
 
 // 32-bit buffer offsets: 256 rows of A or B_T (1-byte elements) span at most
 // 2^31 bytes, 256 rows of C (2-byte elements) likewise.
@@ -88,39 +73,38 @@ int cu_count() {
   return n;
 }
 
-template <int kMf, bool kRowCol>
-hipError_t launch_4wave(GemmArgs g, hipStream_t stream) {
-  // Persistent grid: one workgroup per CU at most (the kernel's 160 KiB of
-  // LDS allows no more), each walking tiles w, w + grid, ...
+// The tiled schedules (4-wave, 8-wave) on a persistent grid: one workgroup
+// per CU at most (their 160 KiB of LDS allows no more), each walking tiles
+// w, w + grid, ...  `key.vec` is set here: 16-byte epilogue stores need
+// 8-column groups that never straddle N and 16-byte aligned rows.
+hipError_t launch_tiled(int variant, GemmArgs g, hk::Key key,
+                        hipStream_t stream) {
   const int tiles = tiles_of(g.M, g.N);
   const int cus = cu_count();
   const int grid = tiles < cus ? tiles : cus;
   g.workers = grid;
-  // 16-byte epilogue stores need 8-column groups that never straddle N and
-  // 16-byte aligned rows.
-  const bool vec = (g.N % 8 == 0) && (g.ldc % 8 == 0) && aligned(g.C, 16);
+  key.vec = (g.N % 8 == 0) && (g.ldc % 8 == 0) && aligned(g.C, 16);
+  const void* fn = nullptr;
+  int threads = Cfg4w::kThreads;
+  switch (variant) {
+    case HIPGEMM_VARIANT_8WAVE:
+      fn = !key.ext ? hk::eight_wave_plain(key)
+           : key.out == HIPGEMM_OUT_F16 ? hk::eight_wave_ext_f16(key)
+                                        : hk::eight_wave_ext_bf16(key);
+      threads = Cfg8w::kThreads;
+      break;
+    case HIPGEMM_VARIANT_4WAVE:
+      fn = key.ext ? nullptr : hk::four_wave_plain(32, key);
+      break;
+    default:
+      fn = !key.ext ? hk::four_wave_plain(16, key)
+           : key.out == HIPGEMM_OUT_F16 ? hk::four_wave_ext_f16(key)
+                                        : hk::four_wave_ext_bf16(key);
+      break;
+  }
+  if (!fn) return hipErrorInvalidValue;  // no such instantiation
   void* args[] = {&g};
-  const void* fn =
-      vec ? reinterpret_cast<const void*>(&k_fp8_gemm_4wave<true, kMf, kRowCol>)
-          : reinterpret_cast<const void*>(&k_fp8_gemm_4wave<false, kMf, kRowCol>);
-  return hipLaunchKernel(fn, dim3(grid), dim3(Cfg4w::kThreads), args, 0,
-                         stream);
-}
-
-template <bool kRowCol>
-hipError_t launch_8wave(GemmArgs g, hipStream_t stream) {
-  // Same persistent grid as the 4-wave kernel (160 KiB of LDS: one
-  // workgroup per CU).
-  const int tiles = tiles_of(g.M, g.N);
-  const int cus = cu_count();
-  const int grid = tiles < cus ? tiles : cus;
-  g.workers = grid;
-  const bool vec = (g.N % 8 == 0) && (g.ldc % 8 == 0) && aligned(g.C, 16);
-  void* args[] = {&g};
-  const void* fn =
-      vec ? reinterpret_cast<const void*>(&k_fp8_gemm_8wave<true, kRowCol>)
-          : reinterpret_cast<const void*>(&k_fp8_gemm_8wave<false, kRowCol>);
-  return hipLaunchKernel(fn, dim3(grid), dim3(Cfg8w::kThreads), args, 0, stream);
+  return hipLaunchKernel(fn, dim3(grid), dim3(threads), args, 0, stream);
 }
 
 // Split-K plan of the skinny schedule: 16-row blocks of M, K-slices per
@@ -150,114 +134,133 @@ SkinnyPlan plan_skinny(int M, int N, int K) {
   return p;
 }
 
-template <int kMB, bool kRowCol>
-hipError_t launch_skinny_mb(const SkinnyArgs& g, bool vec8, int grid,
-                            hipStream_t stream) {
-  void* args[] = {const_cast<SkinnyArgs*>(&g)};
-  const void* fn =
-      vec8 ? reinterpret_cast<const void*>(&k_fp8_gemm_skinny<kMB, true, kRowCol>)
-           : reinterpret_cast<const void*>(&k_fp8_gemm_skinny<kMB, false, kRowCol>);
-  return hipLaunchKernel(fn, dim3(grid), dim3(CfgSkinny::kThreads), args, 0,
-                         stream);
-}
-
-template <bool kRowCol>
 hipError_t launch_skinny(const GemmArgs& a, const SkinnyPlan& p, void* ws,
-                         hipStream_t stream) {
+                         hk::Key key, hipStream_t stream) {
   // From 4 row blocks up, one workgroup per column tile summing every slice
   // (1 MiB of partials per tile at M = 128) is the long pole: a second
   // kernel sums them over tiles_n x kmb workgroups instead.
   const int reduce_pass = p.slices > 1 && p.kmb >= 4;
   SkinnyArgs g{a.A, a.B, a.C, a.scale_a, a.scale_b, a.M, a.N, a.K,
                a.lda, a.ldb, a.ldc, p.slices, p.slice_steps, nullptr, nullptr,
-               reduce_pass};
+               reduce_pass, a.epi};
   if (p.slices > 1) {
     g.arrivals = static_cast<int*>(ws);
     g.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + p.counter_bytes);
   }
-  const bool vec8 = (a.N % 4 == 0) && (a.ldc % 4 == 0) && aligned(a.C, 8);
+  // 8-byte stores need 4-column groups that never straddle N.
+  key.vec = (a.N % 4 == 0) && (a.ldc % 4 == 0) && aligned(a.C, 8);
   const int grid = p.tiles_n * p.slices;
-  hipError_t e;
-  switch (p.kmb) {
-    case 1: e = launch_skinny_mb<1, kRowCol>(g, vec8, grid, stream); break;
-    case 2: e = launch_skinny_mb<2, kRowCol>(g, vec8, grid, stream); break;
-    case 4: e = launch_skinny_mb<4, kRowCol>(g, vec8, grid, stream); break;
-    default: e = launch_skinny_mb<8, kRowCol>(g, vec8, grid, stream); break;
-  }
+  const void* fn = key.ext ? hk::skinny_ext(p.kmb, key) : hk::skinny_plain(p.kmb, key);
+  if (!fn) return hipErrorInvalidValue;
+  void* args1[] = {&g};
+  hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(CfgSkinny::kThreads),
+                                 args1, 0, stream);
   if (e != hipSuccess || !reduce_pass) return e;
   int kmb = p.kmb;
   void* args[] = {&g, &kmb};
-  const void* fn =
-      vec8 ? reinterpret_cast<const void*>(&k_fp8_gemm_skinny_reduce<true, kRowCol>)
-           : reinterpret_cast<const void*>(&k_fp8_gemm_skinny_reduce<false, kRowCol>);
-  return hipLaunchKernel(fn, dim3(p.tiles_n * p.kmb), dim3(CfgSkinny::kThreads),
-                         args, 0, stream);
+  return hipLaunchKernel(hk::skinny_reduce(key), dim3(p.tiles_n * p.kmb),
+                         dim3(CfgSkinny::kThreads), args, 0, stream);
 }
 
 int resolve_variant(int variant, int M, int N, int K);
 
+bool valid_code(int v, int count) { return v >= 0 && v < count; }
+
 // Shared body of the GEMM entry points.  `ws` may be null when `ws_given` is
 // false: a schedule that needs a workspace then takes a stream-ordered
-// allocation for the call.  With `rowcol`, scale_a / scale_b are vectors of M
-// / N floats (or null for all ones) applied per row of C / per column of C.
-template <bool kRowCol>
-hipError_t run_gemm(const void* A, const void* B_T, void* C, int M, int N,
-                    int K, int lda, int ldb, int ldc, const float* scale_a,
-                    const float* scale_b, int variant, bool ws_given, void* ws,
-                    size_t ws_bytes, hipStream_t stream) {
-  hipError_t e = validate(A, B_T, C, M, N, K, lda, ldb, ldc, variant);
+// allocation for the call.
+hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
+                    hipStream_t stream) {
+  int M = d.M, N = d.N, K = d.K, lda = d.lda, ldb = d.ldb, variant = d.variant;
+  hipError_t e = validate(d.A, d.B_T, d.C, M, N, K, lda, ldb, d.ldc, variant);
   if (e != hipSuccess) return e;
   if (variant == HIPGEMM_VARIANT_SKINNY && M > CfgSkinny::kMaxM)
     return hipErrorInvalidValue;
+  void* ws = d.workspace;
+  const size_t ws_bytes = d.workspace_bytes;
   if (ws_given && ws_bytes > 0 && (!ws || !aligned(ws, 256)))
     return hipErrorInvalidValue;
+  if (!valid_code(d.a_format, 2) || !valid_code(d.b_format, 2) ||
+      !valid_code(d.out_dtype, 2) || !valid_code(d.activation, 4))
+    return hipErrorInvalidValue;
   if (M == 0 || N == 0) return hipSuccess;
-  // Scale vectors are read with 4-byte loads; the 32x32x64 schedule has no
-  // per-row/per-column epilogue.
-  if (kRowCol && (!aligned(scale_a, 4) || !aligned(scale_b, 4) ||
-                  variant == HIPGEMM_VARIANT_4WAVE))
+  // Vectors are read with 4-byte loads.
+  if (!aligned(d.scale_rows, 4) || !aligned(d.scale_cols, 4) ||
+      !aligned(d.bias, 4))
+    return hipErrorInvalidValue;
+  const bool ext = d.scale_rows || d.scale_cols || d.bias ||
+                   d.activation != HIPGEMM_ACT_NONE ||
+                   d.out_dtype != HIPGEMM_OUT_BF16;
+  const int fmt = d.a_format | (d.b_format << 1);
+  // The 32x32x64 schedule is built for e4m3 x e4m3 with the per-tensor
+  // epilogue only.
+  if (variant == HIPGEMM_VARIANT_4WAVE && (ext || fmt != 0))
     return hipErrorInvalidValue;
   variant = resolve_variant(variant, M, N, K);
   if (K == 0) lda = ldb = 16;  // nothing is read; keep the offset math inert
   const int tiles_m = (M + Cfg4w::kBM - 1) / Cfg4w::kBM;
   const int tiles_n = (N + Cfg4w::kBN - 1) / Cfg4w::kBN;
-  GemmArgs g{static_cast<const uint8_t*>(A),
-             static_cast<const uint8_t*>(B_T),
-             static_cast<uint16_t*>(C),
-             scale_a,
-             scale_b,
+  GemmArgs g{static_cast<const uint8_t*>(d.A),
+             static_cast<const uint8_t*>(d.B_T),
+             static_cast<uint16_t*>(d.C),
+             d.scale_a,
+             d.scale_b,
              M,
              N,
              K,
              lda,
              ldb,
-             ldc,
+             d.ldc,
              default_group_m(tiles_m, tiles_n),
-             0};
+             0,
+             EpiArgs{}};
+  g.epi.row_scale = d.scale_rows;
+  g.epi.col_scale = d.scale_cols;
+  g.epi.bias = d.bias;
+  g.epi.act = d.activation;
+  g.epi.out = d.out_dtype;
+  hk::Key key;
+  key.fmt = fmt;
+  key.ext = ext;
+  key.act = d.activation;
+  key.out = d.out_dtype;
   switch (variant) {
     case HIPGEMM_VARIANT_SKINNY: {
       const SkinnyPlan p = plan_skinny(M, N, K);
-      if (p.ws_bytes == 0) return launch_skinny<kRowCol>(g, p, nullptr, stream);
+      auto go = [&](void* w) { return launch_skinny(g, p, w, key, stream); };
+      if (p.ws_bytes == 0) return go(nullptr);
       if (ws_given) {
         if (ws_bytes < p.ws_bytes) return hipErrorInvalidValue;
-        return launch_skinny<kRowCol>(g, p, ws, stream);
+        return go(ws);
       }
       void* tmp = nullptr;
       if ((e = hipMallocAsync(&tmp, p.ws_bytes, stream)) != hipSuccess) return e;
       e = hipMemsetAsync(tmp, 0, p.counter_bytes, stream);
-      if (e == hipSuccess) e = launch_skinny<kRowCol>(g, p, tmp, stream);
+      if (e == hipSuccess) e = go(tmp);
       const hipError_t f = hipFreeAsync(tmp, stream);
       return e != hipSuccess ? e : f;
     }
-    case HIPGEMM_VARIANT_4WAVE_MFMA16:
-      return launch_4wave<16, kRowCol>(g, stream);
-    case HIPGEMM_VARIANT_8WAVE:
-      return launch_8wave<kRowCol>(g, stream);
-    case HIPGEMM_VARIANT_4WAVE:
     default:
-      if constexpr (kRowCol) return hipErrorInvalidValue;  // rejected above
-      else return launch_4wave<32, false>(g, stream);
+      return launch_tiled(variant, g, key, stream);
   }
+}
+
+hipgemm_gemm_desc base_desc(const void* A, const void* B_T, void* C, int M,
+                            int N, int K, int lda, int ldb, int ldc,
+                            int variant) {
+  hipgemm_gemm_desc d{};
+  d.size = sizeof(hipgemm_gemm_desc);
+  d.A = A;
+  d.B_T = B_T;
+  d.C = C;
+  d.M = M;
+  d.N = N;
+  d.K = K;
+  d.lda = lda;
+  d.ldb = ldb;
+  d.ldc = ldc;
+  d.variant = variant;
+  return d;
 }
 
 int resolve_variant(int variant, int M, int N, int K) {
@@ -286,8 +289,10 @@ hipError_t hipgemm_fp8_gemm_bf16(const void* A, const void* B_T, void* C,
                                  int ldc, const float* scale_a,
                                  const float* scale_b, int variant,
                                  hipStream_t stream) {
-  return run_gemm<false>(A, B_T, C, M, N, K, lda, ldb, ldc, scale_a, scale_b,
-                         variant, false, nullptr, 0, stream);
+  hipgemm_gemm_desc d = base_desc(A, B_T, C, M, N, K, lda, ldb, ldc, variant);
+  d.scale_a = scale_a;
+  d.scale_b = scale_b;
+  return run_gemm(d, false, stream);
 }
 
 hipError_t hipgemm_fp8_gemm_bf16_ws(const void* A, const void* B_T, void* C,
@@ -296,8 +301,12 @@ hipError_t hipgemm_fp8_gemm_bf16_ws(const void* A, const void* B_T, void* C,
                                     const float* scale_b, int variant,
                                     void* workspace, size_t workspace_bytes,
                                     hipStream_t stream) {
-  return run_gemm<false>(A, B_T, C, M, N, K, lda, ldb, ldc, scale_a, scale_b,
-                         variant, true, workspace, workspace_bytes, stream);
+  hipgemm_gemm_desc d = base_desc(A, B_T, C, M, N, K, lda, ldb, ldc, variant);
+  d.scale_a = scale_a;
+  d.scale_b = scale_b;
+  d.workspace = workspace;
+  d.workspace_bytes = workspace_bytes;
+  return run_gemm(d, true, stream);
 }
 
 hipError_t hipgemm_fp8_gemm_bf16_rowcol(const void* A, const void* B_T, void* C,
@@ -306,12 +315,22 @@ hipError_t hipgemm_fp8_gemm_bf16_rowcol(const void* A, const void* B_T, void* C,
                                         const float* scale_cols, int variant,
                                         void* workspace, size_t workspace_bytes,
                                         hipStream_t stream) {
+  hipgemm_gemm_desc d = base_desc(A, B_T, C, M, N, K, lda, ldb, ldc, variant);
+  d.scale_rows = scale_rows;
+  d.scale_cols = scale_cols;
+  d.workspace = workspace;
+  d.workspace_bytes = workspace_bytes;
   // A null workspace with a zero size lets the call allocate one when the
   // split-K schedule needs it, like hipgemm_fp8_gemm_bf16.
-  const bool ws_given = workspace != nullptr || workspace_bytes != 0;
-  return run_gemm<true>(A, B_T, C, M, N, K, lda, ldb, ldc, scale_rows,
-                        scale_cols, variant, ws_given, workspace,
-                        workspace_bytes, stream);
+  return run_gemm(d, workspace != nullptr || workspace_bytes != 0, stream);
+}
+
+hipError_t hipgemm_gemm(const hipgemm_gemm_desc* desc, hipStream_t stream) {
+  if (!desc || desc->size != sizeof(hipgemm_gemm_desc))
+    return hipErrorInvalidValue;
+  return run_gemm(*desc,
+                  desc->workspace != nullptr || desc->workspace_bytes != 0,
+                  stream);
 }
 
 size_t hipgemm_workspace_size(int M, int N, int K, int variant) {

@@ -1,0 +1,32 @@
+// The 8-wave ping-pong schedule with the extended epilogue and bf16 output,
+// for every operand-format pair and activation.
+#include "kernels.hpp"
+
+namespace hipgemm {
+namespace kernels {
+namespace {
+
+using namespace detail;
+
+template <bool kVec, int kFmt, int kAct>
+__global__ __launch_bounds__(512, 1) void k_fp8_gemm_8wave_ext(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg8w::kLdsBytes];
+  gemm_8wave_body<kVec, true, kFmt, kAct, kOutBf16>(g, (lds_u8*)lds);
+}
+
+}  // namespace
+
+const void* eight_wave_ext_bf16(const Key& k) {
+  return sel4(k.fmt, [&](auto F) {
+    return sel4(k.act, [&](auto A) {
+      return sel2(k.vec, [&](auto V) {
+        return (const void*)&k_fp8_gemm_8wave_ext<decltype(V)::value == 1,
+                                                  decltype(F)::value,
+                                                  decltype(A)::value>;
+      });
+    });
+  });
+}
+
+}  // namespace kernels
+}  // namespace hipgemm

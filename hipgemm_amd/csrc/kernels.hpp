@@ -1,0 +1,58 @@
+// Kernel lookup across the library's translation units.  Each schedule's
+// instantiations live in their own file (compiled in parallel); the C ABI
+// (hipgemm.hip) asks here for the entry point of one configuration.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "hipgemm/detail/gemm_8wave.hpp"
+#include "hipgemm/detail/gemm_skinny.hpp"
+
+namespace hipgemm {
+namespace kernels {
+
+// One configuration: operand formats (bit 0 A, bit 1 B_T), extended
+// epilogue, its activation and output type, and the store width (16 bytes
+// per lane for the tiled schedules, 8 for the skinny one).
+struct Key {
+  int fmt = 0;
+  bool ext = false;
+  int act = 0;
+  int out = 0;
+  bool vec = true;
+};
+
+// Entry points (host handles for hipLaunchKernel), nullptr for a
+// configuration that is not built.
+const void* four_wave_plain(int mf, const Key& k);  // k4wave_plain.hip
+const void* four_wave_ext_bf16(const Key& k);       // k4wave_ext_bf16.hip
+const void* four_wave_ext_f16(const Key& k);        // k4wave_ext_f16.hip
+const void* eight_wave_plain(const Key& k);         // k8wave_plain.hip
+const void* eight_wave_ext_bf16(const Key& k);      // k8wave_ext_bf16.hip
+const void* eight_wave_ext_f16(const Key& k);       // k8wave_ext_f16.hip
+const void* skinny_plain(int kmb, const Key& k);    // kskinny_plain.hip
+const void* skinny_ext(int kmb, const Key& k);      // kskinny_ext.hip
+const void* skinny_reduce(const Key& k);            // kskinny_plain.hip
+
+// Runtime value -> integral_constant, for building the lookups.
+template <int I>
+using ic = std::integral_constant<int, I>;
+template <class F>
+const void* sel2(int v, F&& f) {
+  return v ? f(ic<1>{}) : f(ic<0>{});
+}
+template <class F>
+const void* sel4(int v, F&& f) {
+  switch (v) {
+    case 0: return f(ic<0>{});
+    case 1: return f(ic<1>{});
+    case 2: return f(ic<2>{});
+    case 3: return f(ic<3>{});
+    default: return nullptr;
+  }
+}
+
+}  // namespace kernels
+}  // namespace hipgemm

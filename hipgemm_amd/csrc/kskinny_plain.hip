@@ -1,0 +1,55 @@
+// The split-K skinny schedule (M <= 128) with the per-tensor epilogue, for
+// every row-block count and operand-format pair, and the slice-reduce
+// kernel for both epilogues.
+#include "kernels.hpp"
+
+namespace hipgemm {
+namespace kernels {
+namespace {
+
+using namespace detail;
+
+template <int kMB, bool kVec8, int kFmt>
+__global__ __launch_bounds__(256, 1) void k_fp8_gemm_skinny(SkinnyArgs g) {
+  gemm_skinny_body<kMB, kVec8, false, kFmt>(g);
+}
+
+template <bool kVec8, bool kExt>
+__global__ __launch_bounds__(256, 1) void k_fp8_gemm_skinny_reduce(SkinnyArgs g,
+                                                                    int kmb) {
+  gemm_skinny_reduce_body<kVec8, kExt>(g, kmb);
+}
+
+template <class F>
+const void* sel_mb(int kmb, F&& f) {
+  switch (kmb) {
+    case 1: return f(ic<1>{});
+    case 2: return f(ic<2>{});
+    case 4: return f(ic<4>{});
+    case 8: return f(ic<8>{});
+    default: return nullptr;
+  }
+}
+
+}  // namespace
+
+const void* skinny_plain(int kmb, const Key& k) {
+  return sel_mb(kmb, [&](auto B) {
+    return sel4(k.fmt, [&](auto F) {
+      return sel2(k.vec, [&](auto V) {
+        return (const void*)&k_fp8_gemm_skinny<decltype(B)::value, decltype(V)::value == 1, decltype(F)::value>;
+      });
+    });
+  });
+}
+
+const void* skinny_reduce(const Key& k) {
+  return sel2(k.ext, [&](auto E) {
+    return sel2(k.vec, [&](auto V) {
+      return (const void*)&k_fp8_gemm_skinny_reduce<decltype(V)::value == 1, decltype(E)::value == 1>;
+    });
+  });
+}
+
+}  // namespace kernels
+}  // namespace hipgemm

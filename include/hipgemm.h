@@ -6,6 +6,8 @@
  * A is M x K, row-major, e4m3 (OCP E4M3FN, one byte), row stride lda bytes.
  * B_T is N x K, row-major (K contiguous), e4m3, row stride ldb bytes.
  * C is M x N, row-major, bf16, row stride ldc elements.
+ * (hipgemm_gemm generalises this: e5m2 operands, fp16 output, row / column
+ * scales, bias and activation; see hipgemm_gemm_desc.)
  * Accumulation is fp32.  scale_a / scale_b are DEVICE pointers to one fp32
  * each (per-tensor scales), or NULL for 1.0; the product scale_a * scale_b is
  * formed in fp32 and applied to the fp32 accumulator before rounding.
@@ -66,6 +68,63 @@ enum {
   HIPGEMM_VARIANT_COUNT = 5
 };
 
+/* 8-bit operand formats (OCP 8-bit floating point, v1.0). */
+enum {
+  HIPGEMM_FMT_E4M3 = 0, /* E4M3FN: bias 7, max 448, NaN 0x7F/0xFF, no inf */
+  HIPGEMM_FMT_E5M2 = 1  /* E5M2: bias 15, max 57344, IEEE inf and NaN     */
+};
+
+/* Output element types (RNE from the fp32 result). */
+enum { HIPGEMM_OUT_BF16 = 0, HIPGEMM_OUT_F16 = 1 };
+
+/* Activations of the fused epilogue, applied in fp32 after bias:
+ *   RELU(v) = v < 0 ? 0 : v
+ *   GELU_TANH(v) = v/2 (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3)))
+ *   SILU(v) = v / (1 + exp(-v))
+ * evaluated with the hardware exponential and reciprocal (a few ulp of
+ * fp32 before the rounding to the output type). */
+enum {
+  HIPGEMM_ACT_NONE = 0,
+  HIPGEMM_ACT_RELU = 1,
+  HIPGEMM_ACT_GELU_TANH = 2,
+  HIPGEMM_ACT_SILU = 3
+};
+
+/*
+ * Full description of one GEMM for hipgemm_gemm:
+ *
+ *   scale[m,n] = scale_rows[m] * (scale_cols[n] * (scale_a * scale_b))
+ *   v[m,n]     = fma(acc[m,n], scale[m,n], bias[n])       (one rounding)
+ *   C[m,n]     = round_out(activation(v[m,n]))
+ *
+ * acc is the fp32 sum over K of A[m,k] * B_T[n,k] with A in a_format and
+ * B_T in b_format.  NULL scalars and vectors are ones, a NULL bias is
+ * -0.0 (v is then exactly acc * scale).  With the defaults (e4m3 x e4m3, no
+ * vectors, no bias, no activation, bf16) this is hipgemm_fp8_gemm_bf16,
+ * bit for bit.  Zero-initialise the struct, set `size` to
+ * sizeof(hipgemm_gemm_desc) (a different size is rejected), then the
+ * fields.  Shape, stride, alignment and workspace rules are those of the
+ * entry points above; vectors must be 4-byte aligned; variant
+ * HIPGEMM_VARIANT_4WAVE accepts only the defaults of format and epilogue.
+ */
+typedef struct hipgemm_gemm_desc {
+  size_t size;
+  const void *A;   /* M x K, row stride lda bytes */
+  const void *B_T; /* N x K, row stride ldb bytes */
+  void *C;         /* M x N, row stride ldc elements of out_dtype */
+  int M, N, K;
+  int lda, ldb, ldc;
+  int a_format, b_format; /* HIPGEMM_FMT_* */
+  int out_dtype;          /* HIPGEMM_OUT_* */
+  int activation;         /* HIPGEMM_ACT_* */
+  const float *scale_a, *scale_b;       /* device scalars or NULL */
+  const float *scale_rows, *scale_cols; /* device vectors of M, N or NULL */
+  const float *bias;                    /* device vector of N or NULL */
+  int variant;                          /* HIPGEMM_VARIANT_* */
+  void *workspace; /* as for hipgemm_fp8_gemm_bf16_ws; NULL with size 0: */
+  size_t workspace_bytes; /* allocate one when needed, stream-ordered    */
+} hipgemm_gemm_desc;
+
 /*
  * Runtime-shape GEMM with scales and a stream.
  * Replaces: fp8_gemm_4wave_256x256x128<M, N, K><<<(M*N)/65536, 256>>>(A, B_T,
@@ -125,6 +184,17 @@ hipError_t hipgemm_fp8_gemm_bf16_rowcol(const void *A, const void *B_T, void *C,
                                         const float *scale_cols, int variant,
                                         void *workspace, size_t workspace_bytes,
                                         hipStream_t stream);
+
+/*
+ * The general entry point: operand formats (e4m3 / e5m2, mixed), output
+ * type (bf16 / fp16), per-tensor and per-row / per-column scales, bias and
+ * activation, fused into the one kernel (see hipgemm_gemm_desc).
+ * No reference counterpart beyond the plain launch it generalises: the
+ * reference's kernel is e4m3 x e4m3 -> bf16 with no scales
+ * (fp8_4wave.hpp:58 passes format codes 0, 0 and zero scales to the MFMA;
+ * store_rt, :214-238, converts the accumulator straight to bf16).
+ */
+hipError_t hipgemm_gemm(const hipgemm_gemm_desc *desc, hipStream_t stream);
 
 /* Workspace bytes hipgemm_fp8_gemm_bf16_ws needs for this shape and variant
  * on the current device (0: none).  No GPU work.  No reference counterpart. */

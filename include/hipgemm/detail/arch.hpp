@@ -95,17 +95,27 @@ __device__ __forceinline__ i32x8 join(i32x4 lo, i32x4 hi) {
   return i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 }
 
-// D[32x32] += X[32x64] . Y[32x64]^T, e4m3 x e4m3 -> fp32.  Lane l carries
-// row l%32 of X (and of Y) and 32 of its 64 K-bytes.
+// 8-bit operand formats of the f8f6f4 MFMA family (its cbsz / blgp
+// immediates): OCP E4M3 (fp8) and OCP E5M2 (bf8).
+constexpr int kFmtE4M3 = 0, kFmtE5M2 = 1;
+// A kernel's operand-format pair kFmt: bit 0 the format of A, bit 1 that of
+// B_T.  0 = e4m3 x e4m3.
+__host__ __device__ constexpr int fmt_a(int f) { return f & 1; }
+__host__ __device__ constexpr int fmt_b(int f) { return (f >> 1) & 1; }
+
+// D[32x32] += X[32x64] . Y[32x64]^T -> fp32, X in format kFx, Y in kFy.
+// Lane l carries row l%32 of X (and of Y) and 32 of its 64 K-bytes.
+template <int kFx = kFmtE4M3, int kFy = kFmtE4M3>
 __device__ __forceinline__ f32x16 mfma_32x32x64(i32x8 x, i32x8 y, f32x16 acc) {
-  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(x, y, acc, 0, 0, 0, 0,
-                                                         0, 0);
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(x, y, acc, kFx, kFy, 0,
+                                                         0, 0, 0);
 }
 
-// D[16x16] += X[16x128] . Y[16x128]^T, e4m3 x e4m3 -> fp32.
+// D[16x16] += X[16x128] . Y[16x128]^T -> fp32, X in format kFx, Y in kFy.
+template <int kFx = kFmtE4M3, int kFy = kFmtE4M3>
 __device__ __forceinline__ f32x4 mfma_16x16x128(i32x8 x, i32x8 y, f32x4 acc) {
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(x, y, acc, 0, 0, 0, 0,
-                                                          0, 0);
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(x, y, acc, kFx, kFy,
+                                                          0, 0, 0, 0);
 }
 
 // One accumulator element (AGPR) -> VGPR at this point of the program.  The

@@ -65,21 +65,23 @@
 #include <type_traits>
 
 #include "arch.hpp"
+#include "epilogue.hpp"
 #include "layout.hpp"
 
 namespace hipgemm {
 namespace detail {
 
 struct GemmArgs {
-  const uint8_t* A;      // M x K e4m3, row stride lda bytes
-  const uint8_t* B;      // N x K e4m3 (B_T), row stride ldb bytes
-  uint16_t* C;           // M x N bf16, row stride ldc elements
+  const uint8_t* A;      // M x K 8-bit (format by kFmt), row stride lda bytes
+  const uint8_t* B;      // N x K 8-bit (B_T), row stride ldb bytes
+  uint16_t* C;           // M x N bf16 (fp16: kExt, epi.out), stride ldc elements
   const float* scale_a;  // device scalar, nullptr = 1.0
   const float* scale_b;  // device scalar, nullptr = 1.0
   int M, N, K;
   int lda, ldb, ldc;
   int group_m;
   int workers;  // persistent workgroups (<= grid); 0 = the whole grid
+  EpiArgs epi;  // extended epilogue (kExt instantiations only)
 };
 
 // The GemmArgs of a kernel whose only argument is a GemmArgs, read again
@@ -91,6 +93,16 @@ kernel_args() {
       __builtin_amdgcn_kernarg_segment_ptr();
   asm volatile("" : "+s"(p));
   return p;
+}
+__device__ __forceinline__ EpiArgs kernel_epi() {
+  const auto* k = kernel_args();
+  EpiArgs e;
+  e.row_scale = k->epi.row_scale;
+  e.col_scale = k->epi.col_scale;
+  e.bias = k->epi.bias;
+  e.act = k->epi.act;
+  e.out = k->epi.out;
+  return e;
 }
 
 __host__ __device__ constexpr int default_group_m(int tiles_m, int tiles_n) {
@@ -187,90 +199,22 @@ __device__ __forceinline__ TileSrc tile_src(const GemmArgs& g, int t,
                            (uint32_t)rows_b * (uint32_t)g.ldb)};
 }
 
-// Per-row / per-column scales (scale mode "rowcol": scale_a holds M floats,
-// scale_b N floats, either may be null = 1.0) for a wave's 16 x 16
-// accumulator blocks: lane l needs, for block row bi, the scale of row
-// row0 + 16 bi + l % 16 and, for block column bj, those of columns
-// col0 + 16 bj + 4 (l / 16) + e, e < 4.  Rows or columns past M or N load
-// 0 (their results are never stored).  The loads count in vmcnt; the
-// caller waits for them.
-template <int kBR, int kBC>
-struct RowColScales {
-  float r[kBR];
-  float c[kBC][4];
-  __device__ __forceinline__ void load(const GemmArgs& g, int row0, int col0,
-                                       int lane) {
-    const int lr = lane & 15, lc = 4 * (lane >> 4);
-    if (g.scale_a) {
-      const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.scale_a, (uint32_t)g.M * 4);
-#pragma unroll
-      for (int bi = 0; bi < kBR; ++bi)
-        r[bi] = __builtin_bit_cast(
-            float, __builtin_amdgcn_raw_buffer_load_b32(
-                       ra, (uint32_t)(row0 + 16 * bi + lr) * 4u, 0, 0));
-    } else {
-#pragma unroll
-      for (int bi = 0; bi < kBR; ++bi) r[bi] = 1.0f;
-    }
-    if (g.scale_b) {
-      const __amdgpu_buffer_rsrc_t rb = make_rsrc(g.scale_b, (uint32_t)g.N * 4);
-#pragma unroll
-      for (int bj = 0; bj < kBC; ++bj)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          c[bj][e] = __builtin_bit_cast(
-              float, __builtin_amdgcn_raw_buffer_load_b32(
-                         rb, (uint32_t)(col0 + 16 * bj + lc + e) * 4u, 0, 0));
-    } else {
-#pragma unroll
-      for (int bj = 0; bj < kBC; ++bj)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) c[bj][e] = 1.0f;
-    }
-  }
-  // The same from LDS: row scales at base + 4 r, column scales at
-  // base + 512 + 4 c (r, c relative to row0, col0); `has_rows` /
-  // `has_cols` false = all ones.  Read as integers, like the epilogue's own
-  // LDS traffic, and fenced: type-based alias analysis must not let a float
-  // read move past the staging writes that overwrite the scales.
-  __device__ __forceinline__ void read_lds(const lds_u8* base, bool has_rows,
-                                           bool has_cols, int lane) {
-    const int lr = lane & 15, lc = 4 * (lane >> 4);
-    // (The 16-byte read is bit-cast as a whole vector: __builtin_bit_cast of
-    // one element of a vector, v[e], yields element 0 with this compiler.)
-#pragma unroll
-    for (int bi = 0; bi < kBR; ++bi) {
-      const float x = __builtin_bit_cast(float, lds_read4(base + 4 * (16 * bi + lr)));
-      r[bi] = has_rows ? x : 1.0f;
-    }
-#pragma unroll
-    for (int bj = 0; bj < kBC; ++bj) {
-      const f32x4 v =
-          __builtin_bit_cast(f32x4, lds_read16(base + 512 + 4 * (16 * bj + lc)));
-#pragma unroll
-      for (int e = 0; e < 4; ++e) c[bj][e] = has_cols ? v[e] : 1.0f;
-    }
-    compiler_fence();
-  }
-  // The scale of element e of block (bi, bj): row scale times column scale,
-  // one fp32 product (the per-tensor path's scale_a * scale_b, per element).
-  __device__ __forceinline__ float at(int bi, int bj, int e) const {
-    return r[bi] * c[bj][e];
-  }
-};
-
 // kMf selects the MFMA: 32 = v_mfma_f32_32x32x64_f8f6f4 (4 x 4 blocks of
 // 32 x 32 per wave, two MFMA per block per step), 16 =
 // v_mfma_f32_16x16x128_f8f6f4 (8 x 8 blocks of 16 x 16, one per block per
 // step).  Same data flow and the same 2048 MFMA cycles per step either way.
-// kRowCol: per-row / per-column scales (RowColScales) instead of the
-// per-tensor pair; 16x16x128 only.
-template <bool kVecStore, int kMf = 32, bool kRowCol = false>
+// kExt: the extended epilogue of epilogue.hpp (row / column scales, bias,
+// activation, fp16 output) from g.epi; 16x16x128 only.
+// kAct / kOut (kExt only): the activation and the output type
+// (epilogue.hpp) -- template parameters, so that each instantiation has one
+// straight-line epilogue.
+template <bool kVecStore, int kMf = 32, bool kExt = false, int kFmt = 0,
+          int kAct = kActNone, int kOut = kOutBf16>
 __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                                                 lds_u8* lds) {
   using Cfg = Cfg4w;
   static_assert(kMf == 32 || kMf == 16, "MFMA shape");
-  static_assert(!kRowCol || kMf == 16, "row/column scales: 16x16x128 only");
+  static_assert(!kExt || kMf == 16, "extended epilogue: 16x16x128 only");
   constexpr bool k16 = kMf == 16;
   constexpr int kDmaPerGroup = 4;  // per wave
   constexpr int kWaitSteady = 4 * kDmaPerGroup;
@@ -293,10 +237,9 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   int t = walk.first;
   if (t >= walk.end) return;
 
-  // Per-tensor scales (with kRowCol the pointers are vectors, read in the
-  // epilogue instead).
-  const float sa = !kRowCol && g.scale_a ? *g.scale_a : 1.0f;
-  const float sb = !kRowCol && g.scale_b ? *g.scale_b : 1.0f;
+  // Per-tensor scales.
+  const float sa = g.scale_a ? *g.scale_a : 1.0f;
+  const float sb = g.scale_b ? *g.scale_b : 1.0f;
   const float scale = sa * sb;
 
   // ---- DMA lane geometry: instruction q of wave w covers rows
@@ -371,34 +314,39 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     for (int qq = 0; qq < kDmaPerGroup; ++qq) dma_one(d, stage, op, hi, qq);
   };
 
-  // kRowCol: the wave's 128 row scales and 128 column scales of tile t, by
-  // DMA into the first 1 KiB of its epilogue stage (rows at +0, columns at
-  // +512), one float per lane (4 loads; rows past M or columns past N read
-  // zero).  Issued at the tile's first barrier, when the previous epilogue's
-  // LDS reads are done; retired by the K loop's own vmcnt waits, so the
-  // epilogue only reads LDS (a load issued there would retire behind the
-  // next tile's prefetch).  A null vector gets an empty range (every lane
-  // reads zero); the epilogue uses 1.0 for it.
-  // The vectors' addresses are reloaded from the kernel arguments (the
-  // kernel's only argument is the GemmArgs) and the lane index goes through
-  // an opaque copy, so that nothing here is hoisted out of the tile loop:
-  // values held across the K loop change how it is scheduled (measured 1-2 %
-  // slower).
+  // kExt: the wave's 128 row scales, 128 column scales and 128 biases of
+  // tile t, by DMA into the first 1.5 KiB of its epilogue stage (rows at +0,
+  // columns at +512, bias at +1024), one float per lane (6 loads; rows past
+  // M or columns past N read zero).  Issued at the tile's first barrier,
+  // when the previous epilogue's LDS reads are done; retired by the K loop's
+  // own vmcnt waits, so the epilogue only reads LDS (a load issued there
+  // would retire behind the next tile's prefetch).  A null vector gets an
+  // empty range (every lane reads zero); the epilogue substitutes 1.0 or
+  // -0.0 for it.  The vectors' addresses are reloaded from the kernel
+  // arguments (the kernel's only argument is the GemmArgs) and the lane
+  // index goes through an opaque copy, so that nothing here is hoisted out
+  // of the tile loop.
   auto scale_dma = [&](int tile) {
     const TileCoord sc = grouped_tile(tile, tiles_m, tiles_n, g.group_m);
-    const float* pa = kernel_args()->scale_a;
-    const float* pb = kernel_args()->scale_b;
+    const EpiArgs ea = kernel_epi();
+    const float* pr = ea.row_scale;
+    const float* pc = ea.col_scale;
+    const float* pbias = ea.bias;
     int ln = lane;
     asm volatile("" : "+v"(ln));
     lds_u8* dst = lds + Cfg::kStoreBase + wave * Cfg::kStoreStage;
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(pa, pa ? (uint32_t)M * 4u : 0u);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(pb, pb ? (uint32_t)N * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(pr, pr ? (uint32_t)M * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(pc, pc ? (uint32_t)N * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rb =
+        make_rsrc(pbias, pbias ? (uint32_t)N * 4u : 0u);
     const uint32_t ro = (uint32_t)(sc.m * Cfg::kBM + wm * 128 + ln) * 4u;
     const uint32_t co = (uint32_t)(sc.n * Cfg::kBN + wn * 128 + ln) * 4u;
-    dma4(ra, dst, ro);
-    dma4(ra, dst + 256, ro + 256);
-    dma4(rb, dst + 512, co);
-    dma4(rb, dst + 768, co + 256);
+    dma4(rr, dst, ro);
+    dma4(rr, dst + 256, ro + 256);
+    dma4(rc, dst + 512, co);
+    dma4(rc, dst + 768, co + 256);
+    dma4(rb, dst + 1024, co);
+    dma4(rb, dst + 1280, co + 256);
   };
 
   i32x8 fa[4][2], fb[4][2];  // 32x32x64: [32-row fragment][K-half]
@@ -452,14 +400,16 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
 #pragma unroll
       for (int n = from; n < to; ++n) {
         const int i = 4 * qi + n / 4, j = 4 * qj + n % 4;
-        acc16[i][j] = mfma_16x16x128(fb16[j], fa16[i], acc16[i][j]);
+        acc16[i][j] = mfma_16x16x128<fmt_b(kFmt), fmt_a(kFmt)>(
+            fb16[j], fa16[i], acc16[i][j]);
       }
       return;
     }
 #pragma unroll
     for (int n = from; n < to; ++n) {
       const int kh = n / 4, i = 2 * qi + (n / 2) % 2, j = 2 * qj + n % 2;
-      acc[i][j] = mfma_32x32x64(fb[j][kh], fa[i][kh], acc[i][j]);
+      acc[i][j] = mfma_32x32x64<fmt_b(kFmt), fmt_a(kFmt)>(fb[j][kh], fa[i][kh],
+                                                           acc[i][j]);
     }
   };
   using QS = QuarterShape<kMf>;
@@ -471,14 +421,15 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // `tail`, the head MFMA of quarter q, the LDS reads of register tile
   // (rop, rhi) of stage rst, and DMA group (dop, dhi) of step kb into stage
   // dst, in the order of quarter_schedule.  The scheduler follows that
-  // pattern for the per-tensor instantiations, but for the row/column one
-  // it clustered the DMAs and the reads instead (4 % slower): there the
-  // order is written out, one scheduling region per pair.  (Written out for
-  // the per-tensor path too, it measured 0.6 % slower than the scheduler's
-  // own placement of the address arithmetic.)
+  // pattern for the default instantiation (e4m3, per-tensor epilogue), but
+  // for the extended-epilogue ones and other formats it clustered the DMAs
+  // and the reads instead (4 % slower): there the order is written out, one
+  // scheduling region per pair.  (Written out for the default instantiation
+  // too, it measured 0.6 % slower than the scheduler's own placement of the
+  // address arithmetic.)
   auto quarter = [&](bool tail, int tqi, int tqj, int qi, int qj, int rop,
                      int rhi, int rst, int kb, int dst, int dop, int dhi) {
-    if constexpr (k16 && kRowCol) {
+    if constexpr (k16 && (kExt || kFmt != 0)) {
       if (tail) quarter_mfma(tqi, tqj, QS::kHead, QS::kMfma);
       const DmaSrc d = dma_src(kb, dop);
       sched_fence();
@@ -537,10 +488,9 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       const bool tail = !(kFirst && s == 0);
       wait_lgkmcnt<0>();
       if (kFirst) wait_vmcnt<kWaitAfterStores>(); else wait_vmcnt<kWaitSteady>();
-      // After the wait (which counts only older operations): the four
-      // loads at most make the tile's next two waits retire four more
-      // stores.
-      if constexpr (kRowCol && kFirst)
+      // After the wait (which counts only older operations): the six loads
+      // at most make the tile's next two waits retire six more stores.
+      if constexpr (kExt && kFirst)
         if (s == 0) scale_dma(t);
       barrier();  // Q00
       quarter(tail, 1, 1, 0, 0, 1, 1, s, kt + 2, s, 0, 0);
@@ -624,21 +574,23 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
         (uint32_t)(((rows_c - 1) * g.ldc + Cfg::kBN) * 2));
     const int rows_left = M - tc.m * Cfg::kBM - wm * 128;  // from wave row 0
     const int cols_left = N - tc.n * Cfg::kBN - wn * 128;  // from wave col 0
-    // Scale of element e of 16 x 16 block (bi, bj).  Row / column scales
-    // come from the wave's stage (scale_dma), read before the staging of C
+    // Elements of 16 x 16 block (bi, bj), packed.  kExt: the vectors come
+    // from the wave's stage (scale_dma), read before the staging of C
     // overwrites them.
-    RowColScales<8, 8> rcs;
-    if constexpr (kRowCol) {
-      const float* pa = kernel_args()->scale_a;
-      const float* pb = kernel_args()->scale_b;
-      rcs.read_lds(lds + Cfg::kStoreBase + wave * Cfg::kStoreStage,
-                   pa != nullptr, pb != nullptr, elane);
-    }
-    auto sc16 = [&](int bi, int bj, int e) -> float {
-      if constexpr (kRowCol)
-        return rcs.at(bi, bj, e);
+    EpiVec<8, 8> ev;
+    if constexpr (kExt)
+      ev.read_lds(lds + Cfg::kStoreBase + wave * Cfg::kStoreStage,
+                  kernel_epi(), scale, elane);
+    // The epilogue proper.
+    auto store_tile = [&]() {
+    auto pack16 = [&](const f32x4& a, int bi, int bj) -> u32x2 {
+      if constexpr (kExt)
+        return ev.template pack4<kAct, kOut>(acc_read(a[0]), acc_read(a[1]),
+                                               acc_read(a[2]), acc_read(a[3]),
+                                               bi, bj);
       else
-        return scale;
+        return u32x2{pack_bf16x2(acc_read(a[0]) * scale, acc_read(a[1]) * scale),
+                     pack_bf16x2(acc_read(a[2]) * scale, acc_read(a[3]) * scale)};
     };
 
     if constexpr (kVecStore) {
@@ -685,10 +637,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
           const int bi = 2 * i + ii;
           const f32x4& a = acc16[bi][j];
           lds_write8(stg + (16 * ii + wr) * 256 + (((4 * j + wg) ^ (2 * wr)) * 8),
-                     u32x2{pack_bf16x2(acc_read(a[0]) * sc16(bi, j, 0),
-                                       acc_read(a[1]) * sc16(bi, j, 1)),
-                           pack_bf16x2(acc_read(a[2]) * sc16(bi, j, 2),
-                                       acc_read(a[3]) * sc16(bi, j, 3))});
+                     pack16(a, bi, j));
         };
         auto store_one = [&](int i, int p, const i32x4& v) {
           int row4 = 32 * i + 4 * p;
@@ -780,10 +729,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
           for (int j = 0; j < 8; ++j) {
             const int c = 16 * j + 4 * (elane >> 4);
             const f32x4& a = acc16[i][j];
-            const u32x2 v{pack_bf16x2(acc_read(a[0]) * sc16(i, j, 0),
-                                      acc_read(a[1]) * sc16(i, j, 1)),
-                          pack_bf16x2(acc_read(a[2]) * sc16(i, j, 2),
-                                      acc_read(a[3]) * sc16(i, j, 3))};
+            const u32x2 v = pack16(a, i, j);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const uint32_t w = (r < 2 ? v.x : v.y) >> (16 * (r & 1));
@@ -824,6 +770,8 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
         }
       }
     }
+    };  // store_tile
+    store_tile();
 
     t += walk.stride;
     if (t >= walk.end) break;

@@ -64,9 +64,11 @@ static_assert(Cfg8w::kLdsBytes == 160 * 1024, "LDS budget");
 static_assert(8 * Cfg8w::kStoreStage <= Cfg8w::kAStages * Cfg8w::kAStage,
               "epilogue staging fits the A stages");
 
-// kRowCol: per-row / per-column scales (RowColScales) instead of the
-// per-tensor pair.
-template <bool kVecStore, bool kRowCol = false>
+// kExt: the extended epilogue of epilogue.hpp (row / column scales, bias,
+// activation, fp16 output) from g.epi.
+// kAct / kOut (kExt only): as for gemm_4wave_body.
+template <bool kVecStore, bool kExt = false, int kFmt = 0, int kAct = kActNone,
+          int kOut = kOutBf16>
 __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) {
   using Cfg = Cfg8w;
   const int lane = lane_id();
@@ -82,8 +84,8 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
                                     : (int)gridDim.x;
   if ((int)blockIdx.x >= workers) return;
 
-  const float sa = !kRowCol && g.scale_a ? *g.scale_a : 1.0f;
-  const float sb = !kRowCol && g.scale_b ? *g.scale_b : 1.0f;
+  const float sa = g.scale_a ? *g.scale_a : 1.0f;
+  const float sb = g.scale_b ? *g.scale_b : 1.0f;
   const float scale = sa * sb;
 
   // DMA lane geometry: instruction q covers operand rows 8q .. 8q + 7; lane l
@@ -206,7 +208,8 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int m = 0; m < 32; ++m)
-        acc[m / 4][m % 4] = mfma_16x16x128(fb[m % 4], fa[m / 4], acc[m / 4][m % 4]);
+        acc[m / 4][m % 4] = mfma_16x16x128<fmt_b(kFmt), fmt_a(kFmt)>(
+            fb[m % 4], fa[m / 4], acc[m / 4][m % 4]);
       __builtin_amdgcn_s_setprio(0);
       // Group 0: its B rows of step j + 1 landed for its own next memory
       // phase; newer: this step's 8.  At the last step, all DMAs of both
@@ -233,24 +236,26 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
         (uint32_t)(((rows_c - 1) * g.ldc + Cfg::kBN) * 2));
     const int rows_left = M - tc.m * Cfg::kBM - wm * 128;
     const int cols_left = N - tc.n * Cfg::kBN - wn * 64;
-    RowColScales<8, 4> rcs;
-    if constexpr (kRowCol) {
-      rcs.load(g, tc.m * Cfg::kBM + wm * 128, tc.n * Cfg::kBN + wn * 64, elane);
+    // kExt: the vectors are loaded here (there is no free LDS to stage
+    // them in); waiting for them also waits for the next tile's first DMAs.
+    EpiVec<8, 4> ev;
+    if constexpr (kExt) {
+      ev.load(g.epi, M, N, tc.m * Cfg::kBM + wm * 128, tc.n * Cfg::kBN + wn * 64,
+              scale, elane);
       wait_vmcnt<0>();
     }
-    auto sc16 = [&](int bi, int bj, int e) -> float {
-      if constexpr (kRowCol)
-        return rcs.at(bi, bj, e);
-      else
-        return scale;
-    };
+    // The epilogue proper.
+    auto store_tile = [&]() {
     // block (bi, bj) of the wave's 8 x 4, scaled and rounded
     auto cvt = [&](int bi, int bj) {
       const f32x4& v = acc[bi][bj];
-      return u32x2{pack_bf16x2(acc_read(v[0]) * sc16(bi, bj, 0),
-                               acc_read(v[1]) * sc16(bi, bj, 1)),
-                   pack_bf16x2(acc_read(v[2]) * sc16(bi, bj, 2),
-                               acc_read(v[3]) * sc16(bi, bj, 3))};
+      if constexpr (kExt)
+        return ev.template pack4<kAct, kOut>(acc_read(v[0]), acc_read(v[1]),
+                                               acc_read(v[2]), acc_read(v[3]),
+                                               bi, bj);
+      else
+        return u32x2{pack_bf16x2(acc_read(v[0]) * scale, acc_read(v[1]) * scale),
+                     pack_bf16x2(acc_read(v[2]) * scale, acc_read(v[3]) * scale)};
     };
     if constexpr (kVecStore) {
       // Staging: row r (0..31) at 128 r; 8-byte piece x (0..15) at slot
@@ -317,6 +322,8 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
         }
       }
     }
+    };  // store_tile
+    store_tile();
   }
   wait_vmcnt<0>();
 }

@@ -31,15 +31,16 @@
 #pragma once
 
 #include "arch.hpp"
+#include "epilogue.hpp"
 #include "layout.hpp"
 
 namespace hipgemm {
 namespace detail {
 
 struct SkinnyArgs {
-  const uint8_t* A;      // M x K e4m3, row stride lda bytes
-  const uint8_t* B;      // N x K e4m3 (B_T), row stride ldb bytes
-  uint16_t* C;           // M x N bf16, row stride ldc elements
+  const uint8_t* A;      // M x K 8-bit (format by kFmt), row stride lda bytes
+  const uint8_t* B;      // N x K 8-bit (B_T), row stride ldb bytes
+  uint16_t* C;           // M x N bf16 (fp16: kExt, epi.out), stride ldc elements
   const float* scale_a;  // device scalar, nullptr = 1.0
   const float* scale_b;  // device scalar, nullptr = 1.0
   int M, N, K;
@@ -49,6 +50,7 @@ struct SkinnyArgs {
   float* partial;   // tiles_n * slices * kMB * 16 * 256 floats
   int* arrivals;    // tiles_n counters, zero between calls
   int reduce_pass;  // 1: a separate kernel sums the slices (no counters)
+  EpiArgs epi;      // extended epilogue (kExt instantiations only)
 };
 
 struct CfgSkinny {
@@ -60,54 +62,34 @@ struct CfgSkinny {
   static constexpr int partial_floats() { return kMB * 16 * kBN; }
 };
 
-// Scales of the C elements one lane writes: rows 16 m + l % 16 (m <
-// kRows) and columns col0 + 16 f + 4 (l / 16) + i (f, i < 4).  Per-tensor:
-// the product of the two scalars; kRowCol: scale_a holds M floats, scale_b N
-// floats (null = 1.0), the element scale is row scale times column scale, one
-// fp32 product.  Rows or columns past M or N get 0 (never stored).
-template <int kRows, bool kRowCol>
-struct SkinnyScales {
+// Epilogue of the C elements one lane writes: rows 16 (m0 + m) + l % 16
+// (m < kRows) and columns col0 + 16 f + 4 (l / 16) + i (f, i < 4).  Plain:
+// the product of the two per-tensor scalars; kExt: the extended epilogue of
+// epilogue.hpp from g.epi (vectors zero past M or N, never stored).
+template <int kRows, bool kExt>
+struct SkinnyEpi {
   float s = 1.0f;
-  float r[kRowCol ? kRows : 1];
-  float c[kRowCol ? 4 : 1][4];
+  EpiVec<kExt ? kRows : 1, kExt ? 4 : 1> ev;
   __device__ __forceinline__ void load(const SkinnyArgs& g, int m0, int col0,
                                        int lane) {
-    if constexpr (!kRowCol) {
-      const float sa = g.scale_a ? *g.scale_a : 1.0f;
-      const float sb = g.scale_b ? *g.scale_b : 1.0f;
-      s = sa * sb;
-    } else {
-      const int r16 = lane & 15, c4 = 4 * (lane >> 4);
-      const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.scale_a, (uint32_t)g.M * 4);
-      const __amdgpu_buffer_rsrc_t rb = make_rsrc(g.scale_b, (uint32_t)g.N * 4);
-#pragma unroll
-      for (int m = 0; m < kRows; ++m)
-        r[m] = g.scale_a ? __builtin_bit_cast(
-                               float, __builtin_amdgcn_raw_buffer_load_b32(
-                                          ra, (uint32_t)(16 * (m0 + m) + r16) * 4u, 0, 0))
-                         : 1.0f;
-#pragma unroll
-      for (int f = 0; f < 4; ++f)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          c[f][i] = g.scale_b ? __builtin_bit_cast(
-                                    float, __builtin_amdgcn_raw_buffer_load_b32(
-                                               rb, (uint32_t)(col0 + 16 * f + c4 + i) * 4u, 0, 0))
-                              : 1.0f;
-    }
+    const float sa = g.scale_a ? *g.scale_a : 1.0f;
+    const float sb = g.scale_b ? *g.scale_b : 1.0f;
+    s = sa * sb;
+    if constexpr (kExt) ev.load(g.epi, g.M, g.N, 16 * m0, col0, s, lane);
   }
-  __device__ __forceinline__ float at(int m, int f, int i) const {
-    if constexpr (kRowCol)
-      return r[m] * c[f][i];
+  // Elements i = 0..3 of block (m, f), packed.
+  __device__ __forceinline__ u32x2 pack4(const f32x4& v, int m, int f) const {
+    if constexpr (kExt)
+      return ev.pack4(v[0], v[1], v[2], v[3], m, f);
     else
-      return s;
+      return u32x2{pack_bf16x2(v[0] * s, v[1] * s), pack_bf16x2(v[2] * s, v[3] * s)};
   }
 };
 
 // kMB: 16-row blocks of M (M <= 16 kMB).  kVec8: C rows allow 8-byte stores
-// (N % 4 == 0, ldc % 4 == 0, C 8-byte aligned).  kRowCol: per-row /
-// per-column scales (SkinnyScales).
-template <int kMB, bool kVec8, bool kRowCol = false>
+// (N % 4 == 0, ldc % 4 == 0, C 8-byte aligned).  kExt: the extended
+// epilogue (SkinnyEpi).
+template <int kMB, bool kVec8, bool kExt = false, int kFmt = 0>
 __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   using Cfg = CfgSkinny;
   // A (at most 128 rows) is shared by the four waves: up to 32 rows each
@@ -222,7 +204,8 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
       }
 #pragma unroll
       for (int f = 0; f < 4; ++f)
-        acc[m][f] = mfma_16x16x128(join(bq[d][f][0], bq[d][f][1]), a, acc[m][f]);
+        acc[m][f] = mfma_16x16x128<fmt_b(kFmt), fmt_a(kFmt)>(
+            join(bq[d][f][0], bq[d][f][1]), a, acc[m][f]);
     }
   };
 
@@ -290,7 +273,7 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   }
 
   // ---- last arrival: sum the slices in order, scale, bf16, store ----------
-  SkinnyScales<kMB, kRowCol> scl;
+  SkinnyEpi<kMB, kExt> scl;
   scl.load(g, 0, n0 + wave * 64, lane);
   const __amdgpu_buffer_rsrc_t rsrc_c =
       make_rsrc(g.C + n0, (uint32_t)(((M - 1) * g.ldc + rows_b) * 2));
@@ -348,10 +331,8 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
       const int col = wave * 64 + 16 * f + 4 * grp;
       const uint32_t base = (uint32_t)((row * g.ldc + col) * 2) |
                             oob_unless(row, M);
-      const uint32_t lo = pack_bf16x2(sum[m][f][0] * scl.at(m, f, 0),
-                                      sum[m][f][1] * scl.at(m, f, 1));
-      const uint32_t hi = pack_bf16x2(sum[m][f][2] * scl.at(m, f, 2),
-                                      sum[m][f][3] * scl.at(m, f, 3));
+      const u32x2 pk = scl.pack4(sum[m][f], m, f);
+      const uint32_t lo = pk.x, hi = pk.y;
       if constexpr (kVec8) {
         __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc_c,
                                               base | oob_unless(col, rows_b), 0, 0);
@@ -376,7 +357,7 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
 // the in-kernel reduction, spread over tiles_n x kMB workgroups instead of
 // one per tile.  Launched on the same stream right after the split kernel,
 // so its partial tiles are visible without any fence.
-template <bool kVec8, bool kRowCol = false>
+template <bool kVec8, bool kExt = false>
 __device__ __forceinline__ void gemm_skinny_reduce_body(const SkinnyArgs& g,
                                                         int kmb) {
   using Cfg = CfgSkinny;
@@ -399,7 +380,7 @@ __device__ __forceinline__ void gemm_skinny_reduce_body(const SkinnyArgs& g,
   };
   // Scales first: their latency hides under the slice loads (read after the
   // loop they cost this short kernel one more memory round trip).
-  SkinnyScales<1, kRowCol> scl;
+  SkinnyEpi<1, kExt> scl;
   scl.load(g, m, n0 + wave * 64, lane);
   constexpr int kBatch = 8;  // slices whose loads are in flight together
   f32x4 sum[4] = {};
@@ -431,10 +412,8 @@ __device__ __forceinline__ void gemm_skinny_reduce_body(const SkinnyArgs& g,
     const int row = 16 * m + r16;
     const int col = wave * 64 + 16 * f + 4 * grp;
     const uint32_t base = (uint32_t)((row * g.ldc + col) * 2) | oob_unless(row, M);
-    const uint32_t lo = pack_bf16x2(sum[f][0] * scl.at(0, f, 0),
-                                    sum[f][1] * scl.at(0, f, 1));
-    const uint32_t hi = pack_bf16x2(sum[f][2] * scl.at(0, f, 2),
-                                    sum[f][3] * scl.at(0, f, 3));
+    const u32x2 pk = scl.pack4(sum[f], 0, f);
+    const uint32_t lo = pk.x, hi = pk.y;
     if constexpr (kVec8) {
       __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, rsrc_c,
                                             base | oob_unless(col, rows_b), 0, 0);

@@ -70,6 +70,89 @@ uint8_t hg_f32_to_e4m3(float x) {
   return sign | (uint8_t)(((Ev + 7) << 3) | mant);
 }
 
+/* ------------------------------------------------------------------------ */
+/* OCP E5M2 (an extension: the reference is e4m3 only).  1 sign, 5 exponent */
+/* (bias 15), 2 mantissa bits -- the upper byte of an IEEE binary16:         */
+/* exponent field 31 is infinity (m = 0) or NaN, field 0 is subnormal        */
+/* (m * 2^-16); the largest finite magnitude is 1.75 * 2^15 = 57344.         */
+/* ------------------------------------------------------------------------ */
+float hg_e5m2_to_f32(uint8_t v) {
+  const int e = (v >> 2) & 31, m = v & 3;
+  float mag;
+  if (e == 31)
+    mag = m ? NAN : INFINITY;
+  else if (e == 0)
+    mag = ldexpf((float)m, -16);
+  else
+    mag = ldexpf((float)(4 + m), e - 17);
+  return (v & 0x80) ? -mag : mag;
+}
+
+/* Round-to-nearest-even onto the e5m2 grid, IEEE overflow: magnitudes from
+ * 61440 (halfway from 57344 to 2^16) up become infinity, NaN stays NaN
+ * (0x7f | sign).  Same method as hg_f32_to_e4m3. */
+uint8_t hg_f32_to_e5m2(float x) {
+  const uint32_t u = f32_bits(x);
+  const uint8_t sign = (uint8_t)((u >> 24) & 0x80);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7f;    /* NaN                       */
+  const float ax = bits_f32(a);
+  if (ax >= 61440.0f) return sign | 0x7c;     /* rounds past 57344: inf    */
+  int e2;
+  (void)frexpf(ax, &e2);
+  int E = e2 - 1;                             /* ax in [2^E, 2^(E+1))      */
+  if (a == 0 || E < -14) E = -14;             /* subnormal quantum 2^-16   */
+  const int qexp = E - 2;                     /* 2 mantissa bits           */
+  const float n = rintf(ldexpf(ax, -qexp));
+  if (n == 0.0f) return sign;
+  const float v = ldexpf(n, qexp);
+  if (v < 6.103515625e-05f)                   /* < 2^-14: subnormal        */
+    return sign | (uint8_t)ldexpf(v, 16);
+  int ve;
+  (void)frexpf(v, &ve);
+  const int Ev = ve - 1;
+  const int mant = (int)ldexpf(v, 2 - Ev) - 4;
+  return sign | (uint8_t)(((Ev + 15) << 2) | mant);
+}
+
+/* IEEE binary16, round-to-nearest-even, overflow to infinity, NaN kept NaN
+ * (quiet).  Method: as above on the 10-bit mantissa grid. */
+uint16_t hg_f32_to_f16(float x) {
+  const uint32_t u = f32_bits(x);
+  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7e00;
+  const float ax = bits_f32(a);
+  if (ax >= 65520.0f) return sign | 0x7c00;   /* halfway past 65504: inf   */
+  int e2;
+  (void)frexpf(ax, &e2);
+  int E = e2 - 1;
+  if (a == 0 || E < -14) E = -14;             /* subnormal quantum 2^-24   */
+  const int qexp = E - 10;
+  const float n = rintf(ldexpf(ax, -qexp));
+  if (n == 0.0f) return sign;
+  const float v = ldexpf(n, qexp);
+  if (v < 6.103515625e-05f) return sign | (uint16_t)ldexpf(v, 24);
+  int ve;
+  (void)frexpf(v, &ve);
+  const int Ev = ve - 1;
+  const int mant = (int)ldexpf(v, 10 - Ev) - 1024;
+  return sign | (uint16_t)(((Ev + 15) << 10) | mant);
+}
+
+void hg_e5m2_to_f32_n(const uint8_t *x, float *out, size_t n) {
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i) out[i] = hg_e5m2_to_f32(x[i]);
+}
+void hg_f32_to_e5m2_n(const float *x, uint8_t *out, size_t n) {
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i) out[i] = hg_f32_to_e5m2(x[i]);
+}
+void hg_f32_to_f16_n(const float *x, uint16_t *out, size_t n) {
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i) out[i] = hg_f32_to_f16(x[i]);
+}
+
 /* bf16 = upper half of an fp32 with round-to-nearest-even on the dropped
  * half (what __hip_bfloat16(float), test.cpp:27, does on the host); NaN is
  * kept NaN with the quiet bit set. */
@@ -151,6 +234,7 @@ float hg_draw_scale(uint64_t seed, double lo, double hi) {
 /* GEMM                                                                      */
 /* ------------------------------------------------------------------------ */
 static float g_e4m3_lut[256];
+static float g_e5m2_lut[256];
 static int g_lut_ready = 0;
 
 static void lut_init(void) {
@@ -158,10 +242,18 @@ static void lut_init(void) {
 #pragma omp critical(hg_lut)
   {
     if (!g_lut_ready) {
-      for (int i = 0; i < 256; ++i) g_e4m3_lut[i] = hg_e4m3_to_f32((uint8_t)i);
+      for (int i = 0; i < 256; ++i) {
+        g_e4m3_lut[i] = hg_e4m3_to_f32((uint8_t)i);
+        g_e5m2_lut[i] = hg_e5m2_to_f32((uint8_t)i);
+      }
       g_lut_ready = 1;
     }
   }
+}
+
+static const float *lut_of(int fmt) {
+  lut_init();
+  return fmt == HG_FMT_E5M2 ? g_e5m2_lut : g_e4m3_lut;
 }
 
 static inline uint16_t epilogue(float acc, float s) {
@@ -189,19 +281,23 @@ void hg_gemm_ref(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
   }
 }
 
-/* B_T decoded and transposed to Bt[K][N] fp32. */
-static float *decode_bt(const uint8_t *B_T, int N, int K, int ldb) {
+/* B_T decoded (format fmt) and transposed to Bt[K][N] fp32. */
+static float *decode_bt_fmt(const uint8_t *B_T, int N, int K, int ldb,
+                            int fmt) {
   float *Bt = (float *)malloc((size_t)K * N * sizeof(float));
   if (!Bt) return NULL;
-  lut_init();
+  const float *lut = lut_of(fmt);
 #pragma omp parallel for schedule(static)
   for (int kb = 0; kb < K; kb += 64) {
     const int ke = kb + 64 < K ? kb + 64 : K;
     for (int n = 0; n < N; ++n)
       for (int k = kb; k < ke; ++k)
-        Bt[(size_t)k * N + n] = g_e4m3_lut[B_T[(size_t)n * ldb + k]];
+        Bt[(size_t)k * N + n] = lut[B_T[(size_t)n * ldb + k]];
   }
   return Bt;
+}
+static float *decode_bt(const uint8_t *B_T, int N, int K, int ldb) {
+  return decode_bt_fmt(B_T, N, K, ldb, HG_FMT_E4M3);
 }
 
 #define RB 8   /* rows per block    */
@@ -209,9 +305,9 @@ static float *decode_bt(const uint8_t *B_T, int N, int K, int ldb) {
 
 /* acc[r][j] for rows rows[0..nr) and columns [n0, n0+nc): per output the K
  * sum runs k = 0, 1, ..., K-1 in fp32, as in the reference. */
-static void block_acc(const uint8_t *A, const float *Bt, const int *rows,
-                      int nr, int n0, int nc, int N, int K, int lda,
-                      float acc[RB][CB]) {
+static void block_acc(const uint8_t *A, const float *lut_a, const float *Bt,
+                      const int *rows, int nr, int n0, int nc, int N, int K,
+                      int lda, float acc[RB][CB]) {
   const uint8_t *arow[RB];
   for (int r = 0; r < RB; ++r) {
     arow[r] = A + (size_t)rows[r < nr ? r : 0] * lda;
@@ -220,7 +316,7 @@ static void block_acc(const uint8_t *A, const float *Bt, const int *rows,
   for (int k = 0; k < K; ++k) {
     const float *b = Bt + (size_t)k * N + n0;
     for (int r = 0; r < RB; ++r) {
-      const float a = g_e4m3_lut[arow[r][k]];
+      const float a = lut_a[arow[r][k]];
       float *ac = acc[r];
       if (nc == CB) {
 #pragma omp simd
@@ -232,12 +328,46 @@ static void block_acc(const uint8_t *A, const float *Bt, const int *rows,
   }
 }
 
+/* The extended epilogue of hg_gemm_ex. */
+typedef struct {
+  float s;                        /* scale_a * scale_b                     */
+  const float *sr, *sc, *bias;    /* NULL: ones / ones / -0.0              */
+  int act, out;
+} epi_t;
+
+/* The activations from their definitions, in double (the reference for the
+ * kernels' fp32 hardware-exponential evaluation). */
+static float act_f(float v, int act) {
+  const double x = v;
+  switch (act) {
+    case HG_ACT_RELU:
+      return v < 0.0f ? 0.0f : v;
+    case HG_ACT_SILU:
+      return (float)(x / (1.0 + exp(-x)));
+    case HG_ACT_GELU_TANH:
+      return (float)(0.5 * x *
+                     (1.0 + tanh(0.7978845608028654 * (x + 0.044715 * x * x * x))));
+    default:
+      return v;
+  }
+}
+
+static uint16_t epi_value(float acc, int m, int n, const epi_t *e) {
+  const float sr = e->sr ? e->sr[m] : 1.0f;
+  const float sc = e->sc ? e->sc[n] : 1.0f;
+  const float scale = sr * (sc * e->s);
+  const float v = fmaf(acc, scale, e->bias ? e->bias[n] : -0.0f);
+  const float y = act_f(v, e->act);
+  return e->out == HG_OUT_F16 ? hg_f32_to_f16(y) : hg_f32_to_bf16(y);
+}
+
 /* mode 0: bf16 of acc * s, or, with sa / sb given (row / column scale
  * vectors, either may be NULL = 1.0), of acc * (sa[row] * sb[col]); mode 1:
- * the fp32 acc itself. */
-static void rows_impl(const uint8_t *A, const float *Bt, const int *rows,
-                      int nrows, int N, int K, int lda, void *out, int ldo,
-                      int mode, float s, const float *sa, const float *sb) {
+ * the fp32 acc itself; mode 2: the extended epilogue `ep`. */
+static void rows_impl_lut(const uint8_t *A, const float *lut_a,
+                          const float *Bt, const int *rows, int nrows, int N,
+                          int K, int lda, void *out, int ldo, int mode, float s,
+                          const float *sa, const float *sb, const epi_t *ep) {
   const int nrb = (nrows + RB - 1) / RB, ncb = (N + CB - 1) / CB;
 #pragma omp parallel for collapse(2) schedule(dynamic, 1)
   for (int rb = 0; rb < nrb; ++rb) {
@@ -246,11 +376,13 @@ static void rows_impl(const uint8_t *A, const float *Bt, const int *rows,
       const int r0 = rb * RB, n0 = cb * CB;
       const int nr = nrows - r0 < RB ? nrows - r0 : RB;
       const int nc = N - n0 < CB ? N - n0 : CB;
-      block_acc(A, Bt, rows + r0, nr, n0, nc, N, K, lda, acc);
+      block_acc(A, lut_a, Bt, rows + r0, nr, n0, nc, N, K, lda, acc);
       for (int r = 0; r < nr; ++r)
         for (int j = 0; j < nc; ++j) {
           const size_t o = (size_t)(r0 + r) * ldo + n0 + j;
-          if (mode == 0 && (sa || sb)) {
+          if (mode == 2) {
+            ((uint16_t *)out)[o] = epi_value(acc[r][j], rows[r0 + r], n0 + j, ep);
+          } else if (mode == 0 && (sa || sb)) {
             const float rs = sa ? sa[rows[r0 + r]] : 1.0f;
             const float cs = sb ? sb[n0 + j] : 1.0f;
             ((uint16_t *)out)[o] = epilogue(acc[r][j], rs * cs);
@@ -262,6 +394,29 @@ static void rows_impl(const uint8_t *A, const float *Bt, const int *rows,
         }
     }
   }
+}
+
+static void rows_impl(const uint8_t *A, const float *Bt, const int *rows,
+                      int nrows, int N, int K, int lda, void *out, int ldo,
+                      int mode, float s, const float *sa, const float *sb) {
+  rows_impl_lut(A, lut_of(HG_FMT_E4M3), Bt, rows, nrows, N, K, lda, out, ldo,
+                mode, s, sa, sb, NULL);
+}
+
+void hg_gemm_ex(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
+                int N, int K, int lda, int ldb, int ldc, int a_fmt, int b_fmt,
+                int out, int act, float scale_a, float scale_b,
+                const float *scale_rows, const float *scale_cols,
+                const float *bias) {
+  float *Bt = decode_bt_fmt(B_T, N, K, ldb, b_fmt);
+  int *rows = (int *)malloc((size_t)(M > 0 ? M : 1) * sizeof(int));
+  if (!Bt || !rows) abort();
+  for (int i = 0; i < M; ++i) rows[i] = i;
+  const epi_t ep = {scale_a * scale_b, scale_rows, scale_cols, bias, act, out};
+  rows_impl_lut(A, lut_of(a_fmt), Bt, rows, M, N, K, lda, C, ldc, 2, 1.0f, NULL,
+                NULL, &ep);
+  free(rows);
+  free(Bt);
 }
 
 void hg_gemm_fast(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,

@@ -110,6 +110,38 @@ void hg_gemm_rows_f64(const uint8_t *A, const uint8_t *B_T, double *acc_rows,
                       const int *rows, int nrows, int N, int K, int lda,
                       int ldb);
 
+/* ---- Extensions beyond the reference: other formats, fused epilogue ----- */
+enum { HG_FMT_E4M3 = 0, HG_FMT_E5M2 = 1 };
+enum { HG_OUT_BF16 = 0, HG_OUT_F16 = 1 };
+enum { HG_ACT_NONE = 0, HG_ACT_RELU = 1, HG_ACT_GELU_TANH = 2, HG_ACT_SILU = 3 };
+/* OCP E5M2 decode (exact) and RNE encode (overflow to inf, NaN -> NaN),
+ * IEEE binary16 RNE encode.  Pinned: e5m2 decode against its closed form
+ * (the upper byte of a binary16, numpy float16); e5m2 encode against
+ * torch's float8_e5m2 conversion and f16 encode against numpy's float16
+ * conversion on large samples plus every boundary (tests/test_oracle.py). */
+float hg_e5m2_to_f32(uint8_t v);
+uint8_t hg_f32_to_e5m2(float x);
+uint16_t hg_f32_to_f16(float x);
+void hg_e5m2_to_f32_n(const uint8_t *x, float *out, size_t n);
+void hg_f32_to_e5m2_n(const float *x, uint8_t *out, size_t n);
+void hg_f32_to_f16_n(const float *x, uint16_t *out, size_t n);
+/* The hipgemm_gemm semantics: acc = the same sequential-K fp32 sum as
+ * hg_gemm_fast over A decoded as a_fmt and B_T as b_fmt (the products of two
+ * 8-bit values are exact in fp32 for every pair of these formats), then
+ *   scale = scale_rows[m] * (scale_cols[n] * (scale_a * scale_b))
+ *   v = fmaf(acc, scale, bias[n])   (bias NULL: -0.0)
+ *   C = out(act(v))                 (bf16 or f16 bits, RNE)
+ * with the activation evaluated in double from its definition.  Pinned:
+ * the defaults equal hg_gemm_fast and vectors alone equal hg_gemm_rowcol
+ * bit for bit; e5m2 operands against fp64 sums of the decoded values;
+ * bias against an fp64 fma; activations against scipy's expit and torch's
+ * tanh-approximated gelu; f16 output against numpy. */
+void hg_gemm_ex(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
+                int N, int K, int lda, int ldb, int ldc, int a_fmt, int b_fmt,
+                int out, int act, float scale_a, float scale_b,
+                const float *scale_rows, const float *scale_cols,
+                const float *bias);
+
 /* Threads OpenMP will use (for reporting cpu_baseline.cores). */
 int hg_num_threads(void);
 

@@ -23,6 +23,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 
 UNIFORM = 0
 NORMAL = 1
+# hg_gemm_ex codes (oracle.h; the values of include/hipgemm.h's)
+FMT_E4M3, FMT_E5M2 = 0, 1
+OUT_BF16, OUT_F16 = 0, 1
+ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3
 
 _c_u8p = ctypes.POINTER(ctypes.c_uint8)
 _vp = ctypes.c_void_p
@@ -52,7 +56,9 @@ class Oracle:
         L.hg_bf16_to_f32.restype = ctypes.c_float
         L.hg_bf16_to_f32.argtypes = [ctypes.c_uint16]
         for name in ("hg_f32_to_e4m3_n", "hg_e4m3_to_f32_n",
-                     "hg_f32_to_bf16_n", "hg_bf16_to_f32_n"):
+                     "hg_f32_to_bf16_n", "hg_bf16_to_f32_n",
+                     "hg_e5m2_to_f32_n", "hg_f32_to_e5m2_n",
+                     "hg_f32_to_f16_n"):
             getattr(L, name).argtypes = [_vp, _vp, ctypes.c_size_t]
             getattr(L, name).restype = None
         L.hg_rand64.restype = ctypes.c_uint64
@@ -74,6 +80,9 @@ class Oracle:
         L.hg_gemm_rowcol.argtypes = [_vp, _vp, _vp] + [ctypes.c_int] * 6 + \
             [_vp, _vp]
         L.hg_gemm_rowcol.restype = None
+        L.hg_gemm_ex.argtypes = [_vp, _vp, _vp] + [ctypes.c_int] * 10 + \
+            [ctypes.c_float] * 2 + [_vp, _vp, _vp]
+        L.hg_gemm_ex.restype = None
         L.hg_gemm_rows.argtypes = [_vp, _vp, _vp, _vp] + [ctypes.c_int] * 5 + \
             [ctypes.c_float] * 2
         L.hg_gemm_rows.restype = None
@@ -106,6 +115,28 @@ class Oracle:
         out = np.empty(x.shape, np.float32)
         self.lib.hg_bf16_to_f32_n(_ptr(x), _ptr(out), x.size)
         return out
+
+    def e5m2_to_f32(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.uint8)
+        out = np.empty(x.shape, np.float32)
+        self.lib.hg_e5m2_to_f32_n(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def f32_to_e5m2(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty(x.shape, np.uint8)
+        self.lib.hg_f32_to_e5m2_n(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def f32_to_f16(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty(x.shape, np.uint16)
+        self.lib.hg_f32_to_f16_n(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def decode(self, x: np.ndarray, fmt: int) -> np.ndarray:
+        """fp32 values of 8-bit operands in format fmt (FMT_E4M3 / FMT_E5M2)."""
+        return self.e5m2_to_f32(x) if fmt == FMT_E5M2 else self.e4m3_to_f32(x)
 
     # -- generators --------------------------------------------------------
     def fill(self, shape: Sequence[int], seed: int, dist: int = UNIFORM,
@@ -160,6 +191,35 @@ class Oracle:
         self.lib.hg_gemm_rowcol(_ptr(A), _ptr(B), _ptr(C), M, N, K, K, K, N,
                                 None if sr is None else _ptr(sr),
                                 None if sc is None else _ptr(sc))
+        return C
+
+    def gemm_ex(self, A: np.ndarray, B: np.ndarray, a_fmt: int = FMT_E4M3,
+                b_fmt: int = FMT_E4M3, out: int = OUT_BF16, act: int = ACT_NONE,
+                scale_a: float = 1.0, scale_b: float = 1.0,
+                scale_rows: Optional[np.ndarray] = None,
+                scale_cols: Optional[np.ndarray] = None,
+                bias: Optional[np.ndarray] = None) -> np.ndarray:
+        """Output bits (bf16 or f16) of the hipgemm_gemm semantics
+        (oracle.h: hg_gemm_ex)."""
+        A = np.ascontiguousarray(A)
+        B = np.ascontiguousarray(B)
+        M, K = A.shape
+        N = B.shape[0]
+        assert B.shape[1] == K
+
+        def vec(v, n):
+            if v is None:
+                return None
+            v = np.ascontiguousarray(v, np.float32)
+            assert v.shape == (n,)
+            return v
+        sr, sc, bb = vec(scale_rows, M), vec(scale_cols, N), vec(bias, N)
+        C = np.empty((M, N), np.uint16)
+        self.lib.hg_gemm_ex(_ptr(A), _ptr(B), _ptr(C), M, N, K, K, K, N,
+                            a_fmt, b_fmt, out, act, scale_a, scale_b,
+                            None if sr is None else _ptr(sr),
+                            None if sc is None else _ptr(sc),
+                            None if bb is None else _ptr(bb))
         return C
 
     def gemm_rows(self, A: np.ndarray, B: np.ndarray, rows: Sequence[int],

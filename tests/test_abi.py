@@ -132,6 +132,28 @@ def test_rowcol_entry_validation():
     assert hg.gemm_raw_rowcol(*args, FAKE + 64, need) == INVALID   # misaligned
 
 
+def test_gemm_desc_entry_validation():
+    """hipgemm_gemm: the descriptor's size must match (a size-0 problem with
+    the right size is a no-op, so the ctypes layout is the C one); codes,
+    vector alignment and the 32x32x64 schedule's limits are checked before
+    any HIP call."""
+    base = dict(A=FAKE, B_T=FAKE, C=FAKE, M=300, N=300, K=64, lda=64, ldb=64,
+                ldc=300)
+    assert hg.gemm_desc_raw(hg.GemmDesc(**dict(base, M=0))) == 0
+    bad_size = hg.GemmDesc(**base)
+    bad_size.size -= 8
+    assert hg.gemm_desc_raw(bad_size) == INVALID
+    assert hg.lib().hipgemm_gemm(None, None) == INVALID
+    for bad in (dict(a_format=2), dict(b_format=-1), dict(out_dtype=2),
+                dict(activation=4), dict(scale_rows=FAKE + 2),
+                dict(scale_cols=FAKE + 1), dict(bias=FAKE + 3),
+                dict(variant=1, a_format=1), dict(variant=1, bias=FAKE),
+                dict(variant=1, out_dtype=1), dict(variant=1, activation=1),
+                dict(variant=3),  # M = 300 > 128
+                dict(K=40, lda=48, ldb=48), dict(variant=9)):
+        assert hg.gemm_desc_raw(hg.GemmDesc(**dict(base, **bad))) == INVALID, bad
+
+
 def test_dropin_entry_validates_too():
     L = hg.lib()
     assert L.hipgemm_fp8_gemm_4wave_256x256x128(None, None, None, 64, 64, 64,

@@ -277,3 +277,160 @@ def test_golden_vectors(oracle):
         sa, sb = (float(x) for x in z[nm + "_S"])
         assert np.array_equal(oracle.gemm(A, B, sa, sb), C), nm
         assert np.array_equal(oracle.gemm(A, B, sa, sb, faithful=True), C), nm
+
+
+# ---- extensions: e5m2 operands, f16 output, bias, activations -------------
+
+def _f16_bits(x):
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+def test_e5m2_decode_is_upper_byte_of_binary16(oracle):
+    """Closed form: an e5m2 byte b is the binary16 with bits b << 8."""
+    codes = np.arange(256, dtype=np.uint8)
+    got = oracle.e5m2_to_f32(codes)
+    want = (codes.astype(np.uint16) << 8).view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert got[0x7b] == 57344.0 and got[0x01] == 2.0 ** -16 and np.isinf(got[0x7c])
+
+
+def _probe_floats(seed, n=1 << 21):
+    """Every binary16 value (so every e5m2 / f16 grid point), its float32
+    neighbours and midpoints, plus random floats over the whole range."""
+    h = np.arange(1 << 16, dtype=np.uint16).view(np.float16).astype(np.float32)
+    h = h[np.isfinite(h)]
+    mids = ((h[:-1].astype(np.float64) + h[1:]) / 2).astype(np.float32)
+    rng = np.random.default_rng(seed)
+    rnd = rng.integers(0, 1 << 32, n, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    near = np.concatenate([np.nextafter(h, np.float32(np.inf)),
+                           np.nextafter(h, np.float32(-np.inf))])
+    extra = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 61440.0, 61439.996,
+                      65504.0, 65519.996, 65520.0, 2.0 ** -17, 2.0 ** -25,
+                      3 * 2.0 ** -25], np.float32)
+    return np.concatenate([h, mids, near, rnd, extra])
+
+
+def test_e5m2_encode_vs_torch(oracle):
+    torch = pytest.importorskip("torch")
+    x = _probe_floats(7)
+    got = oracle.f32_to_e5m2(x)
+    want = torch.from_numpy(x).to(torch.float8_e5m2).view(torch.uint8).numpy()
+    nan_g = ((got & 0x7c) == 0x7c) & ((got & 3) != 0)
+    nan_w = ((want & 0x7c) == 0x7c) & ((want & 3) != 0)
+    assert np.array_equal(nan_g, nan_w)
+    bad = np.flatnonzero((got != want) & ~nan_w)
+    assert bad.size == 0, [(float(x[i]), int(got[i]), int(want[i])) for i in bad[:8]]
+
+
+def test_f16_encode_vs_numpy(oracle):
+    x = _probe_floats(8)
+    got = oracle.f32_to_f16(x)
+    with np.errstate(over="ignore"):
+        want = _f16_bits(x)
+    nan = np.isnan(x)
+    assert np.all((got[nan] & 0x7c00) == 0x7c00) and np.all(got[nan] & 0x3ff)
+    bad = np.flatnonzero((got != want) & ~nan)
+    assert bad.size == 0, [(float(x[i]), int(got[i]), int(want[i])) for i in bad[:8]]
+
+
+def test_gemm_ex_defaults_equal_per_tensor_and_rowcol(oracle):
+    M, N, K = 37, 45, 208
+    A, B = _inputs(oracle, M, N, K, 41)
+    assert np.array_equal(oracle.gemm_ex(A, B, scale_a=1.5, scale_b=0.75),
+                          oracle.gemm(A, B, 1.5, 0.75))
+    rng = np.random.default_rng(41)
+    sr = rng.uniform(0.25, 4, M).astype(np.float32)
+    sc = rng.uniform(0.25, 4, N).astype(np.float32)
+    assert np.array_equal(oracle.gemm_ex(A, B, scale_rows=sr, scale_cols=sc),
+                          oracle.gemm_rowcol(A, B, sr, sc))
+
+
+# values exact in both e4m3 and e5m2: {0, +-0.5, +-1, +-1.5, +-2, +-3}
+_BOTH = np.array([0.0, 0.5, -0.5, 1.0, -1.0, 1.5, -1.5, 2.0, -2.0, 3.0, -3.0],
+                 np.float32)
+
+
+def test_gemm_ex_formats_pinned_by_reencoding(oracle):
+    """The same values encoded as e4m3 or e5m2 give the same product, for
+    every format pair, and that product is the fp64 one (all partial sums
+    of these values are exact in fp32).  A swapped format, a wrong exponent
+    bias or the wrong table for one operand fails this."""
+    M, N, K = 23, 31, 272
+    rng = np.random.default_rng(42)
+    va = _BOTH[rng.integers(0, len(_BOTH), (M, K))]
+    vb = _BOTH[rng.integers(0, len(_BOTH), (N, K))]
+    enc = {po.FMT_E4M3: oracle.f32_to_e4m3, po.FMT_E5M2: oracle.f32_to_e5m2}
+    want = oracle.f32_to_bf16((va.astype(np.float64) @ vb.T.astype(np.float64))
+                              .astype(np.float32))
+    for fa in (po.FMT_E4M3, po.FMT_E5M2):
+        for fb in (po.FMT_E4M3, po.FMT_E5M2):
+            A, B = enc[fa](va), enc[fb](vb)
+            assert np.array_equal(oracle.decode(A, fa), va)
+            got = oracle.gemm_ex(A, B, a_fmt=fa, b_fmt=fb)
+            assert np.array_equal(got, want), (fa, fb)
+    # e5m2-only magnitudes (beyond e4m3's 448 and below its 2^-9)
+    A = oracle.f32_to_e5m2(np.array([[2.0 ** 14], [2.0 ** -16]], np.float32))
+    B = oracle.f32_to_e5m2(np.array([[2.0], [2.0 ** 10]], np.float32))
+    got = oracle.bf16_to_f32(oracle.gemm_ex(A, B, a_fmt=po.FMT_E5M2,
+                                            b_fmt=po.FMT_E5M2))
+    assert got[0, 0] == 2.0 ** 15 and got[1, 1] == 2.0 ** -6
+
+
+def test_gemm_ex_bias_is_one_fma(oracle):
+    """v = fma(acc, scale, bias): with exact sums, scale a power of two and
+    the bias on a nearby exponent, the fp64 sum is exact and its rounding is
+    the fma's; a separately rounded product would differ on ties."""
+    M, N, K = 16, 64, 256
+    rng = np.random.default_rng(43)
+    A = np.array([0xB8, 0x00, 0x38], np.uint8)[rng.integers(0, 3, (M, K))]
+    B = np.array([0xB8, 0x00, 0x38], np.uint8)[rng.integers(0, 3, (N, K))]
+    bias = rng.uniform(-8, 8, N).astype(np.float32)
+    got = oracle.gemm_ex(A, B, scale_a=0.25, bias=bias)
+    acc = oracle.e4m3_to_f32(A).astype(np.float64) @ oracle.e4m3_to_f32(B).T.astype(np.float64)
+    want = oracle.f32_to_bf16((acc * 0.25 + bias.astype(np.float64)).astype(np.float32))
+    assert np.array_equal(got, want)
+    # no bias: exactly acc * scale, -0 kept
+    neg0 = oracle.gemm_ex(np.zeros((1, 16), np.uint8), np.zeros((1, 16), np.uint8),
+                          scale_a=-1.0)
+    assert neg0[0, 0] == 0x8000 == oracle.gemm(np.zeros((1, 16), np.uint8),
+                                               np.zeros((1, 16), np.uint8), -1.0)[0, 0]
+
+
+def test_gemm_ex_activations_vs_library_routines(oracle):
+    """relu exactly; silu against scipy's expit, gelu (tanh form) against
+    torch's, both in float64, within one bf16 ulp of the oracle's output."""
+    torch = pytest.importorskip("torch")
+    from scipy.special import expit
+    M, N, K = 24, 96, 128
+    A, B = _inputs(oracle, M, N, K, 44)
+    bias = np.random.default_rng(44).uniform(-2, 2, N).astype(np.float32)
+    base = oracle.gemm_ex(A, B, scale_a=0.125, bias=bias, out=po.OUT_BF16)
+    rows = np.arange(M, dtype=np.int32)
+    acc = oracle.gemm_rows_acc(A, B, rows)
+    # fma(acc, 1/8, bias): the fp64 value acc/8 + bias is exact (acc has 24
+    # bits, bias is within 2^4 of it), so rounding it once is the fma
+    v = (acc.astype(np.float64) * 0.125 + bias).astype(np.float32)
+    assert np.array_equal(oracle.f32_to_bf16(v), base)
+    relu = oracle.gemm_ex(A, B, scale_a=0.125, bias=bias, act=po.ACT_RELU)
+    assert np.array_equal(relu, oracle.f32_to_bf16(np.where(v < 0, 0, v).astype(np.float32)))
+    x = v.astype(np.float64)
+    refs = {po.ACT_SILU: x * expit(x),
+            po.ACT_GELU_TANH: torch.nn.functional.gelu(torch.from_numpy(x),
+                                                       approximate="tanh").numpy()}
+    for act, ref in refs.items():
+        got = oracle.bf16_to_f32(oracle.gemm_ex(A, B, scale_a=0.125, bias=bias, act=act))
+        want = oracle.bf16_to_f32(oracle.f32_to_bf16(ref.astype(np.float32)))
+        ulp = np.abs(want) * 2.0 ** -7 + 1e-30
+        assert np.all(np.abs(got - want) <= ulp), act
+        assert np.mean(got == want) > 0.99, act
+
+
+def test_gemm_ex_f16_output(oracle):
+    M, N, K = 20, 40, 160
+    A, B = _inputs(oracle, M, N, K, 45)
+    acc = oracle.gemm_rows_acc(A, B, np.arange(M, dtype=np.int32))
+    got = oracle.gemm_ex(A, B, scale_a=3.0, out=po.OUT_F16)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(got, _f16_bits(acc * np.float32(3.0)))
