@@ -10,8 +10,14 @@ Importing this module registers, in the ``hipgemm`` namespace:
                                     variant=0)
       the same with per-row (M) / per-column (N) float32 scale vectors --
       hipgemm_fp8_gemm_bf16_rowcol.
+  torch.ops.hipgemm.gemm(a, b_t, scale_a=None, scale_b=None, scale_rows=None,
+                         scale_cols=None, bias=None, activation="none",
+                         out_f16=False, variant=0)
+      the general entry point (hipgemm_gemm): a / b_t float8_e4m3fn or
+      float8_e5m2 (uint8 bytes: e4m3), fused bias and activation ("none",
+      "relu", "silu", "gelu_tanh"), bf16 or fp16 output.
 
-Both have fake (meta) implementations, so they trace under torch.compile,
+All have fake (meta) implementations, so they trace under torch.compile,
 torch.export and FakeTensorMode without running, and they run inside CUDA
 graph capture (the split-K workspace is allocated on first use per stream,
 before capture if the caller warms up).  The device implementation is
@@ -20,7 +26,8 @@ libhipgemm.so; CPU tensors raise HipGemmError -- there is no CPU path.
 Fp8Linear is a drop-in for torch.nn.Linear in LLM projections (the reference
 has no layer; its LLM shapes are benchmark configurations): e4m3 weights with
 one fp32 scale per output channel, activations quantised per token (row) on
-the fly, the product through fp8_gemm_rowcol.
+the fly, the product through hipgemm::gemm with the bias and activation
+fused into its epilogue.
 """
 from __future__ import annotations
 
@@ -28,9 +35,11 @@ from typing import Optional
 
 import torch
 
-from . import HipGemmError, fp8_gemm_bf16, fp8_gemm_bf16_rowcol
+from . import ACTIVATIONS, HipGemmError, fp8_gemm_bf16, fp8_gemm_bf16_rowcol
+from . import gemm as _gemm
 
-__all__ = ["fp8_gemm", "fp8_gemm_rowcol", "Fp8Linear", "quantize_rows"]
+__all__ = ["fp8_gemm", "fp8_gemm_rowcol", "gemm", "Fp8Linear",
+           "quantize_rows"]
 
 E4M3_MAX = 448.0
 
@@ -69,6 +78,36 @@ def _fp8_gemm_rowcol_fake(a, b_t, scale_rows=None, scale_cols=None,
     return a.new_empty((a.shape[0], b_t.shape[0]), dtype=torch.bfloat16)
 
 
+@torch.library.custom_op("hipgemm::gemm", mutates_args=())
+def gemm(a: torch.Tensor, b_t: torch.Tensor,
+         scale_a: Optional[torch.Tensor] = None,
+         scale_b: Optional[torch.Tensor] = None,
+         scale_rows: Optional[torch.Tensor] = None,
+         scale_cols: Optional[torch.Tensor] = None,
+         bias: Optional[torch.Tensor] = None, activation: str = "none",
+         out_f16: bool = False, variant: int = 0) -> torch.Tensor:
+    return _gemm(a, b_t, out_dtype=torch.float16 if out_f16 else torch.bfloat16,
+                 scale_a=scale_a, scale_b=scale_b, scale_rows=scale_rows,
+                 scale_cols=scale_cols, bias=bias, activation=activation,
+                 variant=variant)
+
+
+@gemm.register_fake
+def _gemm_fake(a, b_t, scale_a=None, scale_b=None, scale_rows=None,
+               scale_cols=None, bias=None, activation="none", out_f16=False,
+               variant=0):
+    _check_shapes(a, b_t)
+    if activation not in ACTIVATIONS:
+        raise HipGemmError(f"unknown activation {activation!r}")
+    for v, n, name in ((scale_rows, a.shape[0], "scale_rows"),
+                       (scale_cols, b_t.shape[0], "scale_cols"),
+                       (bias, b_t.shape[0], "bias")):
+        if v is not None and tuple(v.shape) != (n,):
+            raise HipGemmError(f"{name} must have {n} elements")
+    return a.new_empty((a.shape[0], b_t.shape[0]),
+                       dtype=torch.float16 if out_f16 else torch.bfloat16)
+
+
 def _check_shapes(a, b_t):
     if a.dim() != 2 or b_t.dim() != 2 or a.shape[1] != b_t.shape[1]:
         raise HipGemmError(f"expected a (M, K) and b_t (N, K), got "
@@ -87,14 +126,17 @@ def quantize_rows(x: torch.Tensor):
 
 
 class Fp8Linear(torch.nn.Module):
-    """y = x W^T + b with W (out x in) held as e4m3 rows and one float32
-    scale per output feature; x is quantised per token (row) to e4m3 with
-    its own scale, and the product runs through hipgemm's per-row /
-    per-column entry point: y[t, o] = bf16(acc[t, o] * (sx[t] * sw[o])).
-    in_features must be a multiple of 16."""
+    """y = act(x W^T + b) with W (out x in) held as e4m3 rows and one
+    float32 scale per output feature; x is quantised per token (row) to e4m3
+    with its own scale, and the product runs through hipgemm's general
+    entry point with the scales, the bias and the activation fused:
+    y[t, o] = bf16(act(fma(acc[t, o], sx[t] * sw[o], b[o]))).
+    in_features must be a multiple of 16.  activation: None, "relu", "silu"
+    or "gelu_tanh"."""
 
     def __init__(self, weight_e4m3: torch.Tensor, weight_scale: torch.Tensor,
-                 bias: Optional[torch.Tensor] = None, variant: int = 0):
+                 bias: Optional[torch.Tensor] = None, variant: int = 0,
+                 activation: Optional[str] = None):
         super().__init__()
         if weight_e4m3.dtype != torch.float8_e4m3fn or weight_e4m3.dim() != 2:
             raise HipGemmError("weight must be a 2-D float8_e4m3fn tensor")
@@ -106,7 +148,10 @@ class Fp8Linear(torch.nn.Module):
         self.register_buffer("weight_scale",
                              weight_scale.to(torch.float32).contiguous())
         self.register_buffer("bias", None if bias is None else
-                             bias.to(torch.bfloat16).contiguous())
+                             bias.to(torch.float32).contiguous())
+        if activation not in ACTIVATIONS:
+            raise HipGemmError(f"unknown activation {activation!r}")
+        self.activation = activation or "none"
         self.variant = variant
 
     @property
@@ -118,18 +163,19 @@ class Fp8Linear(torch.nn.Module):
         return self.weight.shape[0]
 
     @classmethod
-    def from_linear(cls, linear: torch.nn.Linear, variant: int = 0):
+    def from_linear(cls, linear: torch.nn.Linear, variant: int = 0,
+                    activation: Optional[str] = None):
         """Quantise a Linear's weight per output channel (amax / 448)."""
         w, s = quantize_rows(linear.weight.detach())
         return cls(w, s, linear.bias.detach() if linear.bias is not None
-                   else None, variant)
+                   else None, variant, activation)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         lead = x.shape[:-1]
         x2 = x.reshape(-1, self.in_features)
         q, s = quantize_rows(x2)
-        y = torch.ops.hipgemm.fp8_gemm_rowcol(q, self.weight, s,
-                                              self.weight_scale, self.variant)
-        if self.bias is not None:
-            y = y + self.bias
+        y = torch.ops.hipgemm.gemm(q, self.weight, scale_rows=s,
+                                   scale_cols=self.weight_scale, bias=self.bias,
+                                   activation=self.activation,
+                                   variant=self.variant)
         return y.reshape(*lead, self.out_features)

@@ -12,7 +12,8 @@ from torch._subclasses.fake_tensor import FakeTensorMode
 
 import hipgemm_amd as hg
 import hipgemm_amd.torch_ops as ops
-from util import REL_TOL, say
+from oracle import pyoracle as po
+from util import REL_TOL, compare, say
 
 E4M3 = torch.float8_e4m3fn
 
@@ -50,7 +51,20 @@ def test_fp8_linear_traces_as_one_op():
     with FakeTensorMode(allow_non_fake_inputs=True) as mode:
         gm = make_fx(layer, tracing_mode="fake")(mode.from_tensor(x))
     targets = [str(n.target) for n in gm.graph.nodes if n.op == "call_function"]
-    assert targets.count("hipgemm.fp8_gemm_rowcol.default") == 1, targets
+    assert targets.count("hipgemm.gemm.default") == 1, targets
+
+
+def test_general_op_fake_shapes():
+    with FakeTensorMode():
+        a = torch.empty((64, 256), dtype=torch.float8_e5m2)
+        b = torch.empty((96, 256), dtype=E4M3)
+        y = torch.ops.hipgemm.gemm(a, b, bias=torch.empty(96),
+                                   activation="silu", out_f16=True)
+        assert tuple(y.shape) == (64, 96) and y.dtype == torch.float16
+        with pytest.raises(hg.HipGemmError):
+            torch.ops.hipgemm.gemm(a, b, bias=torch.empty(95))
+        with pytest.raises(hg.HipGemmError):
+            torch.ops.hipgemm.gemm(a, b, activation="tanh")
 
 
 def test_cpu_tensors_fail_loudly():
@@ -165,34 +179,49 @@ def test_cuda_graph_replays(gpu):
 
 
 @pytest.mark.gpu
+def test_general_op_equals_abi(gpu, oracle):
+    torch_ = gpu
+    M, N, K = 256, 384, 512
+    say(f"case torch-op gemm M={M} N={N} K={K}")
+    a, b = _inputs(torch_, M, N, K, 66)
+    a5 = a.float().to(torch_.float8_e5m2)
+    bias = torch_.randn(N, device="cuda")
+    y = torch_.ops.hipgemm.gemm(a5, b, bias=bias, activation="gelu_tanh",
+                                out_f16=True)
+    ref = hg.gemm(a5, b, bias=bias, activation="gelu_tanh",
+                  out_dtype=torch_.float16)
+    torch_.cuda.synchronize()
+    assert y.dtype == torch_.float16
+    assert torch_.equal(y.view(torch_.int16), ref.view(torch_.int16))
+
+
+@pytest.mark.gpu
 def test_fp8_linear_matches_fp32_on_quantised_operands(gpu, oracle):
-    """Fp8Linear on an LLM-shaped projection against the oracle's per-row /
-    per-column GEMM of the same quantised operands (north_star tolerance),
-    plus the bias."""
+    """Fp8Linear on an LLM-shaped projection, bias and activation fused,
+    against the oracle's general GEMM of the same quantised operands
+    (north_star tolerance)."""
     torch_ = gpu
     torch_.manual_seed(65)
     lin = torch_.nn.Linear(1024, 3072).cuda()
-    layer = ops.Fp8Linear.from_linear(lin)
+    layer = ops.Fp8Linear.from_linear(lin, activation="silu")
     x = torch_.randn(2, 160, 1024, device="cuda")
-    say("case fp8-linear tokens=320 in=1024 out=3072")
+    say("case fp8-linear tokens=320 in=1024 out=3072 silu")
     y = layer(x)
     torch_.cuda.synchronize()
     assert tuple(y.shape) == (2, 160, 3072) and y.dtype == torch_.bfloat16
     q, s = ops.quantize_rows(x.reshape(-1, 1024))
     A = q.view(torch_.uint8).cpu().numpy()
     B = layer.weight.view(torch_.uint8).cpu().numpy()
-    want = oracle.gemm_rowcol(A, B, s.cpu().numpy(),
-                              layer.weight_scale.cpu().numpy())
-    want_f = torch_.from_numpy(want.view(np.int16)).view(torch_.bfloat16).float()
-    got_f = (y.reshape(-1, 3072).float() - layer.bias.float()).cpu()
-    # bias added in bf16: compare the GEMM part within one bf16 ulp of |y|
-    diff = (got_f - want_f).abs()
-    tol = REL_TOL * want_f.abs().clamp(min=float(want_f.abs().mean())) + \
-        2.0 ** -8 * y.reshape(-1, 3072).float().abs().cpu()
-    assert bool((diff <= tol).all()), float((diff - tol).max())
+    want = oracle.gemm_ex(A, B, act=po.ACT_SILU, scale_rows=s.cpu().numpy(),
+                          scale_cols=layer.weight_scale.cpu().numpy(),
+                          bias=layer.bias.cpu().numpy())
+    got = y.reshape(-1, 3072).view(torch_.int16).cpu().numpy().view(np.uint16)
+    max_rel, exact, _ = compare(got, want)
+    say(f"    max_rel={max_rel:.3e} exact={exact:.4f}")
+    assert max_rel <= REL_TOL
     # and the layer tracks the full-precision Linear to e4m3 accuracy
     with torch_.no_grad():
-        ref = lin(x)
+        ref = torch_.nn.functional.silu(lin(x))
     rel = float((y.float() - ref).norm() / ref.norm())
     say(f"    rel-vs-fp32-linear={rel:.3e}")
     assert rel < 0.05
