@@ -32,6 +32,7 @@ __all__ = [
     "declared_symbols", "gemm_raw_ws", "workspace_size",
     "fp8_gemm_bf16_rowcol", "gemm_raw_rowcol", "GemmDesc", "gemm_desc_raw",
     "gemm", "FMT_E4M3", "FMT_E5M2", "OUT_BF16", "OUT_F16", "ACTIVATIONS",
+    "mx_scales_bytes", "mx_pack_scales",
 ]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -65,7 +66,9 @@ class GemmDesc(ctypes.Structure):
                 ("scale_cols", ctypes.c_void_p), ("bias", ctypes.c_void_p),
                 ("variant", ctypes.c_int),
                 ("workspace", ctypes.c_void_p),
-                ("workspace_bytes", ctypes.c_size_t)]
+                ("workspace_bytes", ctypes.c_size_t),
+                ("mx_scale_a", ctypes.c_void_p),
+                ("mx_scale_b", ctypes.c_void_p)]
 
     def __init__(self, **kw):
         super().__init__()
@@ -75,7 +78,7 @@ class GemmDesc(ctypes.Structure):
 
 
 _PTR_FIELDS = {"A", "B_T", "C", "scale_a", "scale_b", "scale_rows",
-               "scale_cols", "bias", "workspace"}
+               "scale_cols", "bias", "workspace", "mx_scale_a", "mx_scale_b"}
 
 
 class HipGemmError(RuntimeError):
@@ -120,6 +123,10 @@ def lib() -> ctypes.CDLL:
     L.hipgemm_fp8_gemm_bf16_rowcol.restype = ci
     L.hipgemm_gemm.argtypes = [ctypes.POINTER(GemmDesc), vp]
     L.hipgemm_gemm.restype = ci
+    L.hipgemm_mx_scales_bytes.argtypes = [ci, ci]
+    L.hipgemm_mx_scales_bytes.restype = ctypes.c_size_t
+    L.hipgemm_mx_pack_scales.argtypes = [vp, ci, ci, ci, vp, vp]
+    L.hipgemm_mx_pack_scales.restype = ci
     L.hipgemm_workspace_size.argtypes = [ci, ci, ci, ci]
     L.hipgemm_workspace_size.restype = ctypes.c_size_t
     L.hipgemm_fp8_gemm_4wave_256x256x128.argtypes = [vp, vp, vp, ci, ci, ci,
@@ -187,6 +194,33 @@ def gemm_raw_rowcol(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int,
 def gemm_desc_raw(desc: "GemmDesc", stream: int = 0) -> int:
     """Call hipgemm_gemm; returns hipError_t."""
     return int(lib().hipgemm_gemm(ctypes.byref(desc), stream or None))
+
+
+def mx_scales_bytes(rows: int, K: int) -> int:
+    """Bytes of the packed MX scale layout (hipgemm_mx_scales_bytes)."""
+    return int(lib().hipgemm_mx_scales_bytes(rows, K))
+
+
+def mx_pack_scales(scales, K: int, stream=None):
+    """Packs E8M0 block scales (a uint8 device tensor rows x ceil(K/32),
+    unit column stride) into the device layout hipgemm_gemm reads."""
+    torch = _torch()
+    if scales.dtype != torch.uint8 or scales.dim() != 2 or not scales.is_cuda \
+            or (scales.numel() and scales.stride(1) != 1):
+        raise HipGemmError("scales must be a 2-D uint8 device tensor with unit "
+                           "column stride", hipErrorInvalidValue)
+    rows = scales.shape[0]
+    if scales.shape[1] != (K + 31) // 32:
+        raise HipGemmError("scales must have ceil(K/32) columns",
+                           hipErrorInvalidValue)
+    stream = stream or torch.cuda.current_stream(scales.device)
+    out = torch.empty(max(mx_scales_bytes(rows, K), 1), dtype=torch.uint8,
+                      device=scales.device)
+    ld = scales.stride(0) if rows > 1 else scales.shape[1]
+    _check(int(lib().hipgemm_mx_pack_scales(
+        scales.data_ptr() or None, rows, K, ld, out.data_ptr(),
+        stream.cuda_stream or None)), "hipgemm_mx_pack_scales")
+    return out
 
 
 def workspace_size(M: int, N: int, K: int, variant: int = 0) -> int:
@@ -271,6 +305,17 @@ def _vector_ptr(s, n, name):
     return s.data_ptr()
 
 
+def _mx_ptr(t, rows, K, name):
+    if t is None:
+        return 0
+    torch = _torch()
+    if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.uint8
+            and t.numel() >= mx_scales_bytes(rows, K)):
+        raise HipGemmError(f"{name} must be a packed uint8 device tensor "
+                           "(mx_pack_scales)", hipErrorInvalidValue)
+    return t.data_ptr()
+
+
 def _gemm_operands(a, b_t, out, variant, stream):
     """Shared argument handling of the torch entry points: shapes, strides,
     output, stream and workspace."""
@@ -322,7 +367,7 @@ def fp8_gemm_bf16(a, b_t, scale_a=None, scale_b=None, out=None,
 def gemm(a, b_t, *, a_format: int = FMT_E4M3, b_format: int = FMT_E4M3,
          out_dtype=None, scale_a=None, scale_b=None, scale_rows=None,
          scale_cols=None, bias=None, activation=None, out=None,
-         variant: int = 0, stream=None):
+         variant: int = 0, stream=None, mx_scale_a=None, mx_scale_b=None):
     """The general entry point (hipgemm_gemm): out[m, n] =
     round(act(fma(acc, scale_rows[m] * (scale_cols[n] * (scale_a *
     scale_b)), bias[n]))), acc = a @ b_t.T with a in a_format and b_t in
@@ -330,7 +375,9 @@ def gemm(a, b_t, *, a_format: int = FMT_E4M3, b_format: int = FMT_E4M3,
     it from their dtype).  out_dtype: torch.bfloat16 (default) or
     torch.float16.  activation: None, "relu", "gelu_tanh" or "silu".
     scale_a / scale_b: 1-element float32 device tensors; scale_rows (M),
-    scale_cols (N), bias (N): float32 device vectors; any may be None."""
+    scale_cols (N), bias (N): float32 device vectors; any may be None.
+    mx_scale_a / mx_scale_b: MX block scales packed by mx_pack_scales
+    (both or neither)."""
     torch = _torch()
     fmts = {torch.float8_e4m3fn: FMT_E4M3, torch.float8_e5m2: FMT_E5M2}
     a_format = fmts.get(a.dtype, a_format)
@@ -361,7 +408,9 @@ def gemm(a, b_t, *, a_format: int = FMT_E4M3, b_format: int = FMT_E4M3,
                  scale_rows=_vector_ptr(scale_rows, M, "scale_rows"),
                  scale_cols=_vector_ptr(scale_cols, N, "scale_cols"),
                  bias=_vector_ptr(bias, N, "bias"), variant=variant,
-                 workspace=ws, workspace_bytes=nbytes)
+                 workspace=ws, workspace_bytes=nbytes,
+                 mx_scale_a=_mx_ptr(mx_scale_a, M, K, "mx_scale_a"),
+                 mx_scale_b=_mx_ptr(mx_scale_b, N, K, "mx_scale_b"))
     _check(gemm_desc_raw(d, stream.cuda_stream), "hipgemm_gemm")
     return out.view(out_dtype)
 

@@ -97,6 +97,10 @@ hipError_t launch_tiled(int variant, GemmArgs g, hk::Key key,
       fn = key.ext ? nullptr : hk::four_wave_plain(32, key);
       break;
     default:
+      if (g.mx.a) {
+        fn = hk::four_wave_mx(key);
+        break;
+      }
       fn = !key.ext ? hk::four_wave_plain(16, key)
            : key.out == HIPGEMM_OUT_F16 ? hk::four_wave_ext_f16(key)
                                         : hk::four_wave_ext_bf16(key);
@@ -196,7 +200,14 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   // epilogue only.
   if (variant == HIPGEMM_VARIANT_4WAVE && (ext || fmt != 0))
     return hipErrorInvalidValue;
-  variant = resolve_variant(variant, M, N, K);
+  // MX block scales: the 4-wave 16x16x128 schedule, per-tensor epilogue.
+  const bool mx = d.mx_scale_a || d.mx_scale_b;
+  if (mx && (!d.mx_scale_a || !d.mx_scale_b || K % 32 != 0 || ext ||
+             !aligned(d.mx_scale_a, 16) || !aligned(d.mx_scale_b, 16) ||
+             (variant != HIPGEMM_VARIANT_AUTO &&
+              variant != HIPGEMM_VARIANT_4WAVE_MFMA16)))
+    return hipErrorInvalidValue;
+  variant = mx ? HIPGEMM_VARIANT_4WAVE_MFMA16 : resolve_variant(variant, M, N, K);
   if (K == 0) lda = ldb = 16;  // nothing is read; keep the offset math inert
   const int tiles_m = (M + Cfg4w::kBM - 1) / Cfg4w::kBM;
   const int tiles_n = (N + Cfg4w::kBN - 1) / Cfg4w::kBN;
@@ -213,12 +224,15 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
              d.ldc,
              default_group_m(tiles_m, tiles_n),
              0,
-             EpiArgs{}};
+             EpiArgs{},
+             MxArgs{}};
   g.epi.row_scale = d.scale_rows;
   g.epi.col_scale = d.scale_cols;
   g.epi.bias = d.bias;
   g.epi.act = d.activation;
   g.epi.out = d.out_dtype;
+  g.mx.a = static_cast<const uint8_t*>(d.mx_scale_a);
+  g.mx.b = static_cast<const uint8_t*>(d.mx_scale_b);
   hk::Key key;
   key.fmt = fmt;
   key.ext = ext;
@@ -331,6 +345,20 @@ hipError_t hipgemm_gemm(const hipgemm_gemm_desc* desc, hipStream_t stream) {
   return run_gemm(*desc,
                   desc->workspace != nullptr || desc->workspace_bytes != 0,
                   stream);
+}
+
+size_t hipgemm_mx_scales_bytes(int rows, int K) {
+  if (rows <= 0 || K <= 0) return 0;
+  return mx_packed_bytes(rows, K);
+}
+
+hipError_t hipgemm_mx_pack_scales(const void* src, int rows, int K, int ld,
+                                  void* dst, hipStream_t stream) {
+  if (rows < 0 || K < 0 || K % 32 != 0) return hipErrorInvalidValue;
+  if (rows == 0 || K == 0) return hipSuccess;
+  if (!src || !dst || ld < K / 32) return hipErrorInvalidValue;
+  return hk::mx_pack(static_cast<const uint8_t*>(src), rows, K, ld,
+                     static_cast<uint8_t*>(dst), stream);
 }
 
 size_t hipgemm_workspace_size(int M, int N, int K, int variant) {

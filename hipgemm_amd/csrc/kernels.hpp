@@ -35,6 +35,10 @@ const void* eight_wave_ext_f16(const Key& k);       // k8wave_ext_f16.hip
 const void* skinny_plain(int kmb, const Key& k);    // kskinny_plain.hip
 const void* skinny_ext(int kmb, const Key& k);      // kskinny_ext.hip
 const void* skinny_reduce(const Key& k);            // kskinny_plain.hip
+const void* four_wave_mx(const Key& k);             // k4wave_mx.hip
+// Packs [rows][ceil(K/32)] E8M0 scales (row stride ld) into MxArgs' layout.
+hipError_t mx_pack(const uint8_t* src, int rows, int K, int ld, uint8_t* dst,
+                   hipStream_t stream);
 
 // Runtime value -> integral_constant, for building the lookups.
 template <int I>

@@ -123,6 +123,14 @@ typedef struct hipgemm_gemm_desc {
   int variant;                          /* HIPGEMM_VARIANT_* */
   void *workspace; /* as for hipgemm_fp8_gemm_bf16_ws; NULL with size 0: */
   size_t workspace_bytes; /* allocate one when needed, stream-ordered    */
+  /* MX block scales (OCP Microscaling v1.0): E8M0 bytes, one per 32
+   * consecutive K-elements of a row of A / B_T, 2^(e - 127), 255 = NaN,
+   * in the packed device layout hipgemm_mx_pack_scales writes.  Both or
+   * neither; K % 32 == 0, 16-byte aligned.  Each element is multiplied by its
+   * block's scale before the products are summed; the per-tensor scales
+   * still apply.  Not combined with the row / column / bias / activation /
+   * fp16 options; schedules AUTO and HIPGEMM_VARIANT_4WAVE_MFMA16. */
+  const void *mx_scale_a, *mx_scale_b;
 } hipgemm_gemm_desc;
 
 /*
@@ -195,6 +203,21 @@ hipError_t hipgemm_fp8_gemm_bf16_rowcol(const void *A, const void *B_T, void *C,
  * store_rt, :214-238, converts the accumulator straight to bf16).
  */
 hipError_t hipgemm_gemm(const hipgemm_gemm_desc *desc, hipStream_t stream);
+
+/*
+ * MX scale packing.  hipgemm_mx_scales_bytes: bytes of the packed layout for
+ * an operand of `rows` rows and K columns (0 for rows or K <= 0).
+ * hipgemm_mx_pack_scales: packs src, `rows` x ceil(K/32) E8M0 bytes with
+ * row stride ld bytes (device), into dst (device, that many bytes),
+ * stream-ordered.  The layout groups, per 128 rows and per two 128-wide
+ * K-steps, what one wave's MFMA need (padding scales are 1.0).  Returns
+ * hipErrorInvalidValue for K % 32 != 0, ld < K / 32 or null pointers.
+ * No reference counterpart (the reference passes zero scales,
+ * fp8_4wave.hpp:58).
+ */
+size_t hipgemm_mx_scales_bytes(int rows, int K);
+hipError_t hipgemm_mx_pack_scales(const void *src, int rows, int K, int ld,
+                                  void *dst, hipStream_t stream);
 
 /* Workspace bytes hipgemm_fp8_gemm_bf16_ws needs for this shape and variant
  * on the current device (0: none).  No GPU work.  No reference counterpart. */

@@ -118,6 +118,41 @@ __device__ __forceinline__ f32x4 mfma_16x16x128(i32x8 x, i32x8 y, f32x4 acc) {
                                                           0, 0, 0, 0);
 }
 
+// The same with E8M0 block scales (2^(e - 127); 255 is NaN), one byte per
+// lane in the low byte of sx / sy: lane l gives the scale of row l % 16 of X
+// / Y for K-block l / 16 (K 32 (l / 16) .. + 31).  In the instruction's K
+// order, lane l carries K 16 (l / 16) .. + 15 in registers 0-3 and
+// 64 + 16 (l / 16) .. + 15 in registers 4-7, so K-block b is held by lane
+// groups 2b % 4 and 2b % 4 + 1, in registers 0-3 for b < 2 and 4-7 for
+// b >= 2.
+// kOx / kOy (op_sel) pick the byte of sx / sy that holds the scale.
+template <int kFx, int kFy, int kOx, int kOy>
+__device__ __forceinline__ f32x4 mfma_16x16x128_mx(i32x8 x, i32x8 y, f32x4 acc,
+                                                   uint32_t sx, uint32_t sy) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+      x, y, acc, kFx, kFy, kOx, (int)sx, kOy, (int)sy);
+}
+// The same with the bytes ox, oy (0..3) given as values: in unrolled code,
+// where they are constants, the switch folds to the one instruction (no
+// shifts of the scale words).
+template <int kFx = kFmtE4M3, int kFy = kFmtE4M3>
+__device__ __forceinline__ f32x4 mfma_16x16x128_mx(i32x8 x, i32x8 y, f32x4 acc,
+                                                   uint32_t sx, uint32_t sy,
+                                                   int ox, int oy) {
+#define HIPGEMM_MX_CASE(X, Y) \
+  case 4 * X + Y:             \
+    return mfma_16x16x128_mx<kFx, kFy, X, Y>(x, y, acc, sx, sy);
+  switch (4 * ox + oy) {
+    HIPGEMM_MX_CASE(0, 0) HIPGEMM_MX_CASE(0, 1) HIPGEMM_MX_CASE(0, 2)
+    HIPGEMM_MX_CASE(0, 3) HIPGEMM_MX_CASE(1, 0) HIPGEMM_MX_CASE(1, 1)
+    HIPGEMM_MX_CASE(1, 2) HIPGEMM_MX_CASE(1, 3) HIPGEMM_MX_CASE(2, 0)
+    HIPGEMM_MX_CASE(2, 1) HIPGEMM_MX_CASE(2, 2) HIPGEMM_MX_CASE(2, 3)
+    HIPGEMM_MX_CASE(3, 0) HIPGEMM_MX_CASE(3, 1) HIPGEMM_MX_CASE(3, 2)
+    default: return mfma_16x16x128_mx<kFx, kFy, 3, 3>(x, y, acc, sx, sy);
+  }
+#undef HIPGEMM_MX_CASE
+}
+
 // One accumulator element (AGPR) -> VGPR at this point of the program.  The
 // compiler otherwise copies every live accumulator to VGPRs at the end of the
 // K loop in one burst, which needs 256 VGPRs on top of the live ones.

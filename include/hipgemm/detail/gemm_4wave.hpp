@@ -71,6 +71,23 @@
 namespace hipgemm {
 namespace detail {
 
+// MX block scales (E8M0, one per 32 K-elements of a row), packed by
+// hipgemm_mx_pack_scales: for each group of 128 rows W and each pair of
+// 128-byte K-steps p, 1 KiB holding, for lane l, 16 bytes: step 0 then step
+// 1, each the scales of rows 128 W + 16 f + l % 16 (f = 0..7) for K-block
+// l / 16 of that step -- what one wave's 16x16x128 MFMA need, in one 16-byte
+// load per operand per step pair.  W-groups of P = ceil(ceil(K / 128) / 2)
+// pairs.  Null: no MX scaling.
+struct MxArgs {
+  const uint8_t* a = nullptr;
+  const uint8_t* b = nullptr;
+};
+
+__host__ __device__ constexpr int mx_pairs(int K) { return ((K + 127) / 128 + 1) / 2; }
+__host__ __device__ constexpr size_t mx_packed_bytes(int rows, int K) {
+  return (size_t)((rows + 127) / 128) * mx_pairs(K) * 1024;
+}
+
 struct GemmArgs {
   const uint8_t* A;      // M x K 8-bit (format by kFmt), row stride lda bytes
   const uint8_t* B;      // N x K 8-bit (B_T), row stride ldb bytes
@@ -82,6 +99,7 @@ struct GemmArgs {
   int group_m;
   int workers;  // persistent workgroups (<= grid); 0 = the whole grid
   EpiArgs epi;  // extended epilogue (kExt instantiations only)
+  MxArgs mx;    // MX block scales (kMx instantiations only)
 };
 
 // The GemmArgs of a kernel whose only argument is a GemmArgs, read again
@@ -93,6 +111,13 @@ kernel_args() {
       __builtin_amdgcn_kernarg_segment_ptr();
   asm volatile("" : "+s"(p));
   return p;
+}
+__device__ __forceinline__ MxArgs kernel_mx() {
+  const auto* k = kernel_args();
+  MxArgs m;
+  m.a = k->mx.a;
+  m.b = k->mx.b;
+  return m;
 }
 __device__ __forceinline__ EpiArgs kernel_epi() {
   const auto* k = kernel_args();
@@ -208,13 +233,15 @@ __device__ __forceinline__ TileSrc tile_src(const GemmArgs& g, int t,
 // kAct / kOut (kExt only): the activation and the output type
 // (epilogue.hpp) -- template parameters, so that each instantiation has one
 // straight-line epilogue.
+// kMx: MX block scales from g.mx (16x16x128, per-tensor epilogue).
 template <bool kVecStore, int kMf = 32, bool kExt = false, int kFmt = 0,
-          int kAct = kActNone, int kOut = kOutBf16>
+          int kAct = kActNone, int kOut = kOutBf16, bool kMx = false>
 __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                                                 lds_u8* lds) {
   using Cfg = Cfg4w;
   static_assert(kMf == 32 || kMf == 16, "MFMA shape");
   static_assert(!kExt || kMf == 16, "extended epilogue: 16x16x128 only");
+  static_assert(!kMx || (kMf == 16 && !kExt), "MX: 16x16x128, plain epilogue");
   constexpr bool k16 = kMf == 16;
   constexpr int kDmaPerGroup = 4;  // per wave
   constexpr int kWaitSteady = 4 * kDmaPerGroup;
@@ -268,15 +295,21 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   const lds_u8* pb[2][2] = {{lds + off_b, lds + (off_b ^ 16u)},
                             {lds + (off_b ^ 64u), lds + (off_b ^ 80u)}};
   // 16x16x128: fragment row lane%16; lane group g = lane/16 reads K-chunks
-  // 2g and 2g + 1 (32 bytes).
+  // 2g and 2g + 1 (32 bytes).  Any K order serves a plain product as long as
+  // A and B share it; block scales need the instruction's own: its lane
+  // group g holds K 16g .. 16g + 15 in the first four registers and
+  // 64 + 16g .. 64 + 16g + 15 in the last four, so kMx reads K-chunks g and
+  // g + 4 (each 16-lane group reads one chunk per row: conflict-free either
+  // way).
   const int rrow16 = lane & 15;
-  const int rslot16 = (2 * (lane >> 4)) ^ slot_xor(rrow16);
+  const int rslot16 = ((kMx ? 1 : 2) * (lane >> 4)) ^ slot_xor(rrow16);
+  constexpr uint32_t kHalf16 = kMx ? 64u : 16u;  // chunk c -> c + 4 or c + 1
   const uint32_t off16_a =
       Cfg::kABase + (wm * 128 + rrow16) * Cfg::kBK + rslot16 * 16;
   const uint32_t off16_b =
       Cfg::kBBase + (wn * 128 + rrow16) * Cfg::kBK + rslot16 * 16;
-  const lds_u8* pa16[2] = {lds + off16_a, lds + (off16_a ^ 16u)};
-  const lds_u8* pb16[2] = {lds + off16_b, lds + (off16_b ^ 16u)};
+  const lds_u8* pa16[2] = {lds + off16_a, lds + (off16_a ^ kHalf16)};
+  const lds_u8* pb16[2] = {lds + off16_b, lds + (off16_b ^ kHalf16)};
 
   TileSrc cur = tile_src(g, t, walk.end, tiles_m, tiles_n);
   TileSrc nxt = tile_src(g, t + walk.stride, walk.end, tiles_m, tiles_n);
@@ -395,13 +428,21 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // Quarter (qi, qj): the wave's rows 64qi.. x columns 64qj.. (32x32x64:
   // blocks i in {2qi, 2qi+1} x j in {2qj, 2qj+1}, K-half major so the two
   // MFMA of one accumulator are 4 apart; 16x16x128: 4 x 4 blocks).
-  auto quarter_mfma = [&](int qi, int qj, int from, int to) {
+  // kMx: the scale words of the step the MFMA belong to, w = {A frags 0-3,
+  // A frags 4-7, B frags 0-3, B frags 4-7} (one byte per fragment).
+  auto quarter_mfma = [&](int qi, int qj, int from, int to,
+                          const uint32_t* w = nullptr) {
     if constexpr (k16) {
 #pragma unroll
       for (int n = from; n < to; ++n) {
         const int i = 4 * qi + n / 4, j = 4 * qj + n % 4;
-        acc16[i][j] = mfma_16x16x128<fmt_b(kFmt), fmt_a(kFmt)>(
-            fb16[j], fa16[i], acc16[i][j]);
+        if constexpr (kMx)
+          acc16[i][j] = mfma_16x16x128_mx<fmt_b(kFmt), fmt_a(kFmt)>(
+              fb16[j], fa16[i], acc16[i][j], w[2 + j / 4], w[i / 4], j % 4,
+              i % 4);
+        else
+          acc16[i][j] = mfma_16x16x128<fmt_b(kFmt), fmt_a(kFmt)>(
+              fb16[j], fa16[i], acc16[i][j]);
       }
       return;
     }
@@ -413,9 +454,42 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     }
   };
   using QS = QuarterShape<kMf>;
+  // kMx: scale words of the current step pair (mxc: A words 0-3, B words
+  // 4-7, as loaded), of the next pair (mxn, in flight), and of the previous
+  // step (mxp, for the tail MFMA that crosses into the next step).
+  uint32_t mxc[8] = {}, mxn[8] = {}, mxp[4] = {};
+  // Loads the scale words of the step pair starting at step kb2 (steps
+  // kb2 >= kt_pad: the next tile's) into dst: two 16-byte loads per lane,
+  // counted in vmcnt.  The whole offset is in the range-checked VGPR
+  // offset: tiles past the last, 128-row groups past M / N and the padding
+  // steps past the last pair read zero (scale 2^-127 on zero data).
+  auto mx_load = [&](int kb2, uint32_t (&dst)[8]) {
+    const bool next = kb2 >= kt_pad;
+    const int tt = next ? t + walk.stride : t;
+    const int p = (next ? kb2 - kt_pad : kb2) / 2;
+    const MxArgs mx = kernel_mx();
+    const int P = mx_pairs(K);
+    const bool live = tt < walk.end && p < P;
+    const TileCoord c = grouped_tile(live ? tt : t, tiles_m, tiles_n, g.group_m);
+    const __amdgpu_buffer_rsrc_t ra =
+        make_rsrc(mx.a, live ? (uint32_t)mx_packed_bytes(M, K) : 0u);
+    const __amdgpu_buffer_rsrc_t rb =
+        make_rsrc(mx.b, live ? (uint32_t)mx_packed_bytes(N, K) : 0u);
+    const uint32_t vo = (uint32_t)lane * 16u;
+    const i32x4 va = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+        ra, vo + (uint32_t)(((c.m * 2 + wm) * P + p) * 1024), 0, 0));
+    const i32x4 vb = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+        rb, vo + (uint32_t)(((c.n * 2 + wn) * P + p) * 1024), 0, 0));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      dst[q] = (uint32_t)va[q];
+      dst[4 + q] = (uint32_t)vb[q];
+    }
+  };
+
   // The last quarter-step's tail (issued after the K loop, before the
   // epilogue reads the accumulators).
-  auto last_tail = [&]() { quarter_mfma(1, 1, QS::kHead, QS::kMfma); };
+  auto last_tail = [&]() { quarter_mfma(1, 1, QS::kHead, QS::kMfma, mxp); };
 
   // One quarter-step: the previous quarter's tail MFMA (quarter tq) if
   // `tail`, the head MFMA of quarter q, the LDS reads of register tile
@@ -427,16 +501,19 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // scheduling region per pair.  (Written out for the default instantiation
   // too, it measured 0.6 % slower than the scheduler's own placement of the
   // address arithmetic.)
+  // kMx: w / wt are the scale words of this quarter's step and of the
+  // tail's.
   auto quarter = [&](bool tail, int tqi, int tqj, int qi, int qj, int rop,
-                     int rhi, int rst, int kb, int dst, int dop, int dhi) {
-    if constexpr (k16 && (kExt || kFmt != 0)) {
-      if (tail) quarter_mfma(tqi, tqj, QS::kHead, QS::kMfma);
+                     int rhi, int rst, int kb, int dst, int dop, int dhi,
+                     const uint32_t* w = nullptr, const uint32_t* wt = nullptr) {
+    if constexpr (k16 && (kExt || kFmt != 0 || kMx)) {
+      if (tail) quarter_mfma(tqi, tqj, QS::kHead, QS::kMfma, wt);
       const DmaSrc d = dma_src(kb, dop);
       sched_fence();
       i32x4 rd[8];
 #pragma unroll
       for (int n = 0; n < 8; ++n) {
-        quarter_mfma(qi, qj, n, n + 1);
+        quarter_mfma(qi, qj, n, n + 1, w);
         rd[n] = read16_one(rop, rhi, rst, n);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
@@ -444,13 +521,13 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       }
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        quarter_mfma(qi, qj, 8 + n, 9 + n);
+        quarter_mfma(qi, qj, 8 + n, 9 + n, w);
         dma_one(d, dst, dop, dhi, n);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         sched_fence();
       }
-      quarter_mfma(qi, qj, 12, QS::kHead);
+      quarter_mfma(qi, qj, 12, QS::kHead, w);
 #pragma unroll
       for (int f = 0; f < 4; ++f) {
         if (rop == 0)
@@ -493,16 +570,28 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       if constexpr (kExt && kFirst)
         if (s == 0) scale_dma(t);
       barrier();  // Q00
-      quarter(tail, 1, 1, 0, 0, 1, 1, s, kt + 2, s, 0, 0);
+      // kMx: this step's scale words; the next pair's are loaded here (after
+      // the wait, like scale_dma: at most two more stores retired early).
+      uint32_t w[4] = {mxc[2 * s], mxc[2 * s + 1], mxc[4 + 2 * s],
+                       mxc[4 + 2 * s + 1]};
+      if constexpr (kMx)
+        if (s == 0) mx_load(kt0 + 2, mxn);
+      quarter(tail, 1, 1, 0, 0, 1, 1, s, kt + 2, s, 0, 0, w, mxp);
       wait_lgkmcnt<0>();  // Q01
-      quarter(true, 0, 0, 0, 1, 0, 1, s, kt + 2, s, 1, 0);
+      quarter(true, 0, 0, 0, 1, 0, 1, s, kt + 2, s, 1, 0, w, w);
       wait_lgkmcnt<0>();
       if (kFirst && s == 0) wait_vmcnt<kWaitAfterStores>(); else wait_vmcnt<kWaitSteady>();
       barrier();  // Q10
-      quarter(true, 0, 1, 1, 0, 0, 0, s ^ 1, kt + 2, s, 1, 1);
+      quarter(true, 0, 1, 1, 0, 0, 0, s ^ 1, kt + 2, s, 1, 1, w, w);
       wait_lgkmcnt<0>();  // Q11
-      quarter(true, 1, 0, 1, 1, 1, 0, s ^ 1, kt + 2, s, 0, 1);
+      quarter(true, 1, 0, 1, 1, 1, 0, s ^ 1, kt + 2, s, 0, 1, w, w);
+      if constexpr (kMx)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) mxp[q] = w[q];
     }
+    if constexpr (kMx)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) mxc[q] = mxn[q];
   };
 
   // Prologue of the first tile: steps 0 and 1, all landed (so the relaxed
@@ -514,6 +603,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     dma_group(st, st, 1, 1);
     dma_group(st, st, 0, 1);
   }
+  if constexpr (kMx) mx_load(0, mxc);
   wait_vmcnt<0>();
   barrier();
   read_tile(0, 0, 0);

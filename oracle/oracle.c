@@ -419,6 +419,63 @@ void hg_gemm_ex(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
   free(Bt);
 }
 
+/* ------------------------------------------------------------------------ */
+/* MX block scales (OCP Microscaling v1.0, an extension: the reference has   */
+/* none).  One E8M0 scale per 32 consecutive K-elements of a row of A or     */
+/* B_T: the value 2^(e - 127), e = 255 is NaN.  Each operand is decoded and  */
+/* multiplied by its block scale (a power of two: exact unless it leaves     */
+/* the fp32 range), then summed in the same sequential fp32 K order as       */
+/* hg_gemm_fast.                                                             */
+/* ------------------------------------------------------------------------ */
+static inline float e8m0_value(uint8_t e) {
+  return e == 255 ? NAN : ldexpf(1.0f, (int)e - 127);
+}
+
+void hg_gemm_mx(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
+                int N, int K, int lda, int ldb, int ldc, int a_fmt, int b_fmt,
+                const uint8_t *sa, int ldsa, const uint8_t *sb, int ldsb,
+                float scale_a, float scale_b) {
+  const float *la = lut_of(a_fmt), *lb = lut_of(b_fmt);
+  float *Af = (float *)malloc((size_t)(M > 0 ? M : 1) * (K > 0 ? K : 1) * sizeof(float));
+  float *Bt = (float *)malloc((size_t)(N > 0 ? N : 1) * (K > 0 ? K : 1) * sizeof(float));
+  if (!Af || !Bt) abort();
+#pragma omp parallel for schedule(static)
+  for (int m = 0; m < M; ++m)
+    for (int k = 0; k < K; ++k)
+      Af[(size_t)m * K + k] =
+          la[A[(size_t)m * lda + k]] * e8m0_value(sa[(size_t)m * ldsa + k / 32]);
+#pragma omp parallel for schedule(static)
+  for (int k = 0; k < K; ++k)
+    for (int n = 0; n < N; ++n)
+      Bt[(size_t)k * N + n] =
+          lb[B_T[(size_t)n * ldb + k]] * e8m0_value(sb[(size_t)n * ldsb + k / 32]);
+  const float s = scale_a * scale_b;
+  const int ncb = (N + CB - 1) / CB;
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+  for (int m0 = 0; m0 < M; m0 += RB) {
+    for (int cb = 0; cb < ncb; ++cb) {
+      float acc[RB][CB] __attribute__((aligned(64)));
+      const int n0 = cb * CB;
+      const int nr = M - m0 < RB ? M - m0 : RB;
+      const int nc = N - n0 < CB ? N - n0 : CB;
+      for (int r = 0; r < RB; ++r)
+        for (int j = 0; j < CB; ++j) acc[r][j] = 0.0f;
+      for (int k = 0; k < K; ++k) {
+        const float *b = Bt + (size_t)k * N + n0;
+        for (int r = 0; r < nr; ++r) {
+          const float a = Af[(size_t)(m0 + r) * K + k];
+          for (int j = 0; j < nc; ++j) acc[r][j] += a * b[j];
+        }
+      }
+      for (int r = 0; r < nr; ++r)
+        for (int j = 0; j < nc; ++j)
+          C[(size_t)(m0 + r) * ldc + n0 + j] = epilogue(acc[r][j], s);
+    }
+  }
+  free(Af);
+  free(Bt);
+}
+
 void hg_gemm_fast(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
                   int N, int K, int lda, int ldb, int ldc, float scale_a,
                   float scale_b) {

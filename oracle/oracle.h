@@ -142,6 +142,18 @@ void hg_gemm_ex(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
                 const float *scale_rows, const float *scale_cols,
                 const float *bias);
 
+/* MX block scales (OCP Microscaling v1.0): sa is M x ceil(K/32) E8M0 bytes
+ * (row stride ldsa), sb N x ceil(K/32) (ldsb); element k of a row is scaled
+ * by 2^(e - 127) of its block k / 32 (e = 255: NaN), then the sum runs as in
+ * hg_gemm_fast and C = bf16_rne(acc * (scale_a * scale_b)).  Pinned: unit
+ * scales equal hg_gemm_ex; scales constant along each row equal
+ * hg_gemm_ex's row / column vectors; per-block scales on exact sums against
+ * fp64; NaN scales (tests/test_oracle.py). */
+void hg_gemm_mx(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
+                int N, int K, int lda, int ldb, int ldc, int a_fmt, int b_fmt,
+                const uint8_t *sa, int ldsa, const uint8_t *sb, int ldsb,
+                float scale_a, float scale_b);
+
 /* Threads OpenMP will use (for reporting cpu_baseline.cores). */
 int hg_num_threads(void);
 

@@ -83,6 +83,9 @@ class Oracle:
         L.hg_gemm_ex.argtypes = [_vp, _vp, _vp] + [ctypes.c_int] * 10 + \
             [ctypes.c_float] * 2 + [_vp, _vp, _vp]
         L.hg_gemm_ex.restype = None
+        L.hg_gemm_mx.argtypes = [_vp, _vp, _vp] + [ctypes.c_int] * 8 + \
+            [_vp, ctypes.c_int, _vp, ctypes.c_int] + [ctypes.c_float] * 2
+        L.hg_gemm_mx.restype = None
         L.hg_gemm_rows.argtypes = [_vp, _vp, _vp, _vp] + [ctypes.c_int] * 5 + \
             [ctypes.c_float] * 2
         L.hg_gemm_rows.restype = None
@@ -220,6 +223,25 @@ class Oracle:
                             None if sr is None else _ptr(sr),
                             None if sc is None else _ptr(sc),
                             None if bb is None else _ptr(bb))
+        return C
+
+    def gemm_mx(self, A: np.ndarray, B: np.ndarray, sa: np.ndarray,
+                sb: np.ndarray, a_fmt: int = FMT_E4M3, b_fmt: int = FMT_E4M3,
+                scale_a: float = 1.0, scale_b: float = 1.0) -> np.ndarray:
+        """bf16 bits of the MX-scaled product (oracle.h: hg_gemm_mx); sa: M x
+        ceil(K/32) E8M0 bytes, sb: N x ceil(K/32)."""
+        A = np.ascontiguousarray(A)
+        B = np.ascontiguousarray(B)
+        M, K = A.shape
+        N = B.shape[0]
+        kb = (K + 31) // 32
+        sa = np.ascontiguousarray(sa, np.uint8)
+        sb = np.ascontiguousarray(sb, np.uint8)
+        assert B.shape[1] == K and sa.shape == (M, kb) and sb.shape == (N, kb)
+        C = np.empty((M, N), np.uint16)
+        self.lib.hg_gemm_mx(_ptr(A), _ptr(B), _ptr(C), M, N, K, K, K, N,
+                            a_fmt, b_fmt, _ptr(sa), kb, _ptr(sb), kb,
+                            scale_a, scale_b)
         return C
 
     def gemm_rows(self, A: np.ndarray, B: np.ndarray, rows: Sequence[int],

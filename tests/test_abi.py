@@ -154,6 +154,31 @@ def test_gemm_desc_entry_validation():
         assert hg.gemm_desc_raw(hg.GemmDesc(**dict(base, **bad))) == INVALID, bad
 
 
+def test_mx_entry_validation():
+    """MX block scales: packed size, packing arguments, and the descriptor
+    rules (both scales, K % 32, 16-byte alignment, no extended epilogue,
+    the 4-wave 16x16x128 schedule or AUTO) -- all before any HIP call."""
+    assert hg.mx_scales_bytes(0, 256) == 0 and hg.mx_scales_bytes(100, 0) == 0
+    # ceil(rows/128) groups x ceil(ceil(K/128)/2) step pairs x 1 KiB
+    assert hg.mx_scales_bytes(128, 256) == 1024
+    assert hg.mx_scales_bytes(129, 384) == 2 * 2 * 1024
+    assert hg.mx_scales_bytes(8192, 8192) == 64 * 32 * 1024 == 8192 * 8192 // 32
+    L = hg.lib()
+    assert L.hipgemm_mx_pack_scales(FAKE, 64, 48, 2, FAKE, None) == INVALID   # K % 32
+    assert L.hipgemm_mx_pack_scales(FAKE, 64, 64, 1, FAKE, None) == INVALID   # ld < K/32
+    assert L.hipgemm_mx_pack_scales(None, 64, 64, 2, FAKE, None) == INVALID
+    assert L.hipgemm_mx_pack_scales(None, 0, 64, 2, None, None) == 0          # empty
+    base = dict(A=FAKE, B_T=FAKE, C=FAKE, M=300, N=300, K=64, lda=64, ldb=64,
+                ldc=300, mx_scale_a=FAKE, mx_scale_b=FAKE)
+    assert hg.gemm_desc_raw(hg.GemmDesc(**dict(base, M=0))) == 0
+    for bad in (dict(mx_scale_b=0), dict(mx_scale_a=0, mx_scale_b=FAKE),
+                dict(K=48, lda=48, ldb=48), dict(mx_scale_a=FAKE + 8),
+                dict(bias=FAKE), dict(scale_rows=FAKE), dict(out_dtype=1),
+                dict(activation=1), dict(variant=1), dict(variant=3),
+                dict(variant=4)):
+        assert hg.gemm_desc_raw(hg.GemmDesc(**dict(base, **bad))) == INVALID, bad
+
+
 def test_dropin_entry_validates_too():
     L = hg.lib()
     assert L.hipgemm_fp8_gemm_4wave_256x256x128(None, None, None, 64, 64, 64,

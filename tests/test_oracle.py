@@ -434,3 +434,43 @@ def test_gemm_ex_f16_output(oracle):
     got = oracle.gemm_ex(A, B, scale_a=3.0, out=po.OUT_F16)
     with np.errstate(over="ignore"):
         assert np.array_equal(got, _f16_bits(acc * np.float32(3.0)))
+
+
+# ---- MX block scales -------------------------------------------------------
+
+def test_gemm_mx_pinned(oracle):
+    """Unit scales: hg_gemm_ex.  Scales constant along each row: the row /
+    column vectors of hg_gemm_ex with 2^(e-127), bit for bit (powers of two
+    commute with fp32 rounding).  Per-block scales on ternary sums: fp64.
+    A scale of 255 is NaN for every output it touches."""
+    M, N, K = 21, 35, 320
+    kb = K // 32
+    A, B = _inputs(oracle, M, N, K, 51)
+    one_a = np.full((M, kb), 127, np.uint8)
+    one_b = np.full((N, kb), 127, np.uint8)
+    assert np.array_equal(oracle.gemm_mx(A, B, one_a, one_b, scale_a=2.0),
+                          oracle.gemm_ex(A, B, scale_a=2.0))
+    rng = np.random.default_rng(51)
+    er = rng.integers(117, 138, M).astype(np.uint8)
+    ec = rng.integers(117, 138, N).astype(np.uint8)
+    got = oracle.gemm_mx(A, B, np.repeat(er[:, None], kb, 1),
+                         np.repeat(ec[:, None], kb, 1))
+    want = oracle.gemm_ex(A, B, scale_rows=np.exp2(er.astype(np.float64) - 127).astype(np.float32),
+                          scale_cols=np.exp2(ec.astype(np.float64) - 127).astype(np.float32))
+    assert np.array_equal(got, want)
+    # per-block, exact sums
+    T = np.array([0xB8, 0x00, 0x38], np.uint8)
+    A = T[rng.integers(0, 3, (M, K))]
+    B = T[rng.integers(0, 3, (N, K))]
+    sa = rng.integers(120, 135, (M, kb)).astype(np.uint8)
+    sb = rng.integers(120, 135, (N, kb)).astype(np.uint8)
+    af = oracle.e4m3_to_f32(A).astype(np.float64) * np.repeat(np.exp2(sa - 127.0), 32, 1)
+    bf = oracle.e4m3_to_f32(B).astype(np.float64) * np.repeat(np.exp2(sb - 127.0), 32, 1)
+    want = oracle.f32_to_bf16((af @ bf.T).astype(np.float32))
+    assert np.array_equal(oracle.gemm_mx(A, B, sa, sb), want)
+    # a swapped block index (scales of block b applied to block b+1) fails
+    assert not np.array_equal(oracle.gemm_mx(A, B, np.roll(sa, 1, 1), sb), want)
+    sa2 = sa.copy()
+    sa2[3, 2] = 255
+    nan = (oracle.gemm_mx(A, B, sa2, sb) & 0x7FFF) > 0x7F80
+    assert nan[3].all() and not nan[np.arange(M) != 3].any()
