@@ -27,7 +27,7 @@ from typing import Optional
 
 __all__ = [
     "HipGemmError", "lib", "lib_path", "fp8_gemm_bf16", "fp8_gemm",
-    "fp8_gemm_4wave_256x256x128", "gemm_raw", "select_variant",
+    "fp8_gemm_4wave_256x256x128", "gemm_raw", "select_variant", "split_columns",
     "variant_name", "version", "tile_order", "lds_slot", "VARIANTS",
     "declared_symbols", "gemm_raw_ws", "workspace_size",
     "fp8_gemm_bf16_rowcol", "gemm_raw_rowcol", "GemmDesc", "gemm_desc_raw",
@@ -40,7 +40,8 @@ _ROOT = os.path.dirname(_HERE)
 _LIB_PATH = os.path.join(_HERE, "libhipgemm.so")
 _HEADER = os.path.join(_ROOT, "include", "hipgemm.h")
 
-VARIANTS = {"auto": 0, "4wave": 1, "4wave_mfma16": 2, "skinny": 3, "8wave": 4}
+VARIANTS = {"auto": 0, "4wave": 1, "4wave_mfma16": 2, "skinny": 3, "8wave": 4,
+            "tile128": 5}
 
 # include/hipgemm.h codes
 FMT_E4M3, FMT_E5M2 = 0, 1
@@ -134,6 +135,8 @@ def lib() -> ctypes.CDLL:
     L.hipgemm_fp8_gemm_4wave_256x256x128.restype = ci
     L.hipgemm_select_variant.argtypes = [ci, ci, ci]
     L.hipgemm_select_variant.restype = ci
+    L.hipgemm_split_columns.argtypes = [ci, ci, ci]
+    L.hipgemm_split_columns.restype = ci
     L.hipgemm_variant_name.argtypes = [ci]
     L.hipgemm_variant_name.restype = ctypes.c_char_p
     L.hipgemm_version.argtypes = []
@@ -230,6 +233,12 @@ def workspace_size(M: int, N: int, K: int, variant: int = 0) -> int:
 
 def select_variant(M: int, N: int, K: int) -> int:
     return int(lib().hipgemm_select_variant(M, N, K))
+
+
+def split_columns(M: int, N: int, K: int) -> int:
+    """Columns of C that AUTO runs on the 4-wave schedule when it splits C
+    between the 4-wave and 128 x 128 schedules; 0 when it does not."""
+    return int(lib().hipgemm_split_columns(M, N, K))
 
 
 def variant_name(v: int) -> Optional[str]:

@@ -79,7 +79,11 @@ int cu_count() {
 // 8-column groups that never straddle N and 16-byte aligned rows.
 hipError_t launch_tiled(int variant, GemmArgs g, hk::Key key,
                         hipStream_t stream) {
-  const int tiles = tiles_of(g.M, g.N);
+  const int bm = variant == HIPGEMM_VARIANT_TILE128 ? CfgT128::kBM : Cfg4w::kBM;
+  const int bn = variant == HIPGEMM_VARIANT_TILE128 ? CfgT128::kBN : Cfg4w::kBN;
+  const int tm = (g.M + bm - 1) / bm, tn = (g.N + bn - 1) / bn;
+  const int tiles = tm * tn;
+  g.group_m = default_group_m(tm, tn);
   const int cus = cu_count();
   const int grid = tiles < cus ? tiles : cus;
   g.workers = grid;
@@ -87,6 +91,10 @@ hipError_t launch_tiled(int variant, GemmArgs g, hk::Key key,
   const void* fn = nullptr;
   int threads = Cfg4w::kThreads;
   switch (variant) {
+    case HIPGEMM_VARIANT_TILE128:
+      fn = key.ext ? hk::tile128_ext(key) : hk::tile128_plain(key);
+      threads = CfgT128::kThreads;
+      break;
     case HIPGEMM_VARIANT_8WAVE:
       fn = !key.ext ? hk::eight_wave_plain(key)
            : key.out == HIPGEMM_OUT_F16 ? hk::eight_wave_ext_f16(key)
@@ -168,6 +176,30 @@ hipError_t launch_skinny(const GemmArgs& a, const SkinnyPlan& p, void* ws,
 
 int resolve_variant(int variant, int M, int N, int K);
 
+int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// AUTO's split of C's columns when the last round of 256 x 256 tiles would
+// leave most CUs idle (4000 x 5000: 320 tiles = 1.25 rounds): columns
+// [0, n1) on the 4-wave 16x16x128 schedule in whole rounds, the rest on the
+// 128 x 128 schedule (four times as many tiles).  Costs in rounds of the
+// 4-wave schedule over all CUs: a full round of the 128 x 128 schedule
+// measured 0.4-0.6 of one (it moves twice the L2 and LDS bytes per flop), so
+// 0.6 is charged.  Returns n1, or 0 for no split.
+int split_columns(int M, int N, int cus) {
+  const int tm = ceil_div(M, Cfg4w::kBM), tn = ceil_div(N, Cfg4w::kBN);
+  const int tiles = tm * tn;
+  if (M <= CfgSkinny::kMaxM || tiles < cus || tiles % cus == 0) return 0;
+  int c = (tiles / cus) * cus / tm;  // tile columns that fill whole rounds
+  if (c >= tn) c = tn - 1;
+  if (c <= 0) return 0;
+  const int n1 = c * Cfg4w::kBN;
+  const int rounds = ceil_div(tm * c, cus);
+  const int rest = ceil_div(M, CfgT128::kBM) * ceil_div(N - n1, CfgT128::kBN);
+  const double split = rounds + 0.6 * ceil_div(rest, cus);
+  const double plain = ceil_div(tiles, cus);
+  return split + 0.25 <= plain ? n1 : 0;
+}
+
 bool valid_code(int v, int count) { return v >= 0 && v < count; }
 
 // Shared body of the GEMM entry points.  `ws` may be null when `ws_given` is
@@ -207,6 +239,9 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
              (variant != HIPGEMM_VARIANT_AUTO &&
               variant != HIPGEMM_VARIANT_4WAVE_MFMA16)))
     return hipErrorInvalidValue;
+  const int n1 = (variant == HIPGEMM_VARIANT_AUTO && !mx && K > 0)
+                     ? split_columns(M, N, cu_count())
+                     : 0;
   variant = mx ? HIPGEMM_VARIANT_4WAVE_MFMA16 : resolve_variant(variant, M, N, K);
   if (K == 0) lda = ldb = 16;  // nothing is read; keep the offset math inert
   const int tiles_m = (M + Cfg4w::kBM - 1) / Cfg4w::kBM;
@@ -255,6 +290,20 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
       return e != hipSuccess ? e : f;
     }
     default:
+      if (n1 > 0) {
+        // Columns [0, n1) on the 4-wave schedule, [n1, N) on the 128 x 128
+        // one: B_T rows, C columns and the column vectors offset by n1.
+        GemmArgs g2 = g;
+        g.N = n1;
+        g2.N = N - n1;
+        g2.B += (size_t)n1 * ldb;
+        g2.C += n1;
+        if (g2.epi.col_scale) g2.epi.col_scale += n1;
+        if (g2.epi.bias) g2.epi.bias += n1;
+        e = launch_tiled(HIPGEMM_VARIANT_4WAVE_MFMA16, g, key, stream);
+        if (e != hipSuccess) return e;
+        return launch_tiled(HIPGEMM_VARIANT_TILE128, g2, key, stream);
+      }
       return launch_tiled(variant, g, key, stream);
   }
 }
@@ -293,9 +342,23 @@ int hipgemm_select_variant(int M, int N, int K) {
   // except for short K on few tiles (a fraction of one round over the CUs),
   // where the 8-wave one is 3-12 % ahead (2048^3, 512^3).  Measured on
   // MI355X, schedules compared in one process.
+  //
+  // When the 128 x 128 tiles fit in one round over the CUs (the 256 x 256
+  // ones then fill at most a quarter of them), the 128 x 128 schedule
+  // (2048^3: 1.69x the 8-wave one).  AUTO also splits C between the 4-wave
+  // and 128 x 128 schedules for a short last round (hipgemm_split_columns);
+  // this returns the 4-wave one then.
+  (void)K;
   if (M <= CfgSkinny::kMaxM) return HIPGEMM_VARIANT_SKINNY;
+  if (ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN) <= cu_count())
+    return HIPGEMM_VARIANT_TILE128;
   if (K <= 2048 && tiles_of(M, N) <= 128) return HIPGEMM_VARIANT_8WAVE;
   return HIPGEMM_VARIANT_4WAVE_MFMA16;
+}
+
+int hipgemm_split_columns(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return split_columns(M, N, cu_count());
 }
 
 hipError_t hipgemm_fp8_gemm_bf16(const void* A, const void* B_T, void* C,
@@ -387,6 +450,8 @@ const char* hipgemm_variant_name(int variant) {
       return "skinny_splitk_256";
     case HIPGEMM_VARIANT_8WAVE:
       return "8wave_256x256x128_mfma16";
+    case HIPGEMM_VARIANT_TILE128:
+      return "4wave_128x128x128_mfma16";
     default:
       return nullptr;
   }

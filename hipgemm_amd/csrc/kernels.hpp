@@ -9,6 +9,7 @@
 
 #include "hipgemm/detail/gemm_8wave.hpp"
 #include "hipgemm/detail/gemm_skinny.hpp"
+#include "hipgemm/detail/gemm_t128.hpp"
 
 namespace hipgemm {
 namespace kernels {
@@ -36,6 +37,8 @@ const void* skinny_plain(int kmb, const Key& k);    // kskinny_plain.hip
 const void* skinny_ext(int kmb, const Key& k);      // kskinny_ext.hip
 const void* skinny_reduce(const Key& k);            // kskinny_plain.hip
 const void* four_wave_mx(const Key& k);             // k4wave_mx.hip
+const void* tile128_plain(const Key& k);            // kt128_plain.hip
+const void* tile128_ext(const Key& k);              // kt128_ext.hip
 // Packs [rows][ceil(K/32)] E8M0 scales (row stride ld) into MxArgs' layout.
 hipError_t mx_pack(const uint8_t* src, int rows, int K, int ld, uint8_t* dst,
                    hipStream_t stream);

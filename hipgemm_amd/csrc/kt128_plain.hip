@@ -1,0 +1,28 @@
+// The 128 x 128-tile schedule with the per-tensor epilogue, for every
+// operand-format pair.
+#include "kernels.hpp"
+
+namespace hipgemm {
+namespace kernels {
+namespace {
+
+using namespace detail;
+
+template <bool kVec, int kFmt>
+__global__ __launch_bounds__(256, 1) void k_fp8_gemm_t128(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[CfgT128::kLdsBytes];
+  gemm_t128_body<kVec, false, kFmt>(g, (lds_u8*)lds);
+}
+
+}  // namespace
+
+const void* tile128_plain(const Key& k) {
+  return sel4(k.fmt, [&](auto F) {
+    return sel2(k.vec, [&](auto V) {
+      return (const void*)&k_fp8_gemm_t128<decltype(V)::value == 1, decltype(F)::value>;
+    });
+  });
+}
+
+}  // namespace kernels
+}  // namespace hipgemm

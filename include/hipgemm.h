@@ -52,7 +52,9 @@ enum {
    * persistent grid, v_mfma_f32_32x32x64_f8f6f4. */
   HIPGEMM_VARIANT_4WAVE = 1,
   /* The same schedule on v_mfma_f32_16x16x128_f8f6f4: AUTO's choice for
-   * M > 128 (but see 8WAVE), and the schedule behind the drop-in template. */
+   * M > 128 when the 256 x 256 tiles fill the CUs (but see 8WAVE, TILE128
+   * and hipgemm_split_columns), and the schedule behind the drop-in
+   * template. */
   HIPGEMM_VARIANT_4WAVE_MFMA16 = 2,
   /* M <= 128 only: split-K over every CU for the HBM-bound skinny shapes,
    * operands streamed straight into registers, a deterministic in-kernel
@@ -62,10 +64,18 @@ enum {
   /* 512 threads (8 waves, two per SIMD, in two groups that alternate
    * between LDS/DMA work and MFMAs), 256 x 256 tile, each wave 128 x 64 of
    * it, persistent grid, v_mfma_f32_16x16x128_f8f6f4.  AUTO's choice for
-   * M > 128 with K <= 2048 on at most 128 tiles of 256 x 256.  The
-   * reference's kernels are 4-wave only; no reference counterpart. */
+   * M > 128 with K <= 2048 on at most 128 tiles of 256 x 256 when the
+   * 128 x 128 tiles take more than one round.  The reference's kernels are
+   * 4-wave only; no reference counterpart. */
   HIPGEMM_VARIANT_8WAVE = 4,
-  HIPGEMM_VARIANT_COUNT = 5
+  /* 256 threads (4 waves, one per SIMD), 128 x 128 tile, each wave 64 x 64
+   * of it, 4 LDS stages, persistent grid, v_mfma_f32_16x16x128_f8f6f4: four
+   * times as many tiles as the 256 x 256 schedules, for shapes whose 256 x
+   * 256 tiles underfill the CUs: AUTO's choice for M > 128 when its tiles
+   * fit in one round over the CUs.  No reference counterpart (the reference
+   * has 256 x 256 tiles only). */
+  HIPGEMM_VARIANT_TILE128 = 5,
+  HIPGEMM_VARIANT_COUNT = 6
 };
 
 /* 8-bit operand formats (OCP 8-bit floating point, v1.0). */
@@ -236,6 +246,15 @@ hipError_t hipgemm_fp8_gemm_4wave_256x256x128(const void *A, const void *B_T,
 /* Variant AUTO resolves to for this shape (no GPU needed). No reference
  * counterpart (the reference has one schedule). */
 int hipgemm_select_variant(int M, int N, int K);
+
+/* AUTO's column split: when the last round of 256 x 256 tiles would leave
+ * most CUs idle, AUTO runs columns [0, n1) of C on the 4-wave 16x16x128
+ * schedule (whole rounds) and [n1, N) on the 128 x 128 schedule, two
+ * launches on the caller's stream.  Returns n1 (a multiple of 256), or 0
+ * when AUTO runs one schedule.  Uses the current device's CU count (256
+ * without a device).  No reference counterpart (the reference's grid is
+ * M*N/65536 tiles of 256 x 256, fp8_4wave.hpp:357-377). */
+int hipgemm_split_columns(int M, int N, int K);
 
 /* Human-readable variant name, or NULL.  No reference counterpart. */
 const char *hipgemm_variant_name(int variant);

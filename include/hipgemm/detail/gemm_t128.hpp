@@ -1,0 +1,351 @@
+// hipgemm -- 128 x 128-tile FP8 GEMM (gfx950), for grids the 256 x 256
+// tiles leave underfilled.
+//
+// C[M x N] = scale_a * scale_b * A[M x K] . B_T[N x K]^T, the same contract
+// and the same GemmArgs as the 4-wave schedule (gemm_4wave.hpp).  A 256 x 256
+// tile per workgroup leaves most CUs idle when M x N has few tiles (2048^3:
+// 64 tiles for 256 CUs) or a short last round (4000 x 5000: 320 tiles = 1.25
+// rounds); a 128 x 128 tile quarters the work per workgroup.  No reference
+// counterpart: fp8_4wave.hpp:334-567 has 256 x 256 tiles only.
+//
+// Work decomposition
+//   * One workgroup = 4 waves (one per SIMD), persistent over the tiles
+//     (tile_walk / grouped_tile, layout.hpp).  Wave w owns the 64 x 64
+//     quadrant (w / 2, w % 2) of a tile as 4 x 4 blocks of 16 x 16
+//     (v_mfma_f32_16x16x128_f8f6f4, 16 per 128-byte K-step, 64 AGPRs).
+//   * Per K-step a wave reads 4 A and 4 B fragments (8 KiB each) from LDS:
+//     the 64 x 64 wave tile reads as many LDS bytes per MFMA as the LDS can
+//     serve at the MFMA rate, so the fragments of step k + 1 are read while
+//     the MFMA of step k run (two register sets).
+//
+// Pipeline: kStages LDS stages of 128 A rows + 128 B rows x 128 bytes (32
+// KiB each), DMA'd (buffer_load_dwordx4 ... lds, 4 + 4 instructions per wave
+// per step) kStages - 1 steps ahead.  Iteration k: wait for the wave's own
+// DMA of step k + 1, barrier (every wave's part of step k + 1 landed, every
+// wave done with the stage of step k - 1), DMA of step k + kStages - 1 into
+// that stage, LDS reads of step k + 1, MFMA of step k.  The step sequence
+// runs on across tiles: the DMA and the reads past a tile's last step are
+// the next tile's first steps, so its epilogue overlaps the next tile's
+// loads.  Steps per tile are padded to an even count >= kStages (padding
+// steps read zeros).
+//
+// LDS layout: 128-byte rows with the slot_xor swizzle (layout.hpp).  A lane
+// reads K-chunks g and g + 4 of its row (g = lane / 16): the instruction's
+// own K order (lane group g holds K 16g .. 16g + 15 and 64 + 16g ..
+// 64 + 16g + 15), conflict-free (one chunk per 16-lane group).
+//
+// Epilogue: acc * scale (or the extended epilogue, kExt) -> bf16 / fp16,
+// staged through the wave's own 8 KiB of LDS (8-byte pieces, piece p of row r
+// in slot p ^ (r % 16): conflict-free writes and reads), then 16-byte stores
+// of whole 128-byte row segments; 2-byte stores straight from registers when
+// N, ldc or C's alignment do not allow 16 (kVec false).  Lanes outside M x N
+// get out-of-range offsets.  kExt: each wave DMAs its 64 row scales, 64
+// column scales and 64 biases into the first 1.5 KiB of its staging area at
+// the tile's first step; the K loop's own waits retire them.
+#pragma once
+
+#include <type_traits>
+
+#include "arch.hpp"
+#include "epilogue.hpp"
+#include "gemm_4wave.hpp"
+#include "layout.hpp"
+
+namespace hipgemm {
+namespace detail {
+
+struct CfgT128 {
+  static constexpr int kThreads = 256;
+  static constexpr int kBM = 128, kBN = 128, kBK = 128;
+  static constexpr int kStages = 4;
+  static constexpr int kAStage = kBM * kBK;            // 16 KiB
+  static constexpr int kStage = kAStage + kBN * kBK;   // 32 KiB
+  static constexpr int kStoreStage = 64 * 128;         // 8 KiB per wave
+  static constexpr int kStoreBase = kStages * kStage;  // 128 KiB
+  static constexpr int kLdsBytes = kStoreBase + 4 * kStoreStage;  // 160 KiB
+  static constexpr int kDmaPerStep = 8;  // per wave: 4 for A, 4 for B
+  static constexpr int kStores = 8;      // per wave per tile, 16-byte path
+};
+
+template <bool kVec, bool kExt = false, int kFmt = 0, int kAct = kActNone,
+          int kOut = kOutBf16>
+__device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
+  using Cfg = CfgT128;
+  constexpr int S = Cfg::kStages;
+  constexpr int kD = Cfg::kDmaPerStep;
+  constexpr int kScaleDma = kExt ? 3 : 0;
+  static_assert(S >= 3, "pipeline depth");
+  static_assert((S - 3) * kD + Cfg::kStores + kScaleDma + kD < 64, "vmcnt range");
+  const int lane = lane_id();
+  const int wave = wave_id();
+  const int wm = wave >> 1, wn = wave & 1;
+  const int M = g.M, N = g.N, K = g.K;
+  const int tiles_m = (M + Cfg::kBM - 1) / Cfg::kBM;
+  const int tiles_n = (N + Cfg::kBN - 1) / Cfg::kBN;
+  const int tiles = tiles_m * tiles_n;
+  const int steps = (K + Cfg::kBK - 1) / Cfg::kBK;
+  const int steps_pad = max(S, (steps + 1) & ~1);
+  const int workers = g.workers > 0 ? min((int)gridDim.x, g.workers)
+                                    : (int)gridDim.x;
+  if ((int)blockIdx.x >= workers) return;
+  const TileWalk walk = tile_walk(blockIdx.x, workers, tiles);
+  int t = walk.first;
+  if (t >= walk.end) return;
+
+  const float sa = g.scale_a ? *g.scale_a : 1.0f;
+  const float sb = g.scale_b ? *g.scale_b : 1.0f;
+  const float scale = sa * sb;
+
+  // ---- DMA lane geometry: instruction q (0..3) of wave w covers rows
+  // (4q + w) * 8 .. + 8 of A (or B); lane l takes row + l / 8, 16-byte slot
+  // l % 8, which holds global K-chunk (l % 8) ^ slot_xor(row). -------------
+  const int drow = lane >> 3;
+  const int dchunk = (lane & 7) ^ slot_xor(8 * (wave & 1) + drow);
+  uint32_t voff_a[4], voff_b[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int row = (4 * q + wave) * 8 + drow;
+    voff_a[q] = (uint32_t)row * (uint32_t)g.lda + dchunk * 16;
+    voff_b[q] = (uint32_t)row * (uint32_t)g.ldb + dchunk * 16;
+  }
+
+  // Buffer resources of a tile's A rows and B rows (rows past M / N read
+  // zero); a tile index past the walk's end gets empty ranges.
+  struct Src {
+    __amdgpu_buffer_rsrc_t a, b;
+  };
+  auto src_of = [&](int tile) {
+    if (tile >= walk.end) return Src{make_rsrc(g.A, 0u), make_rsrc(g.B, 0u)};
+    const TileCoord c = grouped_tile(tile, tiles_m, tiles_n, g.group_m);
+    const int ra = min(Cfg::kBM, M - c.m * Cfg::kBM);
+    const int rb = min(Cfg::kBN, N - c.n * Cfg::kBN);
+    return Src{make_rsrc(g.A + (size_t)c.m * Cfg::kBM * g.lda,
+                         (uint32_t)ra * (uint32_t)g.lda),
+               make_rsrc(g.B + (size_t)c.n * Cfg::kBN * g.ldb,
+                         (uint32_t)rb * (uint32_t)g.ldb)};
+  };
+  Src cur = src_of(t);
+  Src nxt = src_of(t + walk.stride);
+
+  // DMA of tile-local step d (d >= steps_pad: step d - steps_pad of the next
+  // tile) into `stage`, instruction n (0-3: A rows, 4-7: B rows).  K-chunks
+  // past K read zero.
+  auto dma_one = [&](int d, int stage, int n) {
+    const bool next = d >= steps_pad;
+    uint32_t k0 = (uint32_t)(next ? d - steps_pad : d) * Cfg::kBK;
+    asm volatile("" : "+s"(k0));
+    const bool ok = (int)(k0 + dchunk * 16) < K;
+    const Src& s = next ? nxt : cur;
+    lds_u8* base = lds + stage * Cfg::kStage;
+    const int q = n & 3;
+    if (n < 4)
+      dma16(s.a, base + (4 * q + wave) * 1024, ok ? voff_a[q] : kOobOffset, k0);
+    else
+      dma16(s.b, base + Cfg::kAStage + (4 * q + wave) * 1024,
+            ok ? voff_b[q] : kOobOffset, k0);
+  };
+  auto dma_step = [&](int d, int stage) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n) dma_one(d, stage, n);
+  };
+
+  // ---- fragment reads: A rows 64 wm + 16 i + l % 16, B rows
+  // 64 wn + 16 j + l % 16; K-chunks g and g + 4 (g = l / 16). -------------
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int rslot = grp ^ slot_xor(r16);
+  const uint32_t off_a = (uint32_t)((wm * 64 + r16) * Cfg::kBK + rslot * 16);
+  const uint32_t off_b =
+      (uint32_t)(Cfg::kAStage + (wn * 64 + r16) * Cfg::kBK + rslot * 16);
+  i32x8 fa[2][4], fb[2][4];
+  auto read_step = [&](int stage, int set) {
+    const lds_u8* base = lds + stage * Cfg::kStage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t o = off_a + i * 16 * Cfg::kBK;
+      fa[set][i] = join(lds_read16(base + o), lds_read16(base + (o ^ 64u)));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t o = off_b + j * 16 * Cfg::kBK;
+      fb[set][j] = join(lds_read16(base + o), lds_read16(base + (o ^ 64u)));
+    }
+  };
+
+  f32x4 acc[4][4];
+  // One step, in an explicit order (the scheduler otherwise put the reads
+  // after all the MFMA): MFMA n (block n / 4, n % 4) of register set `set`,
+  // each followed by one 16-byte read for the other set -- in the order the
+  // next step's MFMA use them: A0, B0..B3, A1..A3 -- and, after the first
+  // eight, one DMA each.
+  auto step = [&](int set, int rstage, int d, int dstage) {
+    const lds_u8* rb = lds + rstage * Cfg::kStage;
+    i32x4 rd[16];
+    sched_fence();
+#pragma unroll
+    for (int n = 0; n < 16; ++n) {
+      const int i = n / 4, j = n % 4;
+      acc[i][j] = mfma_16x16x128<fmt_b(kFmt), fmt_a(kFmt)>(fb[set][j], fa[set][i],
+                                                           acc[i][j]);
+      // read n: fragment f (0: A0, 1-4: B0-B3, 5-7: A1-A3), half n % 2
+      const int f = n / 2;
+      const uint32_t o = f == 0   ? off_a
+                         : f <= 4 ? off_b + (f - 1) * 16 * Cfg::kBK
+                                  : off_a + (f - 4) * 16 * Cfg::kBK;
+      rd[n] = lds_read16(rb + ((n & 1) ? (o ^ 64u) : o));
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (n < 8) {
+        dma_one(d, dstage, n);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      }
+      sched_fence();
+    }
+    const int o = set ^ 1;
+    fa[o][0] = join(rd[0], rd[1]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fb[o][j] = join(rd[2 + 2 * j], rd[3 + 2 * j]);
+#pragma unroll
+    for (int i = 1; i < 4; ++i) fa[o][i] = join(rd[8 + 2 * i], rd[9 + 2 * i]);
+  };
+
+  // kExt: the wave's 64 row scales, 64 column scales and 64 biases into its
+  // staging area (rows at +0, columns at +512, bias at +1024), one float per
+  // lane; zero past M / N.
+  lds_u8* stg = lds + Cfg::kStoreBase + wave * Cfg::kStoreStage;
+  auto scale_dma = [&](int tile) {
+    const TileCoord c = grouped_tile(tile, tiles_m, tiles_n, g.group_m);
+    const EpiArgs ea = kernel_epi();
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const __amdgpu_buffer_rsrc_t rr =
+        make_rsrc(ea.row_scale, ea.row_scale ? (uint32_t)M * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rc =
+        make_rsrc(ea.col_scale, ea.col_scale ? (uint32_t)N * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rb =
+        make_rsrc(ea.bias, ea.bias ? (uint32_t)N * 4u : 0u);
+    const uint32_t ro = (uint32_t)(c.m * Cfg::kBM + wm * 64 + ln) * 4u;
+    const uint32_t co = (uint32_t)(c.n * Cfg::kBN + wn * 64 + ln) * 4u;
+    dma4(rr, stg, ro);
+    dma4(rc, stg + 512, co);
+    dma4(rb, stg + 1024, co);
+  };
+
+  // Prologue of the first tile: steps 0 .. S - 2, then the reads of step 0.
+#pragma unroll
+  for (int d = 0; d < S - 1; ++d) dma_step(d, d);
+  wait_vmcnt<(S - 2) * kD>();
+  barrier();
+  read_step(0, 0);
+
+  int base = 0;          // stage of the tile's step 0
+  bool stores = false;   // the previous tile's C stores are in flight
+  for (;;) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{};
+
+    // Two steps per trip (register set 0, then 1); steps_pad is even.
+    for (int k = 0; k < steps_pad; k += 2) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int kk = k + h;
+        // Step kk + 1 landed: newer than it are steps kk + 2 .. kk + S - 2,
+        // and, during the first S - 2 steps of a tile after the first, the
+        // previous tile's stores (issued after this tile's first S - 1
+        // steps' DMA); kExt's three scale loads only make this wait longer.
+        if (stores && kk < S - 2)
+          wait_vmcnt<(S - 3) * kD + Cfg::kStores>();
+        else
+          wait_vmcnt<(S - 3) * kD>();
+        barrier();
+        if constexpr (kExt)
+          if (kk == 0) scale_dma(t);
+        // The reads past the last step are the next tile's step 0, whose
+        // stage is (base + steps_pad) % S.
+        step(h, (base + kk + 1) % S, kk + S - 1, (base + kk + S - 1) % S);
+      }
+    }
+
+    // ---- epilogue ---------------------------------------------------------
+    const TileCoord tc = grouped_tile(t, tiles_m, tiles_n, g.group_m);
+    const int rows_left = M - tc.m * Cfg::kBM - wm * 64;  // from wave row 0
+    const int cols_left = N - tc.n * Cfg::kBN - wn * 64;  // from wave col 0
+    auto oob_unless = [](int x, int limit) -> uint32_t {
+      return (uint32_t)((limit - 1 - x) >> 31) & kOobOffset;
+    };
+    int elane = lane;
+    asm volatile("" : "+v"(elane));
+    const int er16 = elane & 15, egrp = elane >> 4;
+    EpiVec<4, 4> ev;
+    if constexpr (kExt) ev.read_lds(stg, kernel_epi(), scale, elane);
+    auto pack = [&](const f32x4& a, int i, int j) -> u32x2 {
+      if constexpr (kExt)
+        return ev.template pack4<kAct, kOut>(a[0], a[1], a[2], a[3], i, j);
+      else
+        return u32x2{pack_bf16x2(a[0] * scale, a[1] * scale),
+                     pack_bf16x2(a[2] * scale, a[3] * scale)};
+    };
+    // C window of this wave: rows tc.m*128 + 64 wm .., columns tc.n*128 +
+    // 64 wn ..; the range ends at its last valid element.
+    const int wrows = min(64, rows_left), wcols = min(64, cols_left);
+    uint16_t* cw = g.C + (size_t)(tc.m * Cfg::kBM + wm * 64) * g.ldc +
+                   tc.n * Cfg::kBN + wn * 64;
+    const bool any = wrows > 0 && wcols > 0;
+    const __amdgpu_buffer_rsrc_t rsrc_c = make_rsrc(
+        cw, any ? (uint32_t)(((wrows - 1) * g.ldc + wcols) * 2) : 0u);
+    if constexpr (kVec) {
+      // Stage: 8-byte piece p (columns 4p .. 4p + 3) of row r at slot
+      // p ^ (r % 16) of the row's 128 bytes.
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 16 * i + er16, p = 4 * j + egrp;
+          lds_write8(stg + r * 128 + ((p ^ (r & 15)) * 8), pack(acc[i][j], i, j));
+        }
+      // Read back: store q covers rows 8q + l / 8, 16-byte chunk l % 8
+      // (pieces 2c, 2c + 1: one 16-byte unit, halves swapped on odd rows).
+      const int c = elane & 7, rsub = elane >> 3;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int r = 8 * q + rsub;
+        const int u = ((2 * c) ^ (r & 15)) >> 1;
+        i32x4 v = lds_read16(stg + r * 128 + u * 16);
+        if (r & 1) v = i32x4{v[2], v[3], v[0], v[1]};
+        const uint32_t off = (uint32_t)((r * g.ldc + 8 * c) * 2) |
+                             oob_unless(r, rows_left) | oob_unless(8 * c, cols_left);
+        __builtin_amdgcn_raw_buffer_store_b128(v, rsrc_c, off, 0, kStoreC);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const u32x2 pk = pack(acc[i][j], i, j);
+          const int r = 16 * i + er16, col = 16 * j + 4 * egrp;
+          const uint32_t rb = (uint32_t)((r * g.ldc + col) * 2) | oob_unless(r, rows_left);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t w = (e < 2 ? pk.x : pk.y) >> (16 * (e & 1));
+            __builtin_amdgcn_raw_buffer_store_b16(
+                (unsigned short)w, rsrc_c,
+                (rb | oob_unless(col + e, cols_left)) + 2 * e, 0, kStoreC);
+          }
+        }
+    }
+
+    t += walk.stride;
+    if (t >= walk.end) break;
+    base += steps_pad;
+    base %= S;
+    cur = nxt;
+    nxt = src_of(t + walk.stride);
+    stores = kVec;
+  }
+  // The last tile's look-ahead DMA (empty ranges) still count in vmcnt.
+  wait_vmcnt<0>();
+}
+
+}  // namespace detail
+}  // namespace hipgemm

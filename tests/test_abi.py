@@ -35,12 +35,27 @@ def test_version_and_variants():
     assert hg.variant_name(2).startswith("4wave")
     assert hg.variant_name(3).startswith("skinny")
     assert hg.variant_name(4).startswith("8wave")
-    assert hg.variant_name(5) is None
+    assert hg.variant_name(5).startswith("4wave_128x128")
+    assert hg.variant_name(6) is None
     assert hg.select_variant(8192, 8192, 8192) == 2
     assert hg.select_variant(4000, 5000, 3584) == 2
-    assert hg.select_variant(2048, 2048, 2048) == 4
-    assert hg.select_variant(512, 512, 512) == 4
+    # 128 x 128 tiles in one round over the (256, without a device) CUs
+    assert hg.select_variant(2048, 2048, 2048) == 5
+    assert hg.select_variant(512, 512, 512) == 5
+    assert hg.select_variant(2048, 4096, 2048) == 4
     assert hg.select_variant(128, 8192, 8192) == 3
+    assert hg.select_variant(129, 8192, 8192) == 5   # 2 x 64 tiles of 128
+
+
+def test_split_columns_plan():
+    """AUTO's column split (256 CUs without a device): 4000 x 5000 has 16 x
+    20 tiles of 256 = 1.25 rounds; 16 tile columns fill one round, the other
+    904 columns are 32 x 8 = 256 tiles of 128, one round."""
+    assert hg.split_columns(4000, 5000, 3584) == 4096
+    for shape in [(8192, 8192, 8192), (4096, 4096, 4096), (2048, 2048, 2048),
+                  (8192, 28672, 8192), (128, 8192, 8192), (6144, 6144, 4096),
+                  (4000, 5000, 0)]:
+        assert hg.split_columns(*shape) == 0, shape
 
 
 @pytest.mark.parametrize("args", [
@@ -119,7 +134,7 @@ def test_rowcol_entry_validation():
                                   p["rows"], p["cols"], p["variant"], 0, 0, 0)
 
     for bad in (dict(rows=FAKE + 2), dict(cols=FAKE + 1),
-                dict(variant=hg.VARIANTS["4wave"]), dict(variant=5),
+                dict(variant=hg.VARIANTS["4wave"]), dict(variant=6),
                 dict(K=40, lda=48, ldb=48), dict(ldc=299), dict(A=0),
                 dict(variant=hg.VARIANTS["skinny"])):  # M = 300 > 128
         assert call(**bad) == INVALID, bad

@@ -24,7 +24,7 @@ TERN = {po.FMT_E4M3: np.array([0xB8, 0x00, 0x38], np.uint8),   # -1, 0, +1
         po.FMT_E5M2: np.array([0xBC, 0x00, 0x3C], np.uint8)}
 FMTS = [(0, 0), (1, 0), (0, 1), (1, 1)]
 TILED = [pytest.param(0, id="auto"), pytest.param(2, id="mfma16"),
-         pytest.param(4, id="8wave")]
+         pytest.param(4, id="8wave"), pytest.param(5, id="tile128")]
 ALL = TILED + [pytest.param(3, id="skinny")]
 
 
@@ -162,12 +162,34 @@ def test_epilogue_transcendental(gpu, oracle, variant, act):
         assert rel <= REL_TOL
 
 
+def test_auto_split_epilogue(gpu, oracle):
+    """AUTO's column split with every column-indexed option: the column
+    scales and the bias of the 128 x 128 half are offset by the split
+    column.  Ternary e4m3 x e5m2, power-of-two scales, relu, fp16: bit-exact
+    against the oracle, canaries around C."""
+    M, N, K = 4000, 5000, 3584
+    n1 = hg.split_columns(M, N, K)
+    say(f"case [auto] split-epilogue M={M} N={N} K={K} n1={n1}")
+    rng = np.random.default_rng(85)
+    A, B = ternary(0, (M, K), 85), ternary(1, (N, K), 86)
+    sr = np.exp2(rng.integers(-3, 4, M)).astype(np.float32)
+    sc = np.exp2(rng.integers(-3, 4, N)).astype(np.float32)
+    bias = rng.uniform(-4, 4, N).astype(np.float32)
+    C, guard = run(gpu, A, B, fb=1, out=1, act=1, sa=[0.5], sr=sr, sc=sc,
+                   bias=bias, variant=0)
+    assert guard
+    want = oracle.gemm_ex(A, B, b_fmt=1, out=1, act=1, scale_a=0.5,
+                          scale_rows=sr, scale_cols=sc, bias=bias)
+    assert np.array_equal(C, want), f"{int((C != want).sum())} differ"
+
+
 def test_defaults_equal_plain_entry(gpu, oracle):
     """A default descriptor is hipgemm_fp8_gemm_bf16, bit for bit, on every
     schedule (general inputs: the same kernel and accumulation order)."""
     torch = gpu
     for variant, (M, N, K) in [(0, (700, 900, 1040)), (1, (512, 768, 512)),
-                               (3, (64, 2048, 2048)), (4, (512, 512, 512))]:
+                               (3, (64, 2048, 2048)), (4, (512, 512, 512)),
+                               (5, (600, 520, 784))]:
         say(f"case [v{variant}] desc-defaults M={M} N={N} K={K}")
         A = general(oracle, 0, (M, K), 80)
         B = general(oracle, 0, (N, K), 81)

@@ -28,7 +28,7 @@ CANARY = 0x7FA5  # a NaN bit pattern no epilogue produces
 # The tiled schedules of include/hipgemm.h: the 4-wave one on both MFMA
 # shapes, and the 8-wave one.
 SCHEDULES = [pytest.param(1, id="mfma32"), pytest.param(2, id="mfma16"),
-             pytest.param(4, id="8wave")]
+             pytest.param(4, id="8wave"), pytest.param(5, id="tile128")]
 
 
 @pytest.fixture(params=SCHEDULES)
@@ -156,6 +156,36 @@ def test_config5_skinny_and_ragged(gpu, oracle, M, N, K, variant):
     A, B = gen(oracle, M, N, K, 5, po.UNIFORM, -1.0, 1.0)
     C = run_gpu(gpu, A, B, variant=variant)
     check_full(oracle, C, A, B, None, None)
+
+
+def test_config5c_auto_split(gpu, oracle):
+    """AUTO on 4000 x 5000 x 3584 splits C: columns [0, n1) on the 4-wave
+    schedule (one full round of 256 x 256 tiles on a 256-CU device), the rest
+    on the 128 x 128 schedule.  Both halves against the oracle, general
+    inputs and (bit-exact) ternary ones, with canaries around C."""
+    torch = gpu
+    M, N, K = 4000, 5000, 3584
+    n1 = hg.split_columns(M, N, K)
+    say(f"case [auto] config5c-split M={M} N={N} K={K} n1={n1} seed=5")
+    assert n1 in (0, 4096)  # 0 only on a device with another CU count
+    A, B = gen(oracle, M, N, K, 5, po.UNIFORM, -1.0, 1.0)
+    C = run_gpu(torch, A, B, 1.25, 0.75, variant=0)
+    check_full(oracle, C, A, B, 1.25, 0.75)
+    A, B = gen_ternary(M, N, K, 55)
+    ldc = N + 24
+    buf = np.full((M + 4, ldc), CANARY, np.uint16)
+    dev = torch.from_numpy(buf.view(np.int16)).to("cuda")
+    a, b = to_dev(torch, A), to_dev(torch, B)
+    code = hg.gemm_raw(a.data_ptr(), b.data_ptr(), dev.data_ptr() + 2 * ldc * 2,
+                       M, N, K, K, K, ldc, 0, 0, 0,
+                       torch.cuda.current_stream().cuda_stream)
+    assert code == 0
+    torch.cuda.synchronize()
+    got = dev.cpu().numpy().view(np.uint16)
+    assert np.all(got[:2] == CANARY) and np.all(got[M + 2:] == CANARY)
+    assert np.all(got[2:M + 2, N:] == CANARY)
+    check_full(oracle, np.ascontiguousarray(got[2:M + 2, :N]), A, B, None, None,
+               exact=True)
 
 
 # ----------------------------------------------------------- edges ---------

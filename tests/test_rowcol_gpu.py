@@ -23,7 +23,8 @@ TERNARY = np.array([0xB8, 0x00, 0x38], np.uint8)  # -1, 0, +1
 
 # Every schedule the row/column entry point accepts (AUTO resolves per shape).
 VARIANTS = [pytest.param(0, id="auto"), pytest.param(2, id="mfma16"),
-            pytest.param(4, id="8wave"), pytest.param(3, id="skinny")]
+            pytest.param(4, id="8wave"), pytest.param(3, id="skinny"),
+            pytest.param(5, id="tile128")]
 
 
 def ternary(shape, seed):
