@@ -120,17 +120,19 @@ hipError_t launch_tiled(int variant, GemmArgs g, hk::Key key,
 }
 
 // Split-K plan of the skinny schedule: 16-row blocks of M, K-slices per
-// 256-column tile (enough workgroups to give every CU one), and the
-// workspace it needs (arrival counters, then the partial tiles).
+// column tile of CfgSkinny::bn(kmb) columns (enough workgroups to give every
+// CU one), and the workspace it needs (arrival counters, then the partial
+// tiles).
 struct SkinnyPlan {
-  int kmb, tiles_n, slices, slice_steps;
+  int kmb, bn, tiles_n, slices, slice_steps;
   size_t counter_bytes, ws_bytes;
 };
 
 SkinnyPlan plan_skinny(int M, int N, int K) {
   SkinnyPlan p{};
   p.kmb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
-  p.tiles_n = (N + CfgSkinny::kBN - 1) / CfgSkinny::kBN;
+  p.bn = CfgSkinny::bn(p.kmb);
+  p.tiles_n = (N + p.bn - 1) / p.bn;
   const int steps = (K + CfgSkinny::kBK - 1) / CfgSkinny::kBK;
   const int target = cu_count();
   int slices = (target + p.tiles_n - 1) / p.tiles_n;
@@ -141,7 +143,7 @@ SkinnyPlan plan_skinny(int M, int N, int K) {
   if (p.slices > 1) {
     p.counter_bytes = ((size_t)p.tiles_n * sizeof(int) + 255) / 256 * 256;
     p.ws_bytes = p.counter_bytes + (size_t)p.tiles_n * p.slices * p.kmb * 16 *
-                                       CfgSkinny::kBN * sizeof(float);
+                                       p.bn * sizeof(float);
   }
   return p;
 }
@@ -170,7 +172,8 @@ hipError_t launch_skinny(const GemmArgs& a, const SkinnyPlan& p, void* ws,
   if (e != hipSuccess || !reduce_pass) return e;
   int kmb = p.kmb;
   void* args[] = {&g, &kmb};
-  return hipLaunchKernel(hk::skinny_reduce(key), dim3(p.tiles_n * p.kmb),
+  return hipLaunchKernel(hk::skinny_reduce(CfgSkinny::frags(p.kmb), key),
+                         dim3(p.tiles_n * p.kmb),
                          dim3(CfgSkinny::kThreads), args, 0, stream);
 }
 

@@ -35,7 +35,7 @@ const void* eight_wave_ext_bf16(const Key& k);      // k8wave_ext_bf16.hip
 const void* eight_wave_ext_f16(const Key& k);       // k8wave_ext_f16.hip
 const void* skinny_plain(int kmb, const Key& k);    // kskinny_plain.hip
 const void* skinny_ext(int kmb, const Key& k);      // kskinny_ext.hip
-const void* skinny_reduce(const Key& k);            // kskinny_plain.hip
+const void* skinny_reduce(int kf, const Key& k);    // kskinny_plain.hip
 const void* four_wave_mx(const Key& k);             // k4wave_mx.hip
 const void* tile128_plain(const Key& k);            // kt128_plain.hip
 const void* tile128_ext(const Key& k);              // kt128_ext.hip

@@ -14,10 +14,10 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm_skinny(SkinnyArgs g) {
   gemm_skinny_body<kMB, kVec8, false, kFmt>(g);
 }
 
-template <bool kVec8, bool kExt>
+template <bool kVec8, bool kExt, int kF>
 __global__ __launch_bounds__(256, 1) void k_fp8_gemm_skinny_reduce(SkinnyArgs g,
                                                                     int kmb) {
-  gemm_skinny_reduce_body<kVec8, kExt>(g, kmb);
+  gemm_skinny_reduce_body<kVec8, kExt, kF>(g, kmb);
 }
 
 template <class F>
@@ -43,10 +43,16 @@ const void* skinny_plain(int kmb, const Key& k) {
   });
 }
 
-const void* skinny_reduce(const Key& k) {
+const void* skinny_reduce(int kf, const Key& k) {
   return sel2(k.ext, [&](auto E) {
     return sel2(k.vec, [&](auto V) {
-      return (const void*)&k_fp8_gemm_skinny_reduce<decltype(V)::value == 1, decltype(E)::value == 1>;
+      if (kf == 2)
+        return (const void*)&k_fp8_gemm_skinny_reduce<decltype(V)::value == 1,
+                                                      decltype(E)::value == 1, 2>;
+      if (kf == 4)
+        return (const void*)&k_fp8_gemm_skinny_reduce<decltype(V)::value == 1,
+                                                      decltype(E)::value == 1, 4>;
+      return (const void*)nullptr;
     });
   });
 }

@@ -6,11 +6,13 @@
 // (fp8_4wave.hpp:334-567) is only valid for M a multiple of 256.
 //
 // Decomposition: workgroup (n, s) of a (tiles_n x slices) grid computes the
-// fp32 partial C[0:M, 256n : 256n + 256] over K-slice s (`slice_steps` steps
-// of 128).  Slices make the grid fill the GPU although tiles_n is small.
-//   * Wave w owns columns 64w .. 64w + 63 of the tile as 4 x kMB blocks of
-//     16 x 16 (v_mfma_f32_16x16x128_f8f6f4, one per block per step).
-//   * Every wave streams its 64 B_T rows straight into registers with
+// fp32 partial C[0:M, BN n : BN n + BN] over K-slice s (`slice_steps` steps
+// of 128), BN = 64 kF columns (kF = 4 up to 32 rows, 2 above:
+// CfgSkinny::frags).  Slices make the grid fill the GPU although tiles_n is
+// small.
+//   * Wave w owns columns 16 kF w .. + 16 kF - 1 of the tile as kF x kMB
+//     blocks of 16 x 16 (v_mfma_f32_16x16x128_f8f6f4, one per block per step).
+//   * Every wave streams its 16 kF B_T rows straight into registers with
 //     buffer_load_dwordx4, three steps ahead; A (at most 128 rows) too for
 //     M <= 32, else the workgroup stages A once per step through LDS.  A lane holds, for its row, the K-bytes
 //     16g .. 16g + 15 and 64 + 16g .. 64 + 16g + 15 of each 128-byte step
@@ -55,21 +57,27 @@ struct SkinnyArgs {
 
 struct CfgSkinny {
   static constexpr int kThreads = 256;
-  static constexpr int kBN = 256, kBK = 128;
+  static constexpr int kBK = 128;
+  // B_T fragments (16 columns each) per wave, 4 waves per workgroup: 4 up to
+  // 32 rows; 2 above, which halves the workgroup's column tile and so the
+  // K-slices and the partial-tile traffic per output (128 x 8192 x 8192:
+  // 16 instead of 32 MiB written and read back).
+  static constexpr int frags(int kmb) { return kmb >= 4 ? 2 : 4; }
+  static constexpr int bn(int kmb) { return 4 * 16 * frags(kmb); }
   static constexpr int kMaxM = 128;
   // Floats of one slice's partial tile.
   template <int kMB>
-  static constexpr int partial_floats() { return kMB * 16 * kBN; }
+  static constexpr int partial_floats() { return kMB * 16 * bn(kMB); }
 };
 
 // Epilogue of the C elements one lane writes: rows 16 (m0 + m) + l % 16
-// (m < kRows) and columns col0 + 16 f + 4 (l / 16) + i (f, i < 4).  Plain:
+// (m < kRows) and columns col0 + 16 f + 4 (l / 16) + i (f < kF, i < 4).  Plain:
 // the product of the two per-tensor scalars; kExt: the extended epilogue of
 // epilogue.hpp from g.epi (vectors zero past M or N, never stored).
-template <int kRows, bool kExt>
+template <int kRows, bool kExt, int kF>
 struct SkinnyEpi {
   float s = 1.0f;
-  EpiVec<kExt ? kRows : 1, kExt ? 4 : 1> ev;
+  EpiVec<kExt ? kRows : 1, kExt ? kF : 1> ev;
   __device__ __forceinline__ void load(const SkinnyArgs& g, int m0, int col0,
                                        int lane) {
     const float sa = g.scale_a ? *g.scale_a : 1.0f;
@@ -92,6 +100,8 @@ struct SkinnyEpi {
 template <int kMB, bool kVec8, bool kExt = false, int kFmt = 0>
 __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   using Cfg = CfgSkinny;
+  constexpr int kF = Cfg::frags(kMB);  // B_T fragments per wave
+  constexpr int kBN = Cfg::bn(kMB);    // columns per workgroup
   // A (at most 128 rows) is shared by the four waves: up to 32 rows each
   // wave loads its own copy into registers; above, the workgroup stages it
   // through LDS once (DMA, one barrier per step) so A costs no more HBM or
@@ -100,14 +110,16 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   // Register sets / LDS stages: kDepth - 1 steps of loads stay in flight per
   // wave (the whole GPU's worth of in-flight loads is about half of a
   // 64 MiB B_T, so the look-ahead is as deep as the registers allow).
+  // (With A in LDS, 7 steps instead of 3 measured no faster at
+  // 128 x 8192 x 8192 and 24 % slower at 128 x 28672 x 8192.)
   constexpr int kDepth = kLdsA ? 4 : kMB <= 2 ? 4 : 3;
   constexpr int kDmaA = kLdsA ? kMB / 2 : 0;  // A DMA per wave per step
-  constexpr int kLoads = kLdsA ? 8 + kDmaA : 8 + 2 * kMB;  // per wave per step
+  constexpr int kLoads = 2 * kF + (kLdsA ? kDmaA : 2 * kMB);  // per wave per step
   static_assert((kDepth - 1) * kLoads < 64, "vmcnt range");
   const int lane = lane_id();
   const int wave = wave_id();
   const int M = g.M, N = g.N, K = g.K;
-  const int tiles_n = (N + Cfg::kBN - 1) / Cfg::kBN;
+  const int tiles_n = (N + kBN - 1) / kBN;
   const int nt = blockIdx.x % tiles_n;
   const int s = blockIdx.x / tiles_n;
   const int k_begin = s * g.slice_steps * Cfg::kBK;
@@ -115,19 +127,20 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   const int steps = (k_end - k_begin + Cfg::kBK - 1) / Cfg::kBK;
   const int steps_pad = (steps + kDepth - 1) / kDepth * kDepth;
 
-  const int n0 = nt * Cfg::kBN;
-  const int rows_b = min(Cfg::kBN, N - n0);
+  const int n0 = nt * kBN;
+  const int rows_b = min(kBN, N - n0);
   const __amdgpu_buffer_rsrc_t rsrc_a =
       make_rsrc(g.A, (uint32_t)M * (uint32_t)g.lda);
   const __amdgpu_buffer_rsrc_t rsrc_b =
       make_rsrc(g.B + (size_t)n0 * g.ldb, (uint32_t)rows_b * (uint32_t)g.ldb);
 
   const int r16 = lane & 15, grp = lane >> 4;
-  // Lane row offsets: B_T rows 64w + 16f + r16 (f = 0..3), A rows 16m + r16.
-  uint32_t voff_b[4], voff_a[kLdsA ? 1 : kMB];
+  // Lane row offsets: B_T rows 16 kF w + 16f + r16 (f < kF), A rows
+  // 16m + r16.
+  uint32_t voff_b[kF], voff_a[kLdsA ? 1 : kMB];
 #pragma unroll
-  for (int f = 0; f < 4; ++f)
-    voff_b[f] = (uint32_t)(wave * 64 + 16 * f + r16) * (uint32_t)g.ldb + 16 * grp;
+  for (int f = 0; f < kF; ++f)
+    voff_b[f] = (uint32_t)(wave * 16 * kF + 16 * f + r16) * (uint32_t)g.ldb + 16 * grp;
   if constexpr (!kLdsA) {
 #pragma unroll
     for (int m = 0; m < kMB; ++m)
@@ -152,7 +165,7 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   }
   const int sx16 = slot_xor(r16);
 
-  i32x4 bq[kDepth][4][2], aq[kLdsA ? 1 : kDepth][kMB][2];
+  i32x4 bq[kDepth][kF][2], aq[kLdsA ? 1 : kDepth][kMB][2];
   // Loads of step kb into register set / LDS stage d; pieces past the slice
   // end read 0.
   auto load_step = [&](int kb, int d) {
@@ -162,7 +175,7 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
     const uint32_t oob0 = (16 * grp < lim) ? 0u : kOobOffset;
     const uint32_t oob1 = (64 + 16 * grp < lim) ? 0u : kOobOffset;
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
+    for (int f = 0; f < kF; ++f) {
       bq[d][f][0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_b, voff_b[f] | oob0, k0, 0);
       bq[d][f][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_b, voff_b[f] | oob1, k0 + 64, 0);
     }
@@ -185,11 +198,11 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
     }
   };
 
-  f32x4 acc[kMB][4];
+  f32x4 acc[kMB][kF];
 #pragma unroll
   for (int m = 0; m < kMB; ++m)
 #pragma unroll
-    for (int f = 0; f < 4; ++f) acc[m][f] = f32x4{};
+    for (int f = 0; f < kF; ++f) acc[m][f] = f32x4{};
 
   auto mfma_step = [&](int d) {
 #pragma unroll
@@ -203,7 +216,7 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
         a = join(aq[d][m][0], aq[d][m][1]);
       }
 #pragma unroll
-      for (int f = 0; f < 4; ++f)
+      for (int f = 0; f < kF; ++f)
         acc[m][f] = mfma_16x16x128<fmt_b(kFmt), fmt_a(kFmt)>(
             join(bq[d][f][0], bq[d][f][1]), a, acc[m][f]);
     }
@@ -246,7 +259,7 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
       (uint32_t)(g.slices * tile_floats * sizeof(float)));
   // layout: float4 (m, f, wave, lane) at byte ((m*4 + f)*256 + 64 w + l)*16
   auto slot = [&](int m, int f) {
-    return (uint32_t)(((m * 4 + f) * Cfg::kThreads + wave * 64 + lane) * 16);
+    return (uint32_t)(((m * kF + f) * Cfg::kThreads + wave * 64 + lane) * 16);
   };
   const uint32_t mine = (uint32_t)(s * tile_floats * sizeof(float));
   __shared__ int last;
@@ -254,7 +267,7 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
 #pragma unroll
     for (int m = 0; m < kMB; ++m)
 #pragma unroll
-      for (int f = 0; f < 4; ++f) {
+      for (int f = 0; f < kF; ++f) {
         const f32x4 v{acc_read(acc[m][f][0]), acc_read(acc[m][f][1]),
                       acc_read(acc[m][f][2]), acc_read(acc[m][f][3])};
         __builtin_amdgcn_raw_buffer_store_b128(
@@ -273,8 +286,8 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   }
 
   // ---- last arrival: sum the slices in order, scale, bf16, store ----------
-  SkinnyEpi<kMB, kExt> scl;
-  scl.load(g, 0, n0 + wave * 64, lane);
+  SkinnyEpi<kMB, kExt, kF> scl;
+  scl.load(g, 0, n0 + wave * 16 * kF, lane);
   const __amdgpu_buffer_rsrc_t rsrc_c =
       make_rsrc(g.C + n0, (uint32_t)(((M - 1) * g.ldc + rows_b) * 2));
   auto oob_unless = [](int x, int limit) -> uint32_t {
@@ -283,11 +296,11 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   // Sums over the slices, in slice order; the loads of kBatch slices (all
   // kMB x 4 blocks each, 32 loads) are issued before any is consumed.
   constexpr int kBatch = 8 / kMB;
-  f32x4 sum[kMB][4];
+  f32x4 sum[kMB][kF];
 #pragma unroll
   for (int m = 0; m < kMB; ++m)
 #pragma unroll
-    for (int f = 0; f < 4; ++f)
+    for (int f = 0; f < kF; ++f)
       sum[m][f] = g.slices > 1
                       ? f32x4{}
                       : f32x4{acc_read(acc[m][f][0]), acc_read(acc[m][f][1]),
@@ -295,13 +308,13 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   if (g.slices > 1) {
     const uint32_t stride = (uint32_t)(tile_floats * sizeof(float));
     for (int q0 = 0; q0 < g.slices; q0 += kBatch) {
-      f32x4 v[kBatch][kMB][4];
+      f32x4 v[kBatch][kMB][kF];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u)
 #pragma unroll
         for (int m = 0; m < kMB; ++m)
 #pragma unroll
-          for (int f = 0; f < 4; ++f)
+          for (int f = 0; f < kF; ++f)
             v[u][m][f] = __builtin_bit_cast(
                 f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                            rsrc_p, slot(m, f),
@@ -317,18 +330,18 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
 #pragma unroll
         for (int m = 0; m < kMB; ++m)
 #pragma unroll
-          for (int f = 0; f < 4; ++f) sum[m][f] += live ? v[u][m][f] : f32x4{};
+          for (int f = 0; f < kF; ++f) sum[m][f] += live ? v[u][m][f] : f32x4{};
       }
     }
   }
 #pragma unroll
   for (int m = 0; m < kMB; ++m)
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
+    for (int f = 0; f < kF; ++f) {
       // D = B_blk . A_blk^T: lane l, element i -> C row 16m + l%16,
-      // column 64w + 16f + 4(l/16) + i (4 consecutive columns).
+      // column 16 kF w + 16f + 4(l/16) + i (4 consecutive columns).
       const int row = 16 * m + r16;
-      const int col = wave * 64 + 16 * f + 4 * grp;
+      const int col = wave * 16 * kF + 16 * f + 4 * grp;
       const uint32_t base = (uint32_t)((row * g.ldc + col) * 2) |
                             oob_unless(row, M);
       const u32x2 pk = scl.pack4(sum[m][f], m, f);
@@ -357,39 +370,40 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
 // the in-kernel reduction, spread over tiles_n x kMB workgroups instead of
 // one per tile.  Launched on the same stream right after the split kernel,
 // so its partial tiles are visible without any fence.
-template <bool kVec8, bool kExt = false>
+template <bool kVec8, bool kExt, int kF>
 __device__ __forceinline__ void gemm_skinny_reduce_body(const SkinnyArgs& g,
                                                         int kmb) {
   using Cfg = CfgSkinny;
+  constexpr int kBN = 4 * 16 * kF;
   const int lane = lane_id();
   const int wave = wave_id();
   const int M = g.M, N = g.N;
-  const int tiles_n = (N + Cfg::kBN - 1) / Cfg::kBN;
+  const int tiles_n = (N + kBN - 1) / kBN;
   const int nt = blockIdx.x % tiles_n;
   const int m = blockIdx.x / tiles_n;
-  const int n0 = nt * Cfg::kBN;
-  const int rows_b = min(Cfg::kBN, N - n0);
+  const int n0 = nt * kBN;
+  const int rows_b = min(kBN, N - n0);
   const int r16 = lane & 15, grp = lane >> 4;
-  const int tile_floats = kmb * 16 * Cfg::kBN;
+  const int tile_floats = kmb * 16 * kBN;
   const __amdgpu_buffer_rsrc_t rsrc_p = make_rsrc(
       g.partial + (size_t)nt * g.slices * tile_floats,
       (uint32_t)(g.slices * tile_floats * sizeof(float)));
   const uint32_t stride = (uint32_t)(tile_floats * sizeof(float));
   auto slot = [&](int f) {
-    return (uint32_t)(((m * 4 + f) * Cfg::kThreads + wave * 64 + lane) * 16);
+    return (uint32_t)(((m * kF + f) * Cfg::kThreads + wave * 64 + lane) * 16);
   };
   // Scales first: their latency hides under the slice loads (read after the
   // loop they cost this short kernel one more memory round trip).
-  SkinnyEpi<1, kExt> scl;
-  scl.load(g, m, n0 + wave * 64, lane);
+  SkinnyEpi<1, kExt, kF> scl;
+  scl.load(g, m, n0 + wave * 16 * kF, lane);
   constexpr int kBatch = 8;  // slices whose loads are in flight together
-  f32x4 sum[4] = {};
+  f32x4 sum[kF] = {};
   for (int q0 = 0; q0 < g.slices; q0 += kBatch) {
-    f32x4 v[kBatch][4];
+    f32x4 v[kBatch][kF];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
 #pragma unroll
-      for (int f = 0; f < 4; ++f)
+      for (int f = 0; f < kF; ++f)
         v[u][f] = __builtin_bit_cast(
             f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                        rsrc_p, slot(f),
@@ -399,7 +413,7 @@ __device__ __forceinline__ void gemm_skinny_reduce_body(const SkinnyArgs& g,
     for (int u = 0; u < kBatch; ++u) {
       const bool live = q0 + u < g.slices;
 #pragma unroll
-      for (int f = 0; f < 4; ++f) sum[f] += live ? v[u][f] : f32x4{};
+      for (int f = 0; f < kF; ++f) sum[f] += live ? v[u][f] : f32x4{};
     }
   }
   const __amdgpu_buffer_rsrc_t rsrc_c =
@@ -408,9 +422,9 @@ __device__ __forceinline__ void gemm_skinny_reduce_body(const SkinnyArgs& g,
     return (uint32_t)((limit - 1 - x) >> 31) & kOobOffset;
   };
 #pragma unroll
-  for (int f = 0; f < 4; ++f) {
+  for (int f = 0; f < kF; ++f) {
     const int row = 16 * m + r16;
-    const int col = wave * 64 + 16 * f + 4 * grp;
+    const int col = wave * 16 * kF + 16 * f + 4 * grp;
     const uint32_t base = (uint32_t)((row * g.ldc + col) * 2) | oob_unless(row, M);
     const u32x2 pk = scl.pack4(sum[f], 0, f);
     const uint32_t lo = pk.x, hi = pk.y;
