@@ -179,6 +179,61 @@ hipError_t launch_skinny(const GemmArgs& a, const SkinnyPlan& p, void* ws,
 
 int resolve_variant(int variant, int M, int N, int K);
 
+// K-split plan of the 128 x 128 schedule: when its tiles fill at most a
+// quarter of the CUs and K has at least 16 steps of 128, K-slices of at
+// least 8 (even) steps so that tiles x slices approaches the CU count; the
+// workspace holds one 64 KiB fp32 partial tile per (tile, slice).  Measured
+// against no split in one process: 256 x 4096 x 14336 (64 tiles, 4 slices)
+// 1.39x; at 128 tiles (2 slices) 3-8 % slower (256 x 8192 x 8192,
+// 512 x 4096 x 8192), so half-filled grids are not split.  Below 129 rows
+// the skinny schedule stays ahead (128 x 8192 x 8192: 555 against 466
+// TFLOP/s split 4 ways).
+struct T128Plan {
+  int slices = 1, slice_steps = 0;
+  size_t ws_bytes = 0;
+};
+
+T128Plan plan_t128(int M, int N, int K, int cus) {
+  T128Plan p;
+  const int tiles = ((M + CfgT128::kBM - 1) / CfgT128::kBM) *
+                    ((N + CfgT128::kBN - 1) / CfgT128::kBN);
+  const int steps = (K + CfgT128::kBK - 1) / CfgT128::kBK;
+  p.slice_steps = steps;
+  if (tiles <= 0 || 4 * tiles > cus || steps < 16) return p;
+  int sl = cus / tiles < steps / 8 ? cus / tiles : steps / 8;
+  if (sl < 2) return p;
+  int ss = (steps + sl - 1) / sl;
+  ss = (ss + 1) & ~1;
+  sl = (steps + ss - 1) / ss;
+  if (sl < 2) return p;
+  p.slices = sl;
+  p.slice_steps = ss;
+  p.ws_bytes = (size_t)tiles * sl * 65536;
+  return p;
+}
+
+hipError_t launch_t128_split(GemmArgs g, const T128Plan& p, void* ws,
+                             hk::Key key, hipStream_t stream) {
+  const int tm = (g.M + CfgT128::kBM - 1) / CfgT128::kBM;
+  const int tn = (g.N + CfgT128::kBN - 1) / CfgT128::kBN;
+  const int tiles = tm * tn, units = tiles * p.slices, cus = cu_count();
+  g.group_m = default_group_m(tm, tn);
+  g.workers = units < cus ? units : cus;
+  g.split.slices = p.slices;
+  g.split.slice_steps = p.slice_steps;
+  g.split.partial = static_cast<float*>(ws);
+  const void* fn = hk::tile128_split(key);
+  if (!fn) return hipErrorInvalidValue;
+  void* args[] = {&g};
+  hipError_t e = hipLaunchKernel(fn, dim3(g.workers), dim3(CfgT128::kThreads),
+                                 args, 0, stream);
+  if (e != hipSuccess) return e;
+  key.vec = (g.N % 4 == 0) && (g.ldc % 4 == 0) && aligned(g.C, 8);
+  fn = hk::tile128_reduce(key);
+  if (!fn) return hipErrorInvalidValue;
+  return hipLaunchKernel(fn, dim3(tiles * 4), dim3(64), args, 0, stream);
+}
+
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 // AUTO's split of C's columns when the last round of 256 x 256 tiles would
@@ -263,7 +318,8 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
              default_group_m(tiles_m, tiles_n),
              0,
              EpiArgs{},
-             MxArgs{}};
+             MxArgs{},
+             SplitArgs{}};
   g.epi.row_scale = d.scale_rows;
   g.epi.col_scale = d.scale_cols;
   g.epi.bias = d.bias;
@@ -276,21 +332,36 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   key.ext = ext;
   key.act = d.activation;
   key.out = d.out_dtype;
+  // A schedule that needs `need` bytes of workspace (the first `zero` of
+  // them zero-filled): the caller's, or a stream-ordered allocation for the
+  // call.
+  auto with_workspace = [&](size_t need, size_t zero, auto go) -> hipError_t {
+    if (need == 0) return go(nullptr);
+    if (ws_given) {
+      if (ws_bytes < need) return hipErrorInvalidValue;
+      return go(ws);
+    }
+    void* tmp = nullptr;
+    hipError_t r = hipMallocAsync(&tmp, need, stream);
+    if (r != hipSuccess) return r;
+    if (zero > 0) r = hipMemsetAsync(tmp, 0, zero, stream);
+    if (r == hipSuccess) r = go(tmp);
+    const hipError_t f = hipFreeAsync(tmp, stream);
+    return r != hipSuccess ? r : f;
+  };
   switch (variant) {
     case HIPGEMM_VARIANT_SKINNY: {
       const SkinnyPlan p = plan_skinny(M, N, K);
-      auto go = [&](void* w) { return launch_skinny(g, p, w, key, stream); };
-      if (p.ws_bytes == 0) return go(nullptr);
-      if (ws_given) {
-        if (ws_bytes < p.ws_bytes) return hipErrorInvalidValue;
-        return go(ws);
-      }
-      void* tmp = nullptr;
-      if ((e = hipMallocAsync(&tmp, p.ws_bytes, stream)) != hipSuccess) return e;
-      e = hipMemsetAsync(tmp, 0, p.counter_bytes, stream);
-      if (e == hipSuccess) e = go(tmp);
-      const hipError_t f = hipFreeAsync(tmp, stream);
-      return e != hipSuccess ? e : f;
+      return with_workspace(p.ws_bytes, p.counter_bytes, [&](void* w) {
+        return launch_skinny(g, p, w, key, stream);
+      });
+    }
+    case HIPGEMM_VARIANT_TILE128: {
+      const T128Plan p = plan_t128(M, N, K, cu_count());
+      if (p.slices == 1) return launch_tiled(variant, g, key, stream);
+      return with_workspace(p.ws_bytes, 0, [&](void* w) {
+        return launch_t128_split(g, p, w, key, stream);
+      });
     }
     default:
       if (n1 > 0) {
@@ -429,7 +500,9 @@ hipError_t hipgemm_mx_pack_scales(const void* src, int rows, int K, int ld,
 
 size_t hipgemm_workspace_size(int M, int N, int K, int variant) {
   if (M <= 0 || N <= 0 || K < 0) return 0;
-  if (resolve_variant(variant, M, N, K) != HIPGEMM_VARIANT_SKINNY) return 0;
+  const int v = resolve_variant(variant, M, N, K);
+  if (v == HIPGEMM_VARIANT_TILE128) return plan_t128(M, N, K, cu_count()).ws_bytes;
+  if (v != HIPGEMM_VARIANT_SKINNY) return 0;
   if (M > CfgSkinny::kMaxM) return 0;
   return plan_skinny(M, N, K).ws_bytes;
 }

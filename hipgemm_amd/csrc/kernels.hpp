@@ -39,6 +39,8 @@ const void* skinny_reduce(int kf, const Key& k);    // kskinny_plain.hip
 const void* four_wave_mx(const Key& k);             // k4wave_mx.hip
 const void* tile128_plain(const Key& k);            // kt128_plain.hip
 const void* tile128_ext(const Key& k);              // kt128_ext.hip
+const void* tile128_split(const Key& k);            // kt128_plain.hip
+const void* tile128_reduce(const Key& k);           // kt128_plain.hip
 // Packs [rows][ceil(K/32)] E8M0 scales (row stride ld) into MxArgs' layout.
 hipError_t mx_pack(const uint8_t* src, int rows, int K, int ld, uint8_t* dst,
                    hipStream_t stream);

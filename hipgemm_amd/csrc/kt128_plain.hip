@@ -14,7 +14,35 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm_t128(GemmArgs g) {
   gemm_t128_body<kVec, false, kFmt>(g, (lds_u8*)lds);
 }
 
+// K-slices: the partial tiles, then the reduce kernel (one wave per
+// workgroup) with either epilogue.
+template <int kFmt>
+__global__ __launch_bounds__(256, 1) void k_fp8_gemm_t128_split(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[CfgT128::kLdsBytes];
+  gemm_t128_body<true, false, kFmt, kActNone, kOutBf16, true>(g, (lds_u8*)lds);
+}
+
+template <bool kVec8, bool kExt>
+__global__ __launch_bounds__(64) void k_fp8_gemm_t128_reduce(GemmArgs g) {
+  gemm_t128_reduce_body<kVec8, kExt>(g);
+}
+
 }  // namespace
+
+const void* tile128_split(const Key& k) {
+  return sel4(k.fmt, [&](auto F) {
+    return (const void*)&k_fp8_gemm_t128_split<decltype(F)::value>;
+  });
+}
+
+const void* tile128_reduce(const Key& k) {
+  return sel2(k.ext, [&](auto E) {
+    return sel2(k.vec, [&](auto V) {
+      return (const void*)&k_fp8_gemm_t128_reduce<decltype(V)::value == 1,
+                                                 decltype(E)::value == 1>;
+    });
+  });
+}
 
 const void* tile128_plain(const Key& k) {
   return sel4(k.fmt, [&](auto F) {

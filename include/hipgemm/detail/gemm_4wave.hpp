@@ -88,6 +88,16 @@ __host__ __device__ constexpr size_t mx_packed_bytes(int rows, int K) {
   return (size_t)((rows + 127) / 128) * mx_pairs(K) * 1024;
 }
 
+// K-slices of the 128 x 128 schedule (gemm_t128.hpp, kSplit): work unit u
+// of tiles x slices is tile u % tiles over K-steps [s S, s S + S) of 128
+// bytes, s = u / tiles, S = slice_steps; its fp32 partial tile goes to
+// `partial` (64 KiB per unit) for the reduce kernel.
+struct SplitArgs {
+  int slices = 1;
+  int slice_steps = 0;
+  float* partial = nullptr;
+};
+
 struct GemmArgs {
   const uint8_t* A;      // M x K 8-bit (format by kFmt), row stride lda bytes
   const uint8_t* B;      // N x K 8-bit (B_T), row stride ldb bytes
@@ -100,6 +110,7 @@ struct GemmArgs {
   int workers;  // persistent workgroups (<= grid); 0 = the whole grid
   EpiArgs epi;  // extended epilogue (kExt instantiations only)
   MxArgs mx;    // MX block scales (kMx instantiations only)
+  SplitArgs split;  // K-slices (128 x 128 schedule only)
 };
 
 // The GemmArgs of a kernel whose only argument is a GemmArgs, read again

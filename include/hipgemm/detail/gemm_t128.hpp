@@ -67,15 +67,20 @@ struct CfgT128 {
   static constexpr int kStores = 8;      // per wave per tile, 16-byte path
 };
 
+// kSplit: work units are (tile, K-slice) pairs (g.split); each writes its
+// fp32 partial tile instead of C, and gemm_t128_reduce_body sums them.
 template <bool kVec, bool kExt = false, int kFmt = 0, int kAct = kActNone,
-          int kOut = kOutBf16>
+          int kOut = kOutBf16, bool kSplit = false>
 __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   using Cfg = CfgT128;
   constexpr int S = Cfg::kStages;
   constexpr int kD = Cfg::kDmaPerStep;
   constexpr int kScaleDma = kExt ? 3 : 0;
+  // Stores per wave per tile: 8 x 16 bytes of C, or 16 x 16 bytes of partial.
+  constexpr int kStores = kSplit ? 16 : Cfg::kStores;
+  static_assert(!(kSplit && kExt), "the reduce kernel applies the epilogue");
   static_assert(S >= 3, "pipeline depth");
-  static_assert((S - 3) * kD + Cfg::kStores + kScaleDma + kD < 64, "vmcnt range");
+  static_assert((S - 3) * kD + kStores + kScaleDma + kD < 64, "vmcnt range");
   const int lane = lane_id();
   const int wave = wave_id();
   const int wm = wave >> 1, wn = wave & 1;
@@ -83,12 +88,15 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   const int tiles_m = (M + Cfg::kBM - 1) / Cfg::kBM;
   const int tiles_n = (N + Cfg::kBN - 1) / Cfg::kBN;
   const int tiles = tiles_m * tiles_n;
-  const int steps = (K + Cfg::kBK - 1) / Cfg::kBK;
+  const int units = kSplit ? tiles * g.split.slices : tiles;
+  const int steps = kSplit ? g.split.slice_steps : (K + Cfg::kBK - 1) / Cfg::kBK;
   const int steps_pad = max(S, (steps + 1) & ~1);
   const int workers = g.workers > 0 ? min((int)gridDim.x, g.workers)
                                     : (int)gridDim.x;
   if ((int)blockIdx.x >= workers) return;
-  const TileWalk walk = tile_walk(blockIdx.x, workers, tiles);
+  // Work unit u: tile u % tiles, K-slice u / tiles (one slice unless kSplit),
+  // so that units running together share A rows or B columns.
+  const TileWalk walk = tile_walk(blockIdx.x, workers, units);
   int t = walk.first;
   if (t >= walk.end) return;
 
@@ -109,20 +117,28 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
     voff_b[q] = (uint32_t)row * (uint32_t)g.ldb + dchunk * 16;
   }
 
-  // Buffer resources of a tile's A rows and B rows (rows past M / N read
-  // zero); a tile index past the walk's end gets empty ranges.
+  // Buffer resources of a unit's A rows and B rows (rows past M / N read
+  // zero) and its K range [k0, kend); a unit past the walk's end gets empty
+  // ranges.
   struct Src {
     __amdgpu_buffer_rsrc_t a, b;
+    uint32_t k0;
+    int kend;
   };
-  auto src_of = [&](int tile) {
-    if (tile >= walk.end) return Src{make_rsrc(g.A, 0u), make_rsrc(g.B, 0u)};
+  auto src_of = [&](int unit) {
+    if (unit >= walk.end)
+      return Src{make_rsrc(g.A, 0u), make_rsrc(g.B, 0u), 0u, 0};
+    const int tile = kSplit ? unit % tiles : unit;
+    const int slice = kSplit ? unit / tiles : 0;
     const TileCoord c = grouped_tile(tile, tiles_m, tiles_n, g.group_m);
     const int ra = min(Cfg::kBM, M - c.m * Cfg::kBM);
     const int rb = min(Cfg::kBN, N - c.n * Cfg::kBN);
+    const int k0 = slice * steps * Cfg::kBK;
     return Src{make_rsrc(g.A + (size_t)c.m * Cfg::kBM * g.lda,
                          (uint32_t)ra * (uint32_t)g.lda),
                make_rsrc(g.B + (size_t)c.n * Cfg::kBN * g.ldb,
-                         (uint32_t)rb * (uint32_t)g.ldb)};
+                         (uint32_t)rb * (uint32_t)g.ldb),
+               (uint32_t)k0, min(K, k0 + steps * Cfg::kBK)};
   };
   Src cur = src_of(t);
   Src nxt = src_of(t + walk.stride);
@@ -132,10 +148,10 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   // past K read zero.
   auto dma_one = [&](int d, int stage, int n) {
     const bool next = d >= steps_pad;
-    uint32_t k0 = (uint32_t)(next ? d - steps_pad : d) * Cfg::kBK;
-    asm volatile("" : "+s"(k0));
-    const bool ok = (int)(k0 + dchunk * 16) < K;
     const Src& s = next ? nxt : cur;
+    uint32_t k0 = s.k0 + (uint32_t)(next ? d - steps_pad : d) * Cfg::kBK;
+    asm volatile("" : "+s"(k0));
+    const bool ok = (int)(k0 + dchunk * 16) < s.kend;
     lds_u8* base = lds + stage * Cfg::kStage;
     const int q = n & 3;
     if (n < 4)
@@ -255,7 +271,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
         // previous tile's stores (issued after this tile's first S - 1
         // steps' DMA); kExt's three scale loads only make this wait longer.
         if (stores && kk < S - 2)
-          wait_vmcnt<(S - 3) * kD + Cfg::kStores>();
+          wait_vmcnt<(S - 3) * kD + kStores>();
         else
           wait_vmcnt<(S - 3) * kD>();
         barrier();
@@ -268,6 +284,19 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
     }
 
     // ---- epilogue ---------------------------------------------------------
+    if constexpr (kSplit) {
+      // The unit's fp32 partial: wave w's 16 blocks at ((t * 4 + w) * 16 +
+      // 4 i + j) KiB of g.split.partial, lane l's 16 bytes at + 16 l.
+      const __amdgpu_buffer_rsrc_t rp = make_rsrc(
+          g.split.partial + (size_t)(t * 4 + wave) * 16 * 256, 16u * 1024u);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(i32x4, acc[i][j]), rp,
+              (uint32_t)((4 * i + j) * 1024 + lane * 16), 0, 0);
+    } else {
     const TileCoord tc = grouped_tile(t, tiles_m, tiles_n, g.group_m);
     const int rows_left = M - tc.m * Cfg::kBM - wm * 64;  // from wave row 0
     const int cols_left = N - tc.n * Cfg::kBN - wn * 64;  // from wave col 0
@@ -335,16 +364,89 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
         }
     }
 
+    }  // !kSplit
+
     t += walk.stride;
     if (t >= walk.end) break;
     base += steps_pad;
     base %= S;
     cur = nxt;
     nxt = src_of(t + walk.stride);
-    stores = kVec;
+    stores = kSplit || kVec;
   }
   // The last tile's look-ahead DMA (empty ranges) still count in vmcnt.
   wait_vmcnt<0>();
+}
+
+// Sum of the K-slice partials of gemm_t128_body<..., kSplit = true>, in
+// slice order 0, 1, ... (the result does not depend on which unit finished
+// first), then the epilogue (per-tensor, or the extended one with the
+// activation and output type chosen at run time) and the C stores.  One
+// wave per workgroup: quadrant blockIdx % 4 of tile blockIdx / 4, so
+// 4 x tiles workgroups.  Launched right after the split kernel on the same
+// stream, which makes its partials visible.  kVec8: 8-byte C stores (N and
+// ldc multiples of 4, C 8-byte aligned), else 2-byte ones.
+template <bool kVec8, bool kExt>
+__device__ __forceinline__ void gemm_t128_reduce_body(const GemmArgs& g) {
+  using Cfg = CfgT128;
+  const int lane = lane_id();
+  const int M = g.M, N = g.N;
+  const int tiles_m = (M + Cfg::kBM - 1) / Cfg::kBM;
+  const int tiles_n = (N + Cfg::kBN - 1) / Cfg::kBN;
+  const int tiles = tiles_m * tiles_n;
+  const int w = blockIdx.x & 3, t = blockIdx.x >> 2;
+  if (t >= tiles) return;
+  const int wm = w >> 1, wn = w & 1;
+  const TileCoord tc = grouped_tile(t, tiles_m, tiles_n, g.group_m);
+  const int row0 = tc.m * Cfg::kBM + wm * 64, col0 = tc.n * Cfg::kBN + wn * 64;
+  const float s = (g.scale_a ? *g.scale_a : 1.0f) * (g.scale_b ? *g.scale_b : 1.0f);
+  EpiVec<4, 4> ev;
+  if constexpr (kExt) ev.load(g.epi, M, N, row0, col0, s, lane);
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(
+      g.split.partial, (uint32_t)tiles * (uint32_t)g.split.slices * 65536u);
+  f32x4 sum[16];
+#pragma unroll
+  for (int n = 0; n < 16; ++n) sum[n] = f32x4{};
+  for (int q = 0; q < g.split.slices; ++q) {
+    const uint32_t base = (uint32_t)(((q * tiles + t) * 4 + w) * 16384);
+    f32x4 v[16];
+#pragma unroll
+    for (int n = 0; n < 16; ++n)
+      v[n] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rp, base + n * 1024 + lane * 16, 0, 0));
+#pragma unroll
+    for (int n = 0; n < 16; ++n) sum[n] += v[n];
+  }
+  const int rows_left = M - row0, cols_left = N - col0;
+  auto oob_unless = [](int x, int limit) -> uint32_t {
+    return (uint32_t)((limit - 1 - x) >> 31) & kOobOffset;
+  };
+  const int wrows = min(64, rows_left), wcols = min(64, cols_left);
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc(
+      g.C + (size_t)row0 * g.ldc + col0,
+      wrows > 0 && wcols > 0 ? (uint32_t)(((wrows - 1) * g.ldc + wcols) * 2) : 0u);
+  const int r16 = lane & 15, grp = lane >> 4;
+#pragma unroll
+  for (int n = 0; n < 16; ++n) {
+    const int i = n / 4, j = n % 4;
+    const f32x4 a = sum[n];
+    const u32x2 pk = kExt ? ev.pack4(a[0], a[1], a[2], a[3], i, j)
+                          : u32x2{pack_bf16x2(a[0] * s, a[1] * s),
+                                  pack_bf16x2(a[2] * s, a[3] * s)};
+    const int r = 16 * i + r16, col = 16 * j + 4 * grp;
+    const uint32_t rb = (uint32_t)((r * g.ldc + col) * 2) | oob_unless(r, rows_left);
+    if constexpr (kVec8) {
+      __builtin_amdgcn_raw_buffer_store_b64(pk, rc, rb | oob_unless(col, cols_left),
+                                            0, 0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t x = (e < 2 ? pk.x : pk.y) >> (16 * (e & 1));
+        __builtin_amdgcn_raw_buffer_store_b16(
+            (unsigned short)x, rc, (rb | oob_unless(col + e, cols_left)) + 2 * e, 0, 0);
+      }
+    }
+  }
 }
 
 }  // namespace detail

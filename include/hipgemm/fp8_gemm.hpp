@@ -60,7 +60,8 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4wave_256x256x128(
                       default_group_m(tiles_m, tiles_n),
                       Cfg4w::kDropinWorkers,
                       EpiArgs{},
-                      MxArgs{}};
+                      MxArgs{},
+                      SplitArgs{}};
   // 16-byte epilogue stores: N a multiple of 8 (C itself must be 16-byte
   // aligned, as every hipMalloc'd buffer is).
   gemm_4wave_body<N % 8 == 0, 16>(args, (lds_u8*)lds);

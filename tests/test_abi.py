@@ -47,6 +47,18 @@ def test_version_and_variants():
     assert hg.select_variant(129, 8192, 8192) == 5   # 2 x 64 tiles of 128
 
 
+def test_tile128_k_split_workspace():
+    """The 128 x 128 schedule splits K when its tiles fill at most a quarter
+    of the (256) CUs and K has 16+ steps: 256 x 4096 x 14336 is 2 x 32 tiles,
+    4 slices of 28 steps, one 64 KiB partial per (tile, slice)."""
+    assert hg.workspace_size(256, 4096, 14336, 5) == 64 * 4 * 65536
+    assert hg.workspace_size(256, 4096, 14336, 0) == 64 * 4 * 65536  # AUTO
+    assert hg.workspace_size(256, 8192, 8192, 5) == 0    # 128 tiles: no split
+    assert hg.workspace_size(256, 4096, 1920, 5) == 0    # 15 steps: no split
+    # 300 x 1000 x 4112: 3 x 8 tiles, 33 steps -> 4 slices of 10 steps
+    assert hg.workspace_size(300, 1000, 4112, 5) == 24 * 4 * 65536
+
+
 def test_split_columns_plan():
     """AUTO's column split (256 CUs without a device): 4000 x 5000 has 16 x
     20 tiles of 256 = 1.25 rounds; 16 tile columns fill one round, the other

@@ -162,6 +162,29 @@ def test_epilogue_transcendental(gpu, oracle, variant, act):
         assert rel <= REL_TOL
 
 
+@pytest.mark.parametrize("out,act", [(0, 0), (1, 1)])
+def test_tile128_k_split(gpu, oracle, out, act):
+    """The 128 x 128 schedule with K-slices (3 x 8 tiles, 4 slices of 10
+    steps, a K tail) and the reduce kernel's epilogue: formats, scales, bias,
+    relu, fp16; bit-exact on ternary sums, canaries around C."""
+    M, N, K = 300, 1000, 4112
+    say(f"case [v5] k-split out={out} act={act} M={M} N={N} K={K}")
+    assert hg.workspace_size(M, N, K, 5) > 0
+    rng = np.random.default_rng(87)
+    A, B = ternary(1, (M, K), 87), ternary(0, (N, K), 88)
+    sr = np.exp2(rng.integers(-3, 4, M)).astype(np.float32)
+    sc = np.exp2(rng.integers(-3, 4, N)).astype(np.float32)
+    bias = rng.uniform(-4, 4, N).astype(np.float32)
+    ext = dict(sr=sr, sc=sc, bias=bias) if out or act else {}
+    C, guard = run(gpu, A, B, fa=1, out=out, act=act, sa=[0.5], sb=[2.0],
+                   variant=5, **ext)
+    assert guard
+    want = oracle.gemm_ex(A, B, a_fmt=1, out=out, act=act, scale_a=0.5,
+                          scale_b=2.0, scale_rows=ext.get("sr"),
+                          scale_cols=ext.get("sc"), bias=ext.get("bias"))
+    assert np.array_equal(C, want), f"{int((C != want).sum())} differ"
+
+
 def test_auto_split_epilogue(gpu, oracle):
     """AUTO's column split with every column-indexed option: the column
     scales and the bias of the 128 x 128 half are offset by the split

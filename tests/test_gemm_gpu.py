@@ -158,6 +158,17 @@ def test_config5_skinny_and_ragged(gpu, oracle, M, N, K, variant):
     check_full(oracle, C, A, B, None, None)
 
 
+def test_tile128_k_split_general(gpu, oracle):
+    """AUTO on 256 x 4096 x 14336: the 128 x 128 schedule split 4 ways in K
+    (64 tiles), general inputs against the oracle."""
+    M, N, K = 256, 4096, 14336
+    say(f"case [auto] tile128-ksplit M={M} N={N} K={K} N(0,1) seed=57")
+    assert hg.select_variant(M, N, K) == 5
+    A, B = gen(oracle, M, N, K, 57, po.NORMAL, 0.0, 1.0)
+    C = run_gpu(gpu, A, B, 0.75, 1.5, variant=0)
+    check_full(oracle, C, A, B, 0.75, 1.5)
+
+
 def test_config5c_auto_split(gpu, oracle):
     """AUTO on 4000 x 5000 x 3584 splits C: columns [0, n1) on the 4-wave
     schedule (one full round of 256 x 256 tiles on a 256-CU device), the rest
