@@ -31,7 +31,8 @@ __all__ = [
     "variant_name", "version", "tile_order", "lds_slot", "VARIANTS",
     "declared_symbols", "gemm_raw_ws", "workspace_size",
     "fp8_gemm_bf16_rowcol", "gemm_raw_rowcol", "GemmDesc", "gemm_desc_raw",
-    "gemm", "FMT_E4M3", "FMT_E5M2", "OUT_BF16", "OUT_F16", "ACTIVATIONS",
+    "gemm", "FMT_E4M3", "FMT_E5M2", "OUT_BF16", "OUT_F16", "OUT_F32",
+    "OUT_FP8_E4M3", "ACTIVATIONS",
     "mx_scales_bytes", "mx_pack_scales",
 ]
 
@@ -45,7 +46,7 @@ VARIANTS = {"auto": 0, "4wave": 1, "4wave_mfma16": 2, "skinny": 3, "8wave": 4,
 
 # include/hipgemm.h codes
 FMT_E4M3, FMT_E5M2 = 0, 1
-OUT_BF16, OUT_F16 = 0, 1
+OUT_BF16, OUT_F16, OUT_F32, OUT_FP8_E4M3 = 0, 1, 2, 3
 ACTIVATIONS = {None: 0, "none": 0, "relu": 1, "gelu_tanh": 2, "silu": 3}
 
 hipSuccess = 0
@@ -69,7 +70,8 @@ class GemmDesc(ctypes.Structure):
                 ("workspace", ctypes.c_void_p),
                 ("workspace_bytes", ctypes.c_size_t),
                 ("mx_scale_a", ctypes.c_void_p),
-                ("mx_scale_b", ctypes.c_void_p)]
+                ("mx_scale_b", ctypes.c_void_p),
+                ("scale_out", ctypes.c_void_p)]
 
     def __init__(self, **kw):
         super().__init__()
@@ -79,7 +81,8 @@ class GemmDesc(ctypes.Structure):
 
 
 _PTR_FIELDS = {"A", "B_T", "C", "scale_a", "scale_b", "scale_rows",
-               "scale_cols", "bias", "workspace", "mx_scale_a", "mx_scale_b"}
+               "scale_cols", "bias", "workspace", "mx_scale_a", "mx_scale_b",
+               "scale_out"}
 
 
 class HipGemmError(RuntimeError):
@@ -325,10 +328,11 @@ def _mx_ptr(t, rows, K, name):
     return t.data_ptr()
 
 
-def _gemm_operands(a, b_t, out, variant, stream):
+def _gemm_operands(a, b_t, out, variant, stream, out_dtype=None):
     """Shared argument handling of the torch entry points: shapes, strides,
-    output, stream and workspace."""
+    output (out_dtype, default bfloat16), stream and workspace."""
     torch = _torch()
+    out_dtype = out_dtype or torch.bfloat16
     a = _as_bytes_2d(a, "a")
     b_t = _as_bytes_2d(b_t, "b_t")
     M, K = a.shape
@@ -337,10 +341,10 @@ def _gemm_operands(a, b_t, out, variant, stream):
         raise HipGemmError(f"K mismatch: a has {K}, b_t has {K2}",
                            hipErrorInvalidValue)
     if out is None:
-        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
-    elif (out.dtype != torch.bfloat16 or tuple(out.shape) != (M, N) or
+        out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    elif (out.dtype != out_dtype or tuple(out.shape) != (M, N) or
           (M > 0 and N > 0 and out.stride(1) != 1)):
-        raise HipGemmError("out must be a (M, N) bfloat16 tensor with unit "
+        raise HipGemmError(f"out must be a (M, N) {out_dtype} tensor with unit "
                            "column stride", hipErrorInvalidValue)
     if stream is None:
         stream = torch.cuda.current_stream(a.device)
@@ -376,13 +380,17 @@ def fp8_gemm_bf16(a, b_t, scale_a=None, scale_b=None, out=None,
 def gemm(a, b_t, *, a_format: int = FMT_E4M3, b_format: int = FMT_E4M3,
          out_dtype=None, scale_a=None, scale_b=None, scale_rows=None,
          scale_cols=None, bias=None, activation=None, out=None,
-         variant: int = 0, stream=None, mx_scale_a=None, mx_scale_b=None):
+         variant: int = 0, stream=None, mx_scale_a=None, mx_scale_b=None,
+         scale_out=None):
     """The general entry point (hipgemm_gemm): out[m, n] =
     round(act(fma(acc, scale_rows[m] * (scale_cols[n] * (scale_a *
     scale_b)), bias[n]))), acc = a @ b_t.T with a in a_format and b_t in
     b_format (FMT_E4M3 / FMT_E5M2; float8_e4m3fn / float8_e5m2 tensors set
-    it from their dtype).  out_dtype: torch.bfloat16 (default) or
-    torch.float16.  activation: None, "relu", "gelu_tanh" or "silu".
+    it from their dtype).  out_dtype: torch.bfloat16 (default),
+    torch.float16, torch.float32 or torch.float8_e4m3fn (saturating; then
+    scale_out, a 1-element float32 device tensor, multiplies the activated
+    value before the conversion).  activation: None, "relu", "gelu_tanh" or
+    "silu".
     scale_a / scale_b: 1-element float32 device tensors; scale_rows (M),
     scale_cols (N), bias (N): float32 device vectors; any may be None.
     mx_scale_a / mx_scale_b: MX block scales packed by mx_pack_scales
@@ -392,25 +400,24 @@ def gemm(a, b_t, *, a_format: int = FMT_E4M3, b_format: int = FMT_E4M3,
     a_format = fmts.get(a.dtype, a_format)
     b_format = fmts.get(b_t.dtype, b_format)
     out_dtype = out_dtype or (out.dtype if out is not None else torch.bfloat16)
-    if out_dtype not in (torch.bfloat16, torch.float16):
-        raise HipGemmError("out_dtype must be bfloat16 or float16",
-                           hipErrorInvalidValue)
+    codes = {torch.bfloat16: OUT_BF16, torch.float16: OUT_F16,
+             torch.float32: OUT_F32, torch.float8_e4m3fn: OUT_FP8_E4M3}
+    if out_dtype not in codes:
+        raise HipGemmError("out_dtype must be bfloat16, float16, float32 or "
+                           "float8_e4m3fn", hipErrorInvalidValue)
     if activation not in ACTIVATIONS:
         raise HipGemmError(f"activation must be one of {sorted(k for k in ACTIVATIONS if k)}",
                            hipErrorInvalidValue)
-    if out is None:
-        out = torch.empty((a.shape[0], b_t.shape[0]), dtype=out_dtype,
-                          device=a.device)
-    elif out.dtype != out_dtype:
+    if out is not None and out.dtype != out_dtype:
         raise HipGemmError("out has the wrong dtype", hipErrorInvalidValue)
     a, b_t, out, M, N, K, lda, ldb, ldc, ws, nbytes, stream = _gemm_operands(
         a.view(torch.uint8) if a.dtype == torch.float8_e5m2 else a,
         b_t.view(torch.uint8) if b_t.dtype == torch.float8_e5m2 else b_t,
-        out.view(torch.bfloat16), variant, stream)
+        out, variant, stream, out_dtype)
     d = GemmDesc(A=a.data_ptr(), B_T=b_t.data_ptr(), C=out.data_ptr(), M=M,
                  N=N, K=K, lda=lda, ldb=ldb, ldc=ldc, a_format=a_format,
                  b_format=b_format,
-                 out_dtype=OUT_F16 if out_dtype == torch.float16 else OUT_BF16,
+                 out_dtype=codes[out_dtype],
                  activation=ACTIVATIONS[activation],
                  scale_a=_scale_ptr(scale_a, "scale_a"),
                  scale_b=_scale_ptr(scale_b, "scale_b"),
@@ -419,9 +426,10 @@ def gemm(a, b_t, *, a_format: int = FMT_E4M3, b_format: int = FMT_E4M3,
                  bias=_vector_ptr(bias, N, "bias"), variant=variant,
                  workspace=ws, workspace_bytes=nbytes,
                  mx_scale_a=_mx_ptr(mx_scale_a, M, K, "mx_scale_a"),
-                 mx_scale_b=_mx_ptr(mx_scale_b, N, K, "mx_scale_b"))
+                 mx_scale_b=_mx_ptr(mx_scale_b, N, K, "mx_scale_b"),
+                 scale_out=_scale_ptr(scale_out, "scale_out"))
     _check(gemm_desc_raw(d, stream.cuda_stream), "hipgemm_gemm")
-    return out.view(out_dtype)
+    return out
 
 
 def fp8_gemm_bf16_rowcol(a, b_t, scale_rows=None, scale_cols=None, out=None,

@@ -20,27 +20,29 @@ static_assert(HIPGEMM_ACT_NONE == kActNone && HIPGEMM_ACT_RELU == kActRelu &&
                   HIPGEMM_ACT_GELU_TANH == kActGeluTanh &&
                   HIPGEMM_ACT_SILU == kActSilu,
               "activation codes");
-static_assert(HIPGEMM_OUT_BF16 == kOutBf16 && HIPGEMM_OUT_F16 == kOutF16,
+static_assert(HIPGEMM_OUT_BF16 == kOutBf16 && HIPGEMM_OUT_F16 == kOutF16 &&
+                  HIPGEMM_OUT_F32 == kOutF32 && HIPGEMM_OUT_FP8_E4M3 == kOutF8,
               "output codes");
 static_assert(HIPGEMM_FMT_E4M3 == kFmtE4M3 && HIPGEMM_FMT_E5M2 == kFmtE5M2,
               "format codes");
 
 // 32-bit buffer offsets: 256 rows of A or B_T (1-byte elements) span at most
-// 2^31 bytes, 256 rows of C (2-byte elements) likewise.
+// 2^31 bytes, 256 rows of C likewise (ldc * element size <= 2^23 bytes).
 constexpr int kMaxLd = 1 << 23;
-constexpr int kMaxLdc = 1 << 22;
+constexpr int kMaxLdcBytes = 1 << 23;
 
 bool aligned(const void* p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
 
+// es: bytes per element of C.
 hipError_t validate(const void* A, const void* B_T, void* C, int M, int N,
-                    int K, int lda, int ldb, int ldc, int variant) {
+                    int K, int lda, int ldb, int ldc, int variant, int es) {
   if (M < 0 || N < 0 || K < 0) return hipErrorInvalidValue;
   if (variant < 0 || variant >= HIPGEMM_VARIANT_COUNT)
     return hipErrorInvalidValue;
   if (M == 0 || N == 0) return hipSuccess;
-  if (!C || !aligned(C, 2) || ldc < N || ldc > kMaxLdc)
+  if (!C || !aligned(C, es) || ldc < N || ldc > kMaxLdcBytes / es)
     return hipErrorInvalidValue;
   if (K == 0) return hipSuccess;  // A and B_T are not read
   if (!A || !B_T) return hipErrorInvalidValue;
@@ -73,6 +75,13 @@ int cu_count() {
   return n;
 }
 
+// One store per lane of `group` consecutive elements of C (of output type
+// out): N and ldc multiples of the group, C aligned to the group's bytes.
+bool vec_ok(int out, int N, int ldc, const void* C, int group) {
+  const int bytes = group * out_bytes(out);
+  return N % group == 0 && ldc % group == 0 && aligned(C, (uintptr_t)bytes);
+}
+
 // The tiled schedules (4-wave, 8-wave) on a persistent grid: one workgroup
 // per CU at most (their 160 KiB of LDS allows no more), each walking tiles
 // w, w + grid, ...  `key.vec` is set here: 16-byte epilogue stores need
@@ -87,7 +96,9 @@ hipError_t launch_tiled(int variant, GemmArgs g, hk::Key key,
   const int cus = cu_count();
   const int grid = tiles < cus ? tiles : cus;
   g.workers = grid;
-  key.vec = (g.N % 8 == 0) && (g.ldc % 8 == 0) && aligned(g.C, 16);
+  // 2-byte types: 16-byte stores of 8 staged elements; fp32 / e4m3: one
+  // store of 4 elements straight from the accumulators.
+  key.vec = vec_ok(key.out, g.N, g.ldc, g.C, key.out >= kOutF32 ? 4 : 8);
   const void* fn = nullptr;
   int threads = Cfg4w::kThreads;
   switch (variant) {
@@ -110,6 +121,7 @@ hipError_t launch_tiled(int variant, GemmArgs g, hk::Key key,
         break;
       }
       fn = !key.ext ? hk::four_wave_plain(16, key)
+           : key.out >= kOutF32          ? hk::four_wave_ext_wide(key)
            : key.out == HIPGEMM_OUT_F16 ? hk::four_wave_ext_f16(key)
                                         : hk::four_wave_ext_bf16(key);
       break;
@@ -161,8 +173,8 @@ hipError_t launch_skinny(const GemmArgs& a, const SkinnyPlan& p, void* ws,
     g.arrivals = static_cast<int*>(ws);
     g.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + p.counter_bytes);
   }
-  // 8-byte stores need 4-column groups that never straddle N.
-  key.vec = (a.N % 4 == 0) && (a.ldc % 4 == 0) && aligned(a.C, 8);
+  // One store per lane of 4 columns that never straddle N.
+  key.vec = vec_ok(key.out, a.N, a.ldc, a.C, 4);
   const int grid = p.tiles_n * p.slices;
   const void* fn = key.ext ? hk::skinny_ext(p.kmb, key) : hk::skinny_plain(p.kmb, key);
   if (!fn) return hipErrorInvalidValue;
@@ -228,7 +240,7 @@ hipError_t launch_t128_split(GemmArgs g, const T128Plan& p, void* ws,
   hipError_t e = hipLaunchKernel(fn, dim3(g.workers), dim3(CfgT128::kThreads),
                                  args, 0, stream);
   if (e != hipSuccess) return e;
-  key.vec = (g.N % 4 == 0) && (g.ldc % 4 == 0) && aligned(g.C, 8);
+  key.vec = vec_ok(key.out, g.N, g.ldc, g.C, 4);
   fn = hk::tile128_reduce(key);
   if (!fn) return hipErrorInvalidValue;
   return hipLaunchKernel(fn, dim3(tiles * 4), dim3(64), args, 0, stream);
@@ -266,7 +278,9 @@ bool valid_code(int v, int count) { return v >= 0 && v < count; }
 hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
                     hipStream_t stream) {
   int M = d.M, N = d.N, K = d.K, lda = d.lda, ldb = d.ldb, variant = d.variant;
-  hipError_t e = validate(d.A, d.B_T, d.C, M, N, K, lda, ldb, d.ldc, variant);
+  if (!valid_code(d.out_dtype, 4)) return hipErrorInvalidValue;
+  const int es = out_bytes(d.out_dtype);
+  hipError_t e = validate(d.A, d.B_T, d.C, M, N, K, lda, ldb, d.ldc, variant, es);
   if (e != hipSuccess) return e;
   if (variant == HIPGEMM_VARIANT_SKINNY && M > CfgSkinny::kMaxM)
     return hipErrorInvalidValue;
@@ -275,12 +289,17 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   if (ws_given && ws_bytes > 0 && (!ws || !aligned(ws, 256)))
     return hipErrorInvalidValue;
   if (!valid_code(d.a_format, 2) || !valid_code(d.b_format, 2) ||
-      !valid_code(d.out_dtype, 2) || !valid_code(d.activation, 4))
+      !valid_code(d.activation, 4))
+    return hipErrorInvalidValue;
+  // The output scale belongs to the e4m3 output; fp32 / e4m3 outputs are not
+  // built for the 8-wave schedule.
+  if (d.scale_out && d.out_dtype != HIPGEMM_OUT_FP8_E4M3) return hipErrorInvalidValue;
+  if (d.out_dtype >= HIPGEMM_OUT_F32 && variant == HIPGEMM_VARIANT_8WAVE)
     return hipErrorInvalidValue;
   if (M == 0 || N == 0) return hipSuccess;
   // Vectors are read with 4-byte loads.
   if (!aligned(d.scale_rows, 4) || !aligned(d.scale_cols, 4) ||
-      !aligned(d.bias, 4))
+      !aligned(d.bias, 4) || !aligned(d.scale_out, 4))
     return hipErrorInvalidValue;
   const bool ext = d.scale_rows || d.scale_cols || d.bias ||
                    d.activation != HIPGEMM_ACT_NONE ||
@@ -301,6 +320,8 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
                      ? split_columns(M, N, cu_count())
                      : 0;
   variant = mx ? HIPGEMM_VARIANT_4WAVE_MFMA16 : resolve_variant(variant, M, N, K);
+  if (variant == HIPGEMM_VARIANT_8WAVE && d.out_dtype >= HIPGEMM_OUT_F32)
+    variant = HIPGEMM_VARIANT_4WAVE_MFMA16;  // AUTO's 8-wave choice
   if (K == 0) lda = ldb = 16;  // nothing is read; keep the offset math inert
   const int tiles_m = (M + Cfg4w::kBM - 1) / Cfg4w::kBM;
   const int tiles_n = (N + Cfg4w::kBN - 1) / Cfg4w::kBN;
@@ -325,6 +346,7 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   g.epi.bias = d.bias;
   g.epi.act = d.activation;
   g.epi.out = d.out_dtype;
+  g.epi.out_scale = d.scale_out;
   g.mx.a = static_cast<const uint8_t*>(d.mx_scale_a);
   g.mx.b = static_cast<const uint8_t*>(d.mx_scale_b);
   hk::Key key;
@@ -371,7 +393,8 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
         g.N = n1;
         g2.N = N - n1;
         g2.B += (size_t)n1 * ldb;
-        g2.C += n1;
+        g2.C = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(g.C) +
+                                           (size_t)n1 * es);
         if (g2.epi.col_scale) g2.epi.col_scale += n1;
         if (g2.epi.bias) g2.epi.bias += n1;
         e = launch_tiled(HIPGEMM_VARIANT_4WAVE_MFMA16, g, key, stream);

@@ -1,0 +1,35 @@
+// The 4-wave 16x16x128 schedule with the extended epilogue and fp32 or e4m3
+// output, for every operand-format pair and activation.
+#include "kernels.hpp"
+
+namespace hipgemm {
+namespace kernels {
+namespace {
+
+using namespace detail;
+
+template <bool kVec, int kFmt, int kAct, int kOut>
+__global__ __launch_bounds__(256, 1) void k_fp8_gemm_4wave_ext_wide(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg4w::kLdsBytes];
+  gemm_4wave_body<kVec, 16, true, kFmt, kAct, kOut>(g, (lds_u8*)lds);
+}
+
+}  // namespace
+
+const void* four_wave_ext_wide(const Key& k) {
+  if (k.out != kOutF32 && k.out != kOutF8) return nullptr;
+  return sel4(k.fmt, [&](auto F) {
+    return sel4(k.act, [&](auto A) {
+      return sel2(k.vec, [&](auto V) {
+        if (k.out == kOutF32)
+          return (const void*)&k_fp8_gemm_4wave_ext_wide<
+              decltype(V)::value == 1, decltype(F)::value, decltype(A)::value, kOutF32>;
+        return (const void*)&k_fp8_gemm_4wave_ext_wide<
+            decltype(V)::value == 1, decltype(F)::value, decltype(A)::value, kOutF8>;
+      });
+    });
+  });
+}
+
+}  // namespace kernels
+}  // namespace hipgemm

@@ -30,6 +30,7 @@ struct Key {
 const void* four_wave_plain(int mf, const Key& k);  // k4wave_plain.hip
 const void* four_wave_ext_bf16(const Key& k);       // k4wave_ext_bf16.hip
 const void* four_wave_ext_f16(const Key& k);        // k4wave_ext_f16.hip
+const void* four_wave_ext_wide(const Key& k);       // k4wave_ext_wide.hip
 const void* eight_wave_plain(const Key& k);         // k8wave_plain.hip
 const void* eight_wave_ext_bf16(const Key& k);      // k8wave_ext_bf16.hip
 const void* eight_wave_ext_f16(const Key& k);       // k8wave_ext_f16.hip

@@ -1,5 +1,5 @@
 // The 128 x 128-tile schedule with the extended epilogue, for every
-// operand-format pair, activation and output type.
+// operand-format pair, activation and output type (bf16, fp16, fp32, e4m3).
 #include "kernels.hpp"
 
 namespace hipgemm {
@@ -19,7 +19,7 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm_t128_ext(GemmArgs g) {
 const void* tile128_ext(const Key& k) {
   return sel4(k.fmt, [&](auto F) {
     return sel4(k.act, [&](auto A) {
-      return sel2(k.out, [&](auto O) {
+      return sel4(k.out, [&](auto O) {
         return sel2(k.vec, [&](auto V) {
           return (const void*)&k_fp8_gemm_t128_ext<
               decltype(V)::value == 1, decltype(F)::value, decltype(A)::value,

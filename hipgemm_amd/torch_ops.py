@@ -12,10 +12,13 @@ Importing this module registers, in the ``hipgemm`` namespace:
       hipgemm_fp8_gemm_bf16_rowcol.
   torch.ops.hipgemm.gemm(a, b_t, scale_a=None, scale_b=None, scale_rows=None,
                          scale_cols=None, bias=None, activation="none",
-                         out_f16=False, variant=0)
+                         out_f16=False, variant=0, out_dtype=None,
+                         scale_out=None)
       the general entry point (hipgemm_gemm): a / b_t float8_e4m3fn or
       float8_e5m2 (uint8 bytes: e4m3), fused bias and activation ("none",
-      "relu", "silu", "gelu_tanh"), bf16 or fp16 output.
+      "relu", "silu", "gelu_tanh"); output bf16, fp16 (out_f16 or
+      out_dtype), fp32 or float8_e4m3fn (out_dtype; saturating, after
+      multiplying by the 1-element scale_out).
 
 All have fake (meta) implementations, so they trace under torch.compile,
 torch.export and FakeTensorMode without running, and they run inside CUDA
@@ -85,17 +88,28 @@ def gemm(a: torch.Tensor, b_t: torch.Tensor,
          scale_rows: Optional[torch.Tensor] = None,
          scale_cols: Optional[torch.Tensor] = None,
          bias: Optional[torch.Tensor] = None, activation: str = "none",
-         out_f16: bool = False, variant: int = 0) -> torch.Tensor:
-    return _gemm(a, b_t, out_dtype=torch.float16 if out_f16 else torch.bfloat16,
+         out_f16: bool = False, variant: int = 0,
+         out_dtype: Optional[torch.dtype] = None,
+         scale_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    return _gemm(a, b_t, out_dtype=_out_dtype(out_f16, out_dtype),
                  scale_a=scale_a, scale_b=scale_b, scale_rows=scale_rows,
                  scale_cols=scale_cols, bias=bias, activation=activation,
-                 variant=variant)
+                 variant=variant, scale_out=scale_out)
+
+
+def _out_dtype(out_f16, out_dtype):
+    if out_dtype is not None:
+        if out_dtype not in (torch.bfloat16, torch.float16, torch.float32,
+                             torch.float8_e4m3fn):
+            raise HipGemmError(f"unsupported out_dtype {out_dtype}")
+        return out_dtype
+    return torch.float16 if out_f16 else torch.bfloat16
 
 
 @gemm.register_fake
 def _gemm_fake(a, b_t, scale_a=None, scale_b=None, scale_rows=None,
                scale_cols=None, bias=None, activation="none", out_f16=False,
-               variant=0):
+               variant=0, out_dtype=None, scale_out=None):
     _check_shapes(a, b_t)
     if activation not in ACTIVATIONS:
         raise HipGemmError(f"unknown activation {activation!r}")
@@ -105,7 +119,7 @@ def _gemm_fake(a, b_t, scale_a=None, scale_b=None, scale_rows=None,
         if v is not None and tuple(v.shape) != (n,):
             raise HipGemmError(f"{name} must have {n} elements")
     return a.new_empty((a.shape[0], b_t.shape[0]),
-                       dtype=torch.float16 if out_f16 else torch.bfloat16)
+                       dtype=_out_dtype(out_f16, out_dtype))
 
 
 def _check_shapes(a, b_t):

@@ -85,7 +85,18 @@ enum {
 };
 
 /* Output element types (RNE from the fp32 result). */
-enum { HIPGEMM_OUT_BF16 = 0, HIPGEMM_OUT_F16 = 1 };
+/* Output types of hipgemm_gemm.  BF16, F16: round to nearest even; F32: the
+ * fp32 value itself; FP8_E4M3: OCP e4m3 of activation(v) * scale_out, round
+ * to nearest even, finite magnitudes above 448 saturate to 448, Inf and NaN
+ * become NaN (0x7f | sign) -- the __HIP_SATFINITE conversion of
+ * amd_hip_fp8.h.  F32 and FP8_E4M3 run on schedules AUTO, 4WAVE_MFMA16,
+ * SKINNY and TILE128. */
+enum {
+  HIPGEMM_OUT_BF16 = 0,
+  HIPGEMM_OUT_F16 = 1,
+  HIPGEMM_OUT_F32 = 2,
+  HIPGEMM_OUT_FP8_E4M3 = 3
+};
 
 /* Activations of the fused epilogue, applied in fp32 after bias:
  *   RELU(v) = v < 0 ? 0 : v
@@ -105,7 +116,7 @@ enum {
  *
  *   scale[m,n] = scale_rows[m] * (scale_cols[n] * (scale_a * scale_b))
  *   v[m,n]     = fma(acc[m,n], scale[m,n], bias[n])       (one rounding)
- *   C[m,n]     = round_out(activation(v[m,n]))
+ *   C[m,n]     = round_out(activation(v[m,n]) [* scale_out, e4m3 only])
  *
  * acc is the fp32 sum over K of A[m,k] * B_T[n,k] with A in a_format and
  * B_T in b_format.  NULL scalars and vectors are ones, a NULL bias is
@@ -121,7 +132,8 @@ typedef struct hipgemm_gemm_desc {
   size_t size;
   const void *A;   /* M x K, row stride lda bytes */
   const void *B_T; /* N x K, row stride ldb bytes */
-  void *C;         /* M x N, row stride ldc elements of out_dtype */
+  void *C;         /* M x N, row stride ldc elements of out_dtype, aligned
+                    * to one element */
   int M, N, K;
   int lda, ldb, ldc;
   int a_format, b_format; /* HIPGEMM_FMT_* */
@@ -141,6 +153,9 @@ typedef struct hipgemm_gemm_desc {
    * still apply.  Not combined with the row / column / bias / activation /
    * fp16 options; schedules AUTO and HIPGEMM_VARIANT_4WAVE_MFMA16. */
   const void *mx_scale_a, *mx_scale_b;
+  /* Device scalar or NULL (1.0) multiplying activation(v) before the
+   * conversion; FP8_E4M3 output only (NULL otherwise), 4-byte aligned. */
+  const float *scale_out;
 } hipgemm_gemm_desc;
 
 /*

@@ -138,6 +138,7 @@ __device__ __forceinline__ EpiArgs kernel_epi() {
   e.bias = k->epi.bias;
   e.act = k->epi.act;
   e.out = k->epi.out;
+  e.out_scale = k->epi.out_scale;
   return e;
 }
 
@@ -670,9 +671,11 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     // Every store is a buffer store over this tile's window of C; a lane
     // whose row or columns fall outside M x N gets an out-of-range offset and
     // its write is dropped by the hardware range check -- no branches.
+    constexpr int es = kExt ? out_bytes(kOut) : 2;  // bytes per C element
     const __amdgpu_buffer_rsrc_t rsrc_c = make_rsrc(
-        g.C + (size_t)tc.m * Cfg::kBM * g.ldc + (size_t)tc.n * Cfg::kBN,
-        (uint32_t)(((rows_c - 1) * g.ldc + Cfg::kBN) * 2));
+        reinterpret_cast<uint8_t*>(g.C) +
+            ((size_t)tc.m * Cfg::kBM * g.ldc + (size_t)tc.n * Cfg::kBN) * es,
+        (uint32_t)(((rows_c - 1) * g.ldc + Cfg::kBN) * es));
     const int rows_left = M - tc.m * Cfg::kBM - wm * 128;  // from wave row 0
     const int cols_left = N - tc.n * Cfg::kBN - wn * 128;  // from wave col 0
     // Elements of 16 x 16 block (bi, bj), packed.  kExt: the vectors come
@@ -694,7 +697,57 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                      pack_bf16x2(acc_read(a[2]) * scale, acc_read(a[3]) * scale)};
     };
 
-    if constexpr (kVecStore) {
+    if constexpr (kExt && kOut >= kOutF32) {
+      // fp32 / e4m3 output: straight from the accumulators, no staging --
+      // block (i, j): lane l -> row 16 i + l % 16, columns 16 j + 4 (l / 16)
+      // .. + 3, one 16-byte (fp32) or 4-byte (e4m3) store per lane, or one
+      // per element when N, ldc or C's alignment rule that out.
+      const uint32_t vlane =
+          (uint32_t)(((elane & 15) * g.ldc + wn * 128 + 4 * (elane >> 4)) * es);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int srow =
+            __builtin_amdgcn_readfirstlane((wm * 128 + 16 * i) * g.ldc * es);
+        const uint32_t vrow = vlane | oob_unless(16 * i + (elane & 15), rows_left);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int c = 16 * j + 4 * (elane >> 4);
+          const f32x4& a = acc16[i][j];
+          const f32x4 v = ev.template value4<kAct>(acc_read(a[0]), acc_read(a[1]),
+                                                   acc_read(a[2]), acc_read(a[3]),
+                                                   i, j);
+          if constexpr (kOut == kOutF32) {
+            if constexpr (kVecStore) {
+              __builtin_amdgcn_raw_buffer_store_b128(
+                  __builtin_bit_cast(i32x4, v), rsrc_c,
+                  (vrow | oob_unless(c, cols_left)) + 16 * j * es, srow, kStoreC);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                __builtin_amdgcn_raw_buffer_store_b32(
+                    (uint32_t)__builtin_bit_cast(i32x4, v)[e], rsrc_c,
+                    (vrow | oob_unless(c + e, cols_left)) + (16 * j + e) * es,
+                    srow, kStoreC);
+            }
+          } else {
+            const uint32_t w = ev.e4m3x4(v);
+            if constexpr (kVecStore) {
+              __builtin_amdgcn_raw_buffer_store_b32(
+                  w, rsrc_c, (vrow | oob_unless(c, cols_left)) + 16 * j * es, srow,
+                  kStoreC);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                __builtin_amdgcn_raw_buffer_store_b8(
+                    (uint8_t)(w >> (8 * e)), rsrc_c,
+                    (vrow | oob_unless(c + e, cols_left)) + (16 * j + e) * es,
+                    srow, kStoreC);
+            }
+          }
+          sched_fence();  // bound the live range: one block at a time
+        }
+      }
+    } else if constexpr (kVecStore) {
       // 32 rows (one accumulator block row i) at a time through the wave's
       // own 8 KiB: row r at 256 r; the 8-byte piece x (0..31) of the row at
       // slot x ^ r.  Writes: lanes 0-31 (one 8-byte piece each of rows

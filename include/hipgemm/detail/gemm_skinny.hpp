@@ -288,8 +288,10 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   // ---- last arrival: sum the slices in order, scale, bf16, store ----------
   SkinnyEpi<kMB, kExt, kF> scl;
   scl.load(g, 0, n0 + wave * 16 * kF, lane);
+  const int es = kExt ? out_bytes(scl.ev.out) : 2;  // bytes per C element
   const __amdgpu_buffer_rsrc_t rsrc_c =
-      make_rsrc(g.C + n0, (uint32_t)(((M - 1) * g.ldc + rows_b) * 2));
+      make_rsrc(reinterpret_cast<uint8_t*>(g.C) + (size_t)n0 * es,
+                (uint32_t)(((M - 1) * g.ldc + rows_b) * es));
   auto oob_unless = [](int x, int limit) -> uint32_t {
     return (uint32_t)((limit - 1 - x) >> 31) & kOobOffset;
   };
@@ -342,8 +344,14 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
       // column 16 kF w + 16f + 4(l/16) + i (4 consecutive columns).
       const int row = 16 * m + r16;
       const int col = wave * 16 * kF + 16 * f + 4 * grp;
-      const uint32_t base = (uint32_t)((row * g.ldc + col) * 2) |
+      const uint32_t base = (uint32_t)((row * g.ldc + col) * es) |
                             oob_unless(row, M);
+      if constexpr (kExt) {
+        const f32x4& a = sum[m][f];
+        store_out4<kVec8>(scl.ev, a[0], a[1], a[2], a[3], m, f, rsrc_c, base, col,
+                          rows_b);
+        continue;
+      }
       const u32x2 pk = scl.pack4(sum[m][f], m, f);
       const uint32_t lo = pk.x, hi = pk.y;
       if constexpr (kVec8) {
@@ -416,8 +424,10 @@ __device__ __forceinline__ void gemm_skinny_reduce_body(const SkinnyArgs& g,
       for (int f = 0; f < kF; ++f) sum[f] += live ? v[u][f] : f32x4{};
     }
   }
+  const int es = kExt ? out_bytes(scl.ev.out) : 2;  // bytes per C element
   const __amdgpu_buffer_rsrc_t rsrc_c =
-      make_rsrc(g.C + n0, (uint32_t)(((M - 1) * g.ldc + rows_b) * 2));
+      make_rsrc(reinterpret_cast<uint8_t*>(g.C) + (size_t)n0 * es,
+                (uint32_t)(((M - 1) * g.ldc + rows_b) * es));
   auto oob_unless = [](int x, int limit) -> uint32_t {
     return (uint32_t)((limit - 1 - x) >> 31) & kOobOffset;
   };
@@ -425,7 +435,13 @@ __device__ __forceinline__ void gemm_skinny_reduce_body(const SkinnyArgs& g,
   for (int f = 0; f < kF; ++f) {
     const int row = 16 * m + r16;
     const int col = wave * 16 * kF + 16 * f + 4 * grp;
-    const uint32_t base = (uint32_t)((row * g.ldc + col) * 2) | oob_unless(row, M);
+    const uint32_t base = (uint32_t)((row * g.ldc + col) * es) | oob_unless(row, M);
+    if constexpr (kExt) {
+      const f32x4& a = sum[f];
+      store_out4<kVec8>(scl.ev, a[0], a[1], a[2], a[3], 0, f, rsrc_c, base, col,
+                        rows_b);
+      continue;
+    }
     const u32x2 pk = scl.pack4(sum[f], 0, f);
     const uint32_t lo = pk.x, hi = pk.y;
     if constexpr (kVec8) {

@@ -76,8 +76,10 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   constexpr int S = Cfg::kStages;
   constexpr int kD = Cfg::kDmaPerStep;
   constexpr int kScaleDma = kExt ? 3 : 0;
-  // Stores per wave per tile: 8 x 16 bytes of C, or 16 x 16 bytes of partial.
-  constexpr int kStores = kSplit ? 16 : Cfg::kStores;
+  // Stores per wave per tile: 8 x 16 bytes of C (2-byte types, staged),
+  // 16 x 16 bytes of partial, or 16 straight from the accumulators (fp32 /
+  // e4m3 output, one per block).
+  constexpr int kStores = kSplit || (kExt && kOut >= kOutF32) ? 16 : Cfg::kStores;
   static_assert(!(kSplit && kExt), "the reduce kernel applies the epilogue");
   static_assert(S >= 3, "pipeline depth");
   static_assert((S - 3) * kD + kStores + kScaleDma + kD < 64, "vmcnt range");
@@ -317,13 +319,54 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
     };
     // C window of this wave: rows tc.m*128 + 64 wm .., columns tc.n*128 +
     // 64 wn ..; the range ends at its last valid element.
+    constexpr int es = kExt ? out_bytes(kOut) : 2;  // bytes per C element
     const int wrows = min(64, rows_left), wcols = min(64, cols_left);
-    uint16_t* cw = g.C + (size_t)(tc.m * Cfg::kBM + wm * 64) * g.ldc +
-                   tc.n * Cfg::kBN + wn * 64;
+    uint8_t* cw = reinterpret_cast<uint8_t*>(g.C) +
+                  ((size_t)(tc.m * Cfg::kBM + wm * 64) * g.ldc + tc.n * Cfg::kBN +
+                   wn * 64) * es;
     const bool any = wrows > 0 && wcols > 0;
     const __amdgpu_buffer_rsrc_t rsrc_c = make_rsrc(
-        cw, any ? (uint32_t)(((wrows - 1) * g.ldc + wcols) * 2) : 0u);
-    if constexpr (kVec) {
+        cw, any ? (uint32_t)(((wrows - 1) * g.ldc + wcols) * es) : 0u);
+    if constexpr (kExt && kOut >= kOutF32) {
+      // fp32 / e4m3 output: straight from the accumulators (4 consecutive
+      // elements per lane and block: one 16- or 4-byte store, or one per
+      // element when kVec is false).
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 16 * i + er16, col = 16 * j + 4 * egrp;
+          const uint32_t off = (uint32_t)((r * g.ldc + col) * es) |
+                               oob_unless(r, rows_left);
+          const f32x4& a = acc[i][j];
+          const f32x4 v = ev.template value4<kAct>(a[0], a[1], a[2], a[3], i, j);
+          if constexpr (kOut == kOutF32) {
+            if constexpr (kVec) {
+              __builtin_amdgcn_raw_buffer_store_b128(
+                  __builtin_bit_cast(i32x4, v), rsrc_c,
+                  off | oob_unless(col, cols_left), 0, kStoreC);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                __builtin_amdgcn_raw_buffer_store_b32(
+                    (uint32_t)__builtin_bit_cast(i32x4, v)[e], rsrc_c,
+                    (off | oob_unless(col + e, cols_left)) + 4 * e, 0, kStoreC);
+            }
+          } else {
+            const uint32_t w = ev.e4m3x4(v);
+            if constexpr (kVec) {
+              __builtin_amdgcn_raw_buffer_store_b32(
+                  w, rsrc_c, off | oob_unless(col, cols_left), 0, kStoreC);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                __builtin_amdgcn_raw_buffer_store_b8(
+                    (uint8_t)(w >> (8 * e)), rsrc_c,
+                    (off | oob_unless(col + e, cols_left)) + e, 0, kStoreC);
+            }
+          }
+        }
+    } else if constexpr (kVec) {
       // Stage: 8-byte piece p (columns 4p .. 4p + 3) of row r at slot
       // p ^ (r % 16) of the row's 128 bytes.
 #pragma unroll
@@ -384,8 +427,9 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
 // activation and output type chosen at run time) and the C stores.  One
 // wave per workgroup: quadrant blockIdx % 4 of tile blockIdx / 4, so
 // 4 x tiles workgroups.  Launched right after the split kernel on the same
-// stream, which makes its partials visible.  kVec8: 8-byte C stores (N and
-// ldc multiples of 4, C 8-byte aligned), else 2-byte ones.
+// stream, which makes its partials visible.  kVec8: one store per lane and
+// block (N and ldc multiples of 4, C aligned to four elements), else one per
+// element.
 template <bool kVec8, bool kExt>
 __device__ __forceinline__ void gemm_t128_reduce_body(const GemmArgs& g) {
   using Cfg = CfgT128;
@@ -421,20 +465,23 @@ __device__ __forceinline__ void gemm_t128_reduce_body(const GemmArgs& g) {
   auto oob_unless = [](int x, int limit) -> uint32_t {
     return (uint32_t)((limit - 1 - x) >> 31) & kOobOffset;
   };
+  const int es = kExt ? out_bytes(ev.out) : 2;  // bytes per C element
   const int wrows = min(64, rows_left), wcols = min(64, cols_left);
   const __amdgpu_buffer_rsrc_t rc = make_rsrc(
-      g.C + (size_t)row0 * g.ldc + col0,
-      wrows > 0 && wcols > 0 ? (uint32_t)(((wrows - 1) * g.ldc + wcols) * 2) : 0u);
+      reinterpret_cast<uint8_t*>(g.C) + ((size_t)row0 * g.ldc + col0) * es,
+      wrows > 0 && wcols > 0 ? (uint32_t)(((wrows - 1) * g.ldc + wcols) * es) : 0u);
   const int r16 = lane & 15, grp = lane >> 4;
 #pragma unroll
   for (int n = 0; n < 16; ++n) {
     const int i = n / 4, j = n % 4;
     const f32x4 a = sum[n];
-    const u32x2 pk = kExt ? ev.pack4(a[0], a[1], a[2], a[3], i, j)
-                          : u32x2{pack_bf16x2(a[0] * s, a[1] * s),
-                                  pack_bf16x2(a[2] * s, a[3] * s)};
     const int r = 16 * i + r16, col = 16 * j + 4 * grp;
-    const uint32_t rb = (uint32_t)((r * g.ldc + col) * 2) | oob_unless(r, rows_left);
+    const uint32_t rb = (uint32_t)((r * g.ldc + col) * es) | oob_unless(r, rows_left);
+    if constexpr (kExt) {
+      store_out4<kVec8>(ev, a[0], a[1], a[2], a[3], i, j, rc, rb, col, cols_left);
+      continue;
+    }
+    const u32x2 pk = u32x2{pack_bf16x2(a[0] * s, a[1] * s), pack_bf16x2(a[2] * s, a[3] * s)};
     if constexpr (kVec8) {
       __builtin_amdgcn_raw_buffer_store_b64(pk, rc, rb | oob_unless(col, cols_left),
                                             0, 0);

@@ -333,6 +333,7 @@ typedef struct {
   float s;                        /* scale_a * scale_b                     */
   const float *sr, *sc, *bias;    /* NULL: ones / ones / -0.0              */
   int act, out;
+  float so;                       /* e4m3 output scale                     */
 } epi_t;
 
 /* The activations from their definitions, in double (the reference for the
@@ -352,13 +353,21 @@ static float act_f(float v, int act) {
   }
 }
 
-static uint16_t epi_value(float acc, int m, int n, const epi_t *e) {
+/* Element o of the output array (of e->out's type) for accumulator acc at
+ * (m, n). */
+static void epi_store(void *out, size_t o, float acc, int m, int n,
+                      const epi_t *e) {
   const float sr = e->sr ? e->sr[m] : 1.0f;
   const float sc = e->sc ? e->sc[n] : 1.0f;
   const float scale = sr * (sc * e->s);
   const float v = fmaf(acc, scale, e->bias ? e->bias[n] : -0.0f);
   const float y = act_f(v, e->act);
-  return e->out == HG_OUT_F16 ? hg_f32_to_f16(y) : hg_f32_to_bf16(y);
+  switch (e->out) {
+    case HG_OUT_F16: ((uint16_t *)out)[o] = hg_f32_to_f16(y); break;
+    case HG_OUT_F32: ((float *)out)[o] = y; break;
+    case HG_OUT_FP8: ((uint8_t *)out)[o] = hg_f32_to_e4m3(y * e->so); break;
+    default: ((uint16_t *)out)[o] = hg_f32_to_bf16(y); break;
+  }
 }
 
 /* mode 0: bf16 of acc * s, or, with sa / sb given (row / column scale
@@ -381,7 +390,7 @@ static void rows_impl_lut(const uint8_t *A, const float *lut_a,
         for (int j = 0; j < nc; ++j) {
           const size_t o = (size_t)(r0 + r) * ldo + n0 + j;
           if (mode == 2) {
-            ((uint16_t *)out)[o] = epi_value(acc[r][j], rows[r0 + r], n0 + j, ep);
+            epi_store(out, o, acc[r][j], rows[r0 + r], n0 + j, ep);
           } else if (mode == 0 && (sa || sb)) {
             const float rs = sa ? sa[rows[r0 + r]] : 1.0f;
             const float cs = sb ? sb[n0 + j] : 1.0f;
@@ -403,16 +412,17 @@ static void rows_impl(const uint8_t *A, const float *Bt, const int *rows,
                 mode, s, sa, sb, NULL);
 }
 
-void hg_gemm_ex(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
+void hg_gemm_ex(const uint8_t *A, const uint8_t *B_T, void *C, int M,
                 int N, int K, int lda, int ldb, int ldc, int a_fmt, int b_fmt,
                 int out, int act, float scale_a, float scale_b,
                 const float *scale_rows, const float *scale_cols,
-                const float *bias) {
+                const float *bias, float scale_out) {
   float *Bt = decode_bt_fmt(B_T, N, K, ldb, b_fmt);
   int *rows = (int *)malloc((size_t)(M > 0 ? M : 1) * sizeof(int));
   if (!Bt || !rows) abort();
   for (int i = 0; i < M; ++i) rows[i] = i;
-  const epi_t ep = {scale_a * scale_b, scale_rows, scale_cols, bias, act, out};
+  const epi_t ep = {scale_a * scale_b, scale_rows, scale_cols, bias, act, out,
+                    scale_out};
   rows_impl_lut(A, lut_of(a_fmt), Bt, rows, M, N, K, lda, C, ldc, 2, 1.0f, NULL,
                 NULL, &ep);
   free(rows);

@@ -112,7 +112,7 @@ void hg_gemm_rows_f64(const uint8_t *A, const uint8_t *B_T, double *acc_rows,
 
 /* ---- Extensions beyond the reference: other formats, fused epilogue ----- */
 enum { HG_FMT_E4M3 = 0, HG_FMT_E5M2 = 1 };
-enum { HG_OUT_BF16 = 0, HG_OUT_F16 = 1 };
+enum { HG_OUT_BF16 = 0, HG_OUT_F16 = 1, HG_OUT_F32 = 2, HG_OUT_FP8 = 3 };
 enum { HG_ACT_NONE = 0, HG_ACT_RELU = 1, HG_ACT_GELU_TANH = 2, HG_ACT_SILU = 3 };
 /* OCP E5M2 decode (exact) and RNE encode (overflow to inf, NaN -> NaN),
  * IEEE binary16 RNE encode.  Pinned: e5m2 decode against its closed form
@@ -130,17 +130,20 @@ void hg_f32_to_f16_n(const float *x, uint16_t *out, size_t n);
  * 8-bit values are exact in fp32 for every pair of these formats), then
  *   scale = scale_rows[m] * (scale_cols[n] * (scale_a * scale_b))
  *   v = fmaf(acc, scale, bias[n])   (bias NULL: -0.0)
- *   C = out(act(v))                 (bf16 or f16 bits, RNE)
+ *   y = act(v)
+ *   C = bf16 / f16 bits of y (RNE), y itself (fp32), or
+ *       hg_f32_to_e4m3(y * scale_out) (e4m3 output)
+ * C has row stride ldc elements of the output type (2, 2, 4 or 1 bytes).
  * with the activation evaluated in double from its definition.  Pinned:
  * the defaults equal hg_gemm_fast and vectors alone equal hg_gemm_rowcol
  * bit for bit; e5m2 operands against fp64 sums of the decoded values;
  * bias against an fp64 fma; activations against scipy's expit and torch's
  * tanh-approximated gelu; f16 output against numpy. */
-void hg_gemm_ex(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
+void hg_gemm_ex(const uint8_t *A, const uint8_t *B_T, void *C, int M,
                 int N, int K, int lda, int ldb, int ldc, int a_fmt, int b_fmt,
                 int out, int act, float scale_a, float scale_b,
                 const float *scale_rows, const float *scale_cols,
-                const float *bias);
+                const float *bias, float scale_out);
 
 /* MX block scales (OCP Microscaling v1.0): sa is M x ceil(K/32) E8M0 bytes
  * (row stride ldsa), sb N x ceil(K/32) (ldsb); element k of a row is scaled

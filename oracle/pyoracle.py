@@ -25,7 +25,7 @@ UNIFORM = 0
 NORMAL = 1
 # hg_gemm_ex codes (oracle.h; the values of include/hipgemm.h's)
 FMT_E4M3, FMT_E5M2 = 0, 1
-OUT_BF16, OUT_F16 = 0, 1
+OUT_BF16, OUT_F16, OUT_F32, OUT_FP8 = 0, 1, 2, 3
 ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3
 
 _c_u8p = ctypes.POINTER(ctypes.c_uint8)
@@ -81,7 +81,7 @@ class Oracle:
             [_vp, _vp]
         L.hg_gemm_rowcol.restype = None
         L.hg_gemm_ex.argtypes = [_vp, _vp, _vp] + [ctypes.c_int] * 10 + \
-            [ctypes.c_float] * 2 + [_vp, _vp, _vp]
+            [ctypes.c_float] * 2 + [_vp, _vp, _vp, ctypes.c_float]
         L.hg_gemm_ex.restype = None
         L.hg_gemm_mx.argtypes = [_vp, _vp, _vp] + [ctypes.c_int] * 8 + \
             [_vp, ctypes.c_int, _vp, ctypes.c_int] + [ctypes.c_float] * 2
@@ -201,9 +201,10 @@ class Oracle:
                 scale_a: float = 1.0, scale_b: float = 1.0,
                 scale_rows: Optional[np.ndarray] = None,
                 scale_cols: Optional[np.ndarray] = None,
-                bias: Optional[np.ndarray] = None) -> np.ndarray:
-        """Output bits (bf16 or f16) of the hipgemm_gemm semantics
-        (oracle.h: hg_gemm_ex)."""
+                bias: Optional[np.ndarray] = None,
+                scale_out: float = 1.0) -> np.ndarray:
+        """Output bits of the hipgemm_gemm semantics (oracle.h: hg_gemm_ex):
+        uint16 (bf16 / f16), uint32 (fp32 bits) or uint8 (e4m3)."""
         A = np.ascontiguousarray(A)
         B = np.ascontiguousarray(B)
         M, K = A.shape
@@ -217,12 +218,12 @@ class Oracle:
             assert v.shape == (n,)
             return v
         sr, sc, bb = vec(scale_rows, M), vec(scale_cols, N), vec(bias, N)
-        C = np.empty((M, N), np.uint16)
+        C = np.empty((M, N), {OUT_F32: np.uint32, OUT_FP8: np.uint8}.get(out, np.uint16))
         self.lib.hg_gemm_ex(_ptr(A), _ptr(B), _ptr(C), M, N, K, K, K, N,
                             a_fmt, b_fmt, out, act, scale_a, scale_b,
                             None if sr is None else _ptr(sr),
                             None if sc is None else _ptr(sc),
-                            None if bb is None else _ptr(bb))
+                            None if bb is None else _ptr(bb), scale_out)
         return C
 
     def gemm_mx(self, A: np.ndarray, B: np.ndarray, sa: np.ndarray,

@@ -171,14 +171,25 @@ def test_gemm_desc_entry_validation():
     bad_size.size -= 8
     assert hg.gemm_desc_raw(bad_size) == INVALID
     assert hg.lib().hipgemm_gemm(None, None) == INVALID
-    for bad in (dict(a_format=2), dict(b_format=-1), dict(out_dtype=2),
-                dict(activation=4), dict(scale_rows=FAKE + 2),
+    for bad in (dict(a_format=2), dict(b_format=-1), dict(out_dtype=4),
+                dict(out_dtype=-1), dict(activation=4), dict(scale_rows=FAKE + 2),
+                # fp32 / e4m3 output: element alignment, no 8-wave schedule,
+                # the output scale only with e4m3 output, 4-byte aligned
+                dict(out_dtype=2, C=FAKE + 2), dict(out_dtype=2, variant=4),
+                dict(out_dtype=3, variant=4), dict(scale_out=FAKE),
+                dict(out_dtype=2, scale_out=FAKE),
+                dict(out_dtype=3, scale_out=FAKE + 2),
+                # ldc * element size <= 2^23 bytes
+                dict(out_dtype=2, ldc=(1 << 21) + 1),
                 dict(scale_cols=FAKE + 1), dict(bias=FAKE + 3),
                 dict(variant=1, a_format=1), dict(variant=1, bias=FAKE),
                 dict(variant=1, out_dtype=1), dict(variant=1, activation=1),
                 dict(variant=3),  # M = 300 > 128
                 dict(K=40, lda=48, ldb=48), dict(variant=9)):
         assert hg.gemm_desc_raw(hg.GemmDesc(**dict(base, **bad))) == INVALID, bad
+    # e4m3 output: any byte address; the empty problem is a no-op
+    assert hg.gemm_desc_raw(hg.GemmDesc(**dict(base, M=0, out_dtype=3,
+                                               C=FAKE + 1))) == 0
 
 
 def test_mx_entry_validation():

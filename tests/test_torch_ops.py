@@ -65,6 +65,11 @@ def test_general_op_fake_shapes():
             torch.ops.hipgemm.gemm(a, b, bias=torch.empty(95))
         with pytest.raises(hg.HipGemmError):
             torch.ops.hipgemm.gemm(a, b, activation="tanh")
+        for dt in (torch.float32, torch.float8_e4m3fn, torch.bfloat16):
+            y = torch.ops.hipgemm.gemm(a, b, out_dtype=dt)
+            assert y.dtype == dt and tuple(y.shape) == (64, 96)
+        with pytest.raises(hg.HipGemmError):
+            torch.ops.hipgemm.gemm(a, b, out_dtype=torch.float64)
 
 
 def test_cpu_tensors_fail_loudly():
@@ -193,6 +198,15 @@ def test_general_op_equals_abi(gpu, oracle):
     torch_.cuda.synchronize()
     assert y.dtype == torch_.float16
     assert torch_.equal(y.view(torch_.int16), ref.view(torch_.int16))
+    so = torch_.tensor([0.125], device="cuda")
+    for dt in (torch_.float32, torch_.float8_e4m3fn):
+        kw = dict(scale_out=so) if dt == torch_.float8_e4m3fn else {}
+        y = torch_.ops.hipgemm.gemm(a5, b, bias=bias, activation="relu",
+                                    out_dtype=dt, **kw)
+        ref = hg.gemm(a5, b, bias=bias, activation="relu", out_dtype=dt, **kw)
+        torch_.cuda.synchronize()
+        assert y.dtype == dt
+        assert torch_.equal(y.view(torch_.uint8), ref.view(torch_.uint8))
 
 
 @pytest.mark.gpu
