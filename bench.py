@@ -178,6 +178,9 @@ def main():
         raise SystemExit(f"unknown variant {args.variant}")
     vname = hg.variant_name(hg.select_variant(M, N, K) if variant == 0
                             else variant)
+    n1 = hg.split_columns(M, N, K) if variant == 0 else 0
+    if n1:  # AUTO's column split: two schedules, two launches per step
+        vname = f"{vname}[0:{n1}]+{hg.variant_name(5)}[{n1}:{N}]"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     hg.lib()
