@@ -31,7 +31,7 @@ __all__ = [
     "variant_name", "version", "tile_order", "lds_slot", "VARIANTS",
     "declared_symbols", "gemm_raw_ws", "workspace_size",
     "fp8_gemm_bf16_rowcol", "gemm_raw_rowcol", "GemmDesc", "gemm_desc_raw",
-    "gemm", "FMT_E4M3", "FMT_E5M2", "OUT_BF16", "OUT_F16", "OUT_F32",
+    "gemm", "FMT_E4M3", "FMT_E5M2", "FMT_FP4_E2M1", "OUT_BF16", "OUT_F16", "OUT_F32",
     "OUT_FP8_E4M3", "ACTIVATIONS",
     "mx_scales_bytes", "mx_pack_scales",
 ]
@@ -45,7 +45,7 @@ VARIANTS = {"auto": 0, "4wave": 1, "4wave_mfma16": 2, "skinny": 3, "8wave": 4,
             "tile128": 5}
 
 # include/hipgemm.h codes
-FMT_E4M3, FMT_E5M2 = 0, 1
+FMT_E4M3, FMT_E5M2, FMT_FP4_E2M1 = 0, 1, 4
 OUT_BF16, OUT_F16, OUT_F32, OUT_FP8_E4M3 = 0, 1, 2, 3
 ACTIVATIONS = {None: 0, "none": 0, "relu": 1, "gelu_tanh": 2, "silu": 3}
 
@@ -140,6 +140,8 @@ def lib() -> ctypes.CDLL:
     L.hipgemm_select_variant.restype = ci
     L.hipgemm_split_columns.argtypes = [ci, ci, ci]
     L.hipgemm_split_columns.restype = ci
+    L.hipgemm_gemm_workspace_size.argtypes = [ctypes.c_void_p]
+    L.hipgemm_gemm_workspace_size.restype = ctypes.c_size_t
     L.hipgemm_variant_name.argtypes = [ci]
     L.hipgemm_variant_name.restype = ctypes.c_char_p
     L.hipgemm_version.argtypes = []
@@ -386,7 +388,8 @@ def gemm(a, b_t, *, a_format: int = FMT_E4M3, b_format: int = FMT_E4M3,
     round(act(fma(acc, scale_rows[m] * (scale_cols[n] * (scale_a *
     scale_b)), bias[n]))), acc = a @ b_t.T with a in a_format and b_t in
     b_format (FMT_E4M3 / FMT_E5M2; float8_e4m3fn / float8_e5m2 tensors set
-    it from their dtype).  out_dtype: torch.bfloat16 (default),
+    it from their dtype; FMT_FP4_E2M1 for both, or float4_e2m1fn_x2
+    tensors: K / 2 bytes per row, element 2i in the low nibble).  out_dtype: torch.bfloat16 (default),
     torch.float16, torch.float32 or torch.float8_e4m3fn (saturating; then
     scale_out, a 1-element float32 device tensor, multiplies the activated
     value before the conversion).  activation: None, "relu", "gelu_tanh" or
@@ -396,9 +399,14 @@ def gemm(a, b_t, *, a_format: int = FMT_E4M3, b_format: int = FMT_E4M3,
     mx_scale_a / mx_scale_b: MX block scales packed by mx_pack_scales
     (both or neither)."""
     torch = _torch()
-    fmts = {torch.float8_e4m3fn: FMT_E4M3, torch.float8_e5m2: FMT_E5M2}
+    fmts = {torch.float8_e4m3fn: FMT_E4M3, torch.float8_e5m2: FMT_E5M2,
+            torch.float4_e2m1fn_x2: FMT_FP4_E2M1}
     a_format = fmts.get(a.dtype, a_format)
     b_format = fmts.get(b_t.dtype, b_format)
+    if a.dtype == torch.float4_e2m1fn_x2:
+        a = a.view(torch.uint8)
+    if b_t.dtype == torch.float4_e2m1fn_x2:
+        b_t = b_t.view(torch.uint8)
     out_dtype = out_dtype or (out.dtype if out is not None else torch.bfloat16)
     codes = {torch.bfloat16: OUT_BF16, torch.float16: OUT_F16,
              torch.float32: OUT_F32, torch.float8_e4m3fn: OUT_FP8_E4M3}
@@ -414,6 +422,8 @@ def gemm(a, b_t, *, a_format: int = FMT_E4M3, b_format: int = FMT_E4M3,
         a.view(torch.uint8) if a.dtype == torch.float8_e5m2 else a,
         b_t.view(torch.uint8) if b_t.dtype == torch.float8_e5m2 else b_t,
         out, variant, stream, out_dtype)
+    if a_format == FMT_FP4_E2M1 or b_format == FMT_FP4_E2M1:
+        K *= 2  # elements: two per byte
     d = GemmDesc(A=a.data_ptr(), B_T=b_t.data_ptr(), C=out.data_ptr(), M=M,
                  N=N, K=K, lda=lda, ldb=ldb, ldc=ldc, a_format=a_format,
                  b_format=b_format,
@@ -428,6 +438,11 @@ def gemm(a, b_t, *, a_format: int = FMT_E4M3, b_format: int = FMT_E4M3,
                  mx_scale_a=_mx_ptr(mx_scale_a, M, K, "mx_scale_a"),
                  mx_scale_b=_mx_ptr(mx_scale_b, N, K, "mx_scale_b"),
                  scale_out=_scale_ptr(scale_out, "scale_out"))
+    need = int(lib().hipgemm_gemm_workspace_size(ctypes.byref(d)))
+    if need != nbytes:  # the formats decide the schedule (fp4: 128 x 128)
+        w = _workspace(a.device, stream, need) if need else None
+        d.workspace = w.data_ptr() if w is not None else None
+        d.workspace_bytes = need
     _check(gemm_desc_raw(d, stream.cuda_stream), "hipgemm_gemm")
     return out
 

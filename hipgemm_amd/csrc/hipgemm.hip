@@ -279,6 +279,16 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
                     hipStream_t stream) {
   int M = d.M, N = d.N, K = d.K, lda = d.lda, ldb = d.ldb, variant = d.variant;
   if (!valid_code(d.out_dtype, 4)) return hipErrorInvalidValue;
+  // fp4 operands: both, K a multiple of 32 elements, the 128 x 128
+  // schedule; from here on K counts bytes of a row (K / 2).
+  const bool fp4 = d.a_format == HIPGEMM_FMT_FP4_E2M1 ||
+                   d.b_format == HIPGEMM_FMT_FP4_E2M1;
+  if (fp4) {
+    if (d.a_format != d.b_format || K % 32 != 0 || d.mx_scale_a || d.mx_scale_b ||
+        (variant != HIPGEMM_VARIANT_AUTO && variant != HIPGEMM_VARIANT_TILE128))
+      return hipErrorInvalidValue;
+    K /= 2;
+  }
   const int es = out_bytes(d.out_dtype);
   hipError_t e = validate(d.A, d.B_T, d.C, M, N, K, lda, ldb, d.ldc, variant, es);
   if (e != hipSuccess) return e;
@@ -288,7 +298,7 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   const size_t ws_bytes = d.workspace_bytes;
   if (ws_given && ws_bytes > 0 && (!ws || !aligned(ws, 256)))
     return hipErrorInvalidValue;
-  if (!valid_code(d.a_format, 2) || !valid_code(d.b_format, 2) ||
+  if ((!fp4 && (!valid_code(d.a_format, 2) || !valid_code(d.b_format, 2))) ||
       !valid_code(d.activation, 4))
     return hipErrorInvalidValue;
   // The output scale belongs to the e4m3 output; fp32 / e4m3 outputs are not
@@ -304,7 +314,7 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   const bool ext = d.scale_rows || d.scale_cols || d.bias ||
                    d.activation != HIPGEMM_ACT_NONE ||
                    d.out_dtype != HIPGEMM_OUT_BF16;
-  const int fmt = d.a_format | (d.b_format << 1);
+  const int fmt = fp4 ? kFmtPairFp4 : d.a_format | (d.b_format << 1);
   // The 32x32x64 schedule is built for e4m3 x e4m3 with the per-tensor
   // epilogue only.
   if (variant == HIPGEMM_VARIANT_4WAVE && (ext || fmt != 0))
@@ -316,10 +326,12 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
              (variant != HIPGEMM_VARIANT_AUTO &&
               variant != HIPGEMM_VARIANT_4WAVE_MFMA16)))
     return hipErrorInvalidValue;
-  const int n1 = (variant == HIPGEMM_VARIANT_AUTO && !mx && K > 0)
+  const int n1 = (variant == HIPGEMM_VARIANT_AUTO && !mx && !fp4 && K > 0)
                      ? split_columns(M, N, cu_count())
                      : 0;
-  variant = mx ? HIPGEMM_VARIANT_4WAVE_MFMA16 : resolve_variant(variant, M, N, K);
+  variant = mx    ? HIPGEMM_VARIANT_4WAVE_MFMA16
+            : fp4 ? HIPGEMM_VARIANT_TILE128
+                  : resolve_variant(variant, M, N, K);
   if (variant == HIPGEMM_VARIANT_8WAVE && d.out_dtype >= HIPGEMM_OUT_F32)
     variant = HIPGEMM_VARIANT_4WAVE_MFMA16;  // AUTO's 8-wave choice
   if (K == 0) lda = ldb = 16;  // nothing is read; keep the offset math inert
@@ -519,6 +531,17 @@ hipError_t hipgemm_mx_pack_scales(const void* src, int rows, int K, int ld,
   if (!src || !dst || ld < K / 32) return hipErrorInvalidValue;
   return hk::mx_pack(static_cast<const uint8_t*>(src), rows, K, ld,
                      static_cast<uint8_t*>(dst), stream);
+}
+
+size_t hipgemm_gemm_workspace_size(const hipgemm_gemm_desc* d) {
+  if (!d || d->size != sizeof(hipgemm_gemm_desc) || d->M <= 0 || d->N <= 0 ||
+      d->K <= 0)
+    return 0;
+  const bool fp4 = d->a_format == HIPGEMM_FMT_FP4_E2M1 ||
+                   d->b_format == HIPGEMM_FMT_FP4_E2M1;
+  if (d->mx_scale_a || d->mx_scale_b) return 0;  // the 4-wave schedule
+  if (fp4) return plan_t128(d->M, d->N, d->K / 2, cu_count()).ws_bytes;
+  return hipgemm_workspace_size(d->M, d->N, d->K, d->variant);
 }
 
 size_t hipgemm_workspace_size(int M, int N, int K, int variant) {

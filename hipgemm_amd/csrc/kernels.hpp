@@ -39,7 +39,11 @@ const void* skinny_ext(int kmb, const Key& k);      // kskinny_ext.hip
 const void* skinny_reduce(int kf, const Key& k);    // kskinny_plain.hip
 const void* four_wave_mx(const Key& k);             // k4wave_mx.hip
 const void* tile128_plain(const Key& k);            // kt128_plain.hip
-const void* tile128_ext(const Key& k);              // kt128_ext.hip
+const void* tile128_ext_narrow(const Key& k);       // kt128_ext.hip
+const void* tile128_ext_wide(const Key& k);         // kt128_ext_wide.hip
+inline const void* tile128_ext(const Key& k) {
+  return k.out >= detail::kOutF32 ? tile128_ext_wide(k) : tile128_ext_narrow(k);
+}
 const void* tile128_split(const Key& k);            // kt128_plain.hip
 const void* tile128_reduce(const Key& k);           // kt128_plain.hip
 // Packs [rows][ceil(K/32)] E8M0 scales (row stride ld) into MxArgs' layout.
@@ -52,6 +56,18 @@ using ic = std::integral_constant<int, I>;
 template <class F>
 const void* sel2(int v, F&& f) {
   return v ? f(ic<1>{}) : f(ic<0>{});
+}
+// Operand-format pairs: the four 8-bit pairs and fp4 x fp4 (kFmtPairFp4).
+template <class F>
+const void* sel_fmt(int v, F&& f) {
+  switch (v) {
+    case 0: return f(ic<0>{});
+    case 1: return f(ic<1>{});
+    case 2: return f(ic<2>{});
+    case 3: return f(ic<3>{});
+    case 4: return f(ic<4>{});
+    default: return nullptr;
+  }
 }
 template <class F>
 const void* sel4(int v, F&& f) {

@@ -1,5 +1,6 @@
-// The 128 x 128-tile schedule with the extended epilogue, for every
-// operand-format pair, activation and output type (bf16, fp16, fp32, e4m3).
+// The 128 x 128-tile schedule with the extended epilogue and a 2-byte output
+// (bf16, fp16), for every operand-format pair (fp4 x fp4 included) and
+// activation.
 #include "kernels.hpp"
 
 namespace hipgemm {
@@ -16,10 +17,10 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm_t128_ext(GemmArgs g) {
 
 }  // namespace
 
-const void* tile128_ext(const Key& k) {
-  return sel4(k.fmt, [&](auto F) {
+const void* tile128_ext_narrow(const Key& k) {
+  return sel_fmt(k.fmt, [&](auto F) {
     return sel4(k.act, [&](auto A) {
-      return sel4(k.out, [&](auto O) {
+      return sel2(k.out, [&](auto O) {
         return sel2(k.vec, [&](auto V) {
           return (const void*)&k_fp8_gemm_t128_ext<
               decltype(V)::value == 1, decltype(F)::value, decltype(A)::value,

@@ -1,0 +1,35 @@
+// The 128 x 128-tile schedule with the extended epilogue and fp32 or e4m3
+// output, for every operand-format pair (fp4 x fp4 included) and activation.
+#include "kernels.hpp"
+
+namespace hipgemm {
+namespace kernels {
+namespace {
+
+using namespace detail;
+
+template <bool kVec, int kFmt, int kAct, int kOut>
+__global__ __launch_bounds__(256, 1) void k_fp8_gemm_t128_ext_wide(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[CfgT128::kLdsBytes];
+  gemm_t128_body<kVec, true, kFmt, kAct, kOut>(g, (lds_u8*)lds);
+}
+
+}  // namespace
+
+const void* tile128_ext_wide(const Key& k) {
+  if (k.out != kOutF32 && k.out != kOutF8) return nullptr;
+  return sel_fmt(k.fmt, [&](auto F) {
+    return sel4(k.act, [&](auto A) {
+      return sel2(k.vec, [&](auto V) {
+        if (k.out == kOutF32)
+          return (const void*)&k_fp8_gemm_t128_ext_wide<
+              decltype(V)::value == 1, decltype(F)::value, decltype(A)::value, kOutF32>;
+        return (const void*)&k_fp8_gemm_t128_ext_wide<
+            decltype(V)::value == 1, decltype(F)::value, decltype(A)::value, kOutF8>;
+      });
+    });
+  });
+}
+
+}  // namespace kernels
+}  // namespace hipgemm

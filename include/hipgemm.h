@@ -78,13 +78,18 @@ enum {
   HIPGEMM_VARIANT_COUNT = 6
 };
 
-/* 8-bit operand formats (OCP 8-bit floating point, v1.0). */
+/* Operand formats (OCP 8-bit floating point v1.0; OCP Microscaling v1.0
+ * for E2M1).  FP4_E2M1: 1 sign, 2 exponent (bias 1), 1 mantissa bit --
+ * 0, 0.5, 1, 1.5, 2, 3, 4, 6 and their negatives -- two per byte, element
+ * 2i in the low nibble of byte i of a row; A and B_T both FP4_E2M1 (not
+ * mixed with the 8-bit formats), K (in elements) a multiple of 32, lda /
+ * ldb in bytes (>= K / 2), schedules AUTO and TILE128. */
 enum {
-  HIPGEMM_FMT_E4M3 = 0, /* E4M3FN: bias 7, max 448, NaN 0x7F/0xFF, no inf */
-  HIPGEMM_FMT_E5M2 = 1  /* E5M2: bias 15, max 57344, IEEE inf and NaN     */
+  HIPGEMM_FMT_E4M3 = 0,    /* E4M3FN: bias 7, max 448, NaN 0x7F/0xFF, no inf */
+  HIPGEMM_FMT_E5M2 = 1,    /* E5M2: bias 15, max 57344, IEEE inf and NaN     */
+  HIPGEMM_FMT_FP4_E2M1 = 4 /* E2M1: max 6, no inf or NaN                      */
 };
 
-/* Output element types (RNE from the fp32 result). */
 /* Output types of hipgemm_gemm.  BF16, F16: round to nearest even; F32: the
  * fp32 value itself; FP8_E4M3: OCP e4m3 of activation(v) * scale_out, round
  * to nearest even, finite magnitudes above 448 saturate to 448, Inf and NaN
@@ -247,6 +252,12 @@ hipError_t hipgemm_mx_pack_scales(const void *src, int rows, int K, int ld,
 /* Workspace bytes hipgemm_fp8_gemm_bf16_ws needs for this shape and variant
  * on the current device (0: none).  No GPU work.  No reference counterpart. */
 size_t hipgemm_workspace_size(int M, int N, int K, int variant);
+
+/* Workspace bytes hipgemm_gemm needs for this descriptor on the current
+ * device (0: none, or an invalid descriptor); it accounts for the operand
+ * formats (fp4 runs the 128 x 128 schedule).  No GPU work.  No reference
+ * counterpart. */
+size_t hipgemm_gemm_workspace_size(const hipgemm_gemm_desc *desc);
 
 /*
  * The reference launch with runtime shapes: packed strides (lda = ldb = K,

@@ -95,13 +95,17 @@ __device__ __forceinline__ i32x8 join(i32x4 lo, i32x4 hi) {
   return i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 }
 
-// 8-bit operand formats of the f8f6f4 MFMA family (its cbsz / blgp
-// immediates): OCP E4M3 (fp8) and OCP E5M2 (bf8).
-constexpr int kFmtE4M3 = 0, kFmtE5M2 = 1;
-// A kernel's operand-format pair kFmt: bit 0 the format of A, bit 1 that of
-// B_T.  0 = e4m3 x e4m3.
-__host__ __device__ constexpr int fmt_a(int f) { return f & 1; }
-__host__ __device__ constexpr int fmt_b(int f) { return (f >> 1) & 1; }
+// Operand formats of the f8f6f4 MFMA family (its cbsz / blgp immediates):
+// OCP E4M3 (fp8), OCP E5M2 (bf8) and OCP E2M1 (fp4, two per byte).
+constexpr int kFmtE4M3 = 0, kFmtE5M2 = 1, kFmtFp4 = 4;
+// A kernel's operand-format pair kFmt: 0-3, bit 0 the 8-bit format of A,
+// bit 1 that of B_T (0 = e4m3 x e4m3); kFmtPairFp4, fp4 x fp4.
+constexpr int kFmtPairFp4 = 4;
+__host__ __device__ constexpr bool is_fp4(int f) { return f == kFmtPairFp4; }
+__host__ __device__ constexpr int fmt_a(int f) { return is_fp4(f) ? kFmtFp4 : f & 1; }
+__host__ __device__ constexpr int fmt_b(int f) {
+  return is_fp4(f) ? kFmtFp4 : (f >> 1) & 1;
+}
 
 // D[32x32] += X[32x64] . Y[32x64]^T -> fp32, X in format kFx, Y in kFy.
 // Lane l carries row l%32 of X (and of Y) and 32 of its 64 K-bytes.

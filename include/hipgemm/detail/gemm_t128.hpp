@@ -202,15 +202,27 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
 #pragma unroll
     for (int n = 0; n < 16; ++n) {
       const int i = n / 4, j = n % 4;
-      acc[i][j] = mfma_16x16x128<fmt_b(kFmt), fmt_a(kFmt)>(fb[set][j], fa[set][i],
-                                                           acc[i][j]);
+      if constexpr (is_fp4(kFmt)) {
+        // fp4: 256 elements per 128-byte step, two MFMA per block -- the
+        // fragments' low halves (K-chunk g) and high halves (chunk g + 4);
+        // the instruction reads four registers of each operand.
+        const i32x8& x = fb[set][j];
+        const i32x8& y = fa[set][i];
+        acc[i][j] = mfma_16x16x128<kFmtFp4, kFmtFp4>(x, y, acc[i][j]);
+        acc[i][j] = mfma_16x16x128<kFmtFp4, kFmtFp4>(
+            __builtin_shufflevector(x, x, 4, 5, 6, 7, 0, 1, 2, 3),
+            __builtin_shufflevector(y, y, 4, 5, 6, 7, 0, 1, 2, 3), acc[i][j]);
+      } else {
+        acc[i][j] = mfma_16x16x128<fmt_b(kFmt), fmt_a(kFmt)>(fb[set][j], fa[set][i],
+                                                             acc[i][j]);
+      }
       // read n: fragment f (0: A0, 1-4: B0-B3, 5-7: A1-A3), half n % 2
       const int f = n / 2;
       const uint32_t o = f == 0   ? off_a
                          : f <= 4 ? off_b + (f - 1) * 16 * Cfg::kBK
                                   : off_a + (f - 4) * 16 * Cfg::kBK;
       rd[n] = lds_read16(rb + ((n & 1) ? (o ^ 64u) : o));
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, is_fp4(kFmt) ? 2 : 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       if (n < 8) {
         dma_one(d, dstage, n);

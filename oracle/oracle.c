@@ -235,6 +235,7 @@ float hg_draw_scale(uint64_t seed, double lo, double hi) {
 /* ------------------------------------------------------------------------ */
 static float g_e4m3_lut[256];
 static float g_e5m2_lut[256];
+static float g_fp4_lut[256];   /* indexed by a nibble value 0..15 */
 static int g_lut_ready = 0;
 
 static void lut_init(void) {
@@ -245,6 +246,7 @@ static void lut_init(void) {
       for (int i = 0; i < 256; ++i) {
         g_e4m3_lut[i] = hg_e4m3_to_f32((uint8_t)i);
         g_e5m2_lut[i] = hg_e5m2_to_f32((uint8_t)i);
+        g_fp4_lut[i] = hg_fp4_to_f32((uint8_t)(i & 15));
       }
       g_lut_ready = 1;
     }
@@ -253,7 +255,7 @@ static void lut_init(void) {
 
 static const float *lut_of(int fmt) {
   lut_init();
-  return fmt == HG_FMT_E5M2 ? g_e5m2_lut : g_e4m3_lut;
+  return fmt == HG_FMT_E5M2 ? g_e5m2_lut : fmt == HG_FMT_FP4 ? g_fp4_lut : g_e4m3_lut;
 }
 
 static inline uint16_t epilogue(float acc, float s) {
@@ -326,6 +328,28 @@ static void block_acc(const uint8_t *A, const float *lut_a, const float *Bt,
       }
     }
   }
+}
+
+/* OCP E2M1 (OCP Microscaling v1.0, FP4): 1 sign bit (3), 2 exponent bits
+ * (2:1, bias 1), 1 mantissa bit (0); exponent field 0 is subnormal (m/2).
+ * Values 0, 0.5, 1, 1.5, 2, 3, 4, 6.  No Inf or NaN. */
+float hg_fp4_to_f32(uint8_t v) {
+  const int e = (v >> 1) & 3, m = v & 1;
+  const float mag = e == 0 ? 0.5f * (float)m : ldexpf(1.0f + 0.5f * (float)m, e - 1);
+  return (v & 8) ? -mag : mag;
+}
+
+/* rows x K fp4 elements, two per byte (element 2i in the low nibble of byte
+ * i of a row, row stride ld bytes) -> rows x K bytes, one nibble each. */
+static uint8_t *unpack_fp4(const uint8_t *X, int rows, int K, int ld) {
+  uint8_t *u = (uint8_t *)malloc((size_t)(rows > 0 ? rows : 1) * (K > 0 ? K : 1));
+  if (!u) abort();
+  for (int r = 0; r < rows; ++r)
+    for (int k = 0; k < K; ++k) {
+      const uint8_t b = X[(size_t)r * ld + k / 2];
+      u[(size_t)r * K + k] = (k & 1) ? (uint8_t)(b >> 4) : (uint8_t)(b & 15);
+    }
+  return u;
 }
 
 /* The extended epilogue of hg_gemm_ex. */
@@ -417,6 +441,18 @@ void hg_gemm_ex(const uint8_t *A, const uint8_t *B_T, void *C, int M,
                 int out, int act, float scale_a, float scale_b,
                 const float *scale_rows, const float *scale_cols,
                 const float *bias, float scale_out) {
+  /* fp4: one byte per element (the nibble), then the same path. */
+  uint8_t *Au = NULL, *Bu = NULL;
+  if (a_fmt == HG_FMT_FP4) {
+    Au = unpack_fp4(A, M, K, lda);
+    A = Au;
+    lda = K;
+  }
+  if (b_fmt == HG_FMT_FP4) {
+    Bu = unpack_fp4(B_T, N, K, ldb);
+    B_T = Bu;
+    ldb = K;
+  }
   float *Bt = decode_bt_fmt(B_T, N, K, ldb, b_fmt);
   int *rows = (int *)malloc((size_t)(M > 0 ? M : 1) * sizeof(int));
   if (!Bt || !rows) abort();
@@ -427,6 +463,8 @@ void hg_gemm_ex(const uint8_t *A, const uint8_t *B_T, void *C, int M,
                 NULL, &ep);
   free(rows);
   free(Bt);
+  free(Au);
+  free(Bu);
 }
 
 /* ------------------------------------------------------------------------ */

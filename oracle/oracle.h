@@ -111,7 +111,12 @@ void hg_gemm_rows_f64(const uint8_t *A, const uint8_t *B_T, double *acc_rows,
                       int ldb);
 
 /* ---- Extensions beyond the reference: other formats, fused epilogue ----- */
-enum { HG_FMT_E4M3 = 0, HG_FMT_E5M2 = 1 };
+enum { HG_FMT_E4M3 = 0, HG_FMT_E5M2 = 1, HG_FMT_FP4 = 4 };
+/* OCP E2M1 (FP4) decode of the low nibble of v; hg_gemm_ex takes fp4
+ * operands (both) as two elements per byte, element 2i in the low nibble of
+ * byte i, lda / ldb in bytes.  Pinned: the decode against the OCP MX v1.0
+ * value table; the GEMM against fp64 sums of the decoded values. */
+float hg_fp4_to_f32(uint8_t v);
 enum { HG_OUT_BF16 = 0, HG_OUT_F16 = 1, HG_OUT_F32 = 2, HG_OUT_FP8 = 3 };
 enum { HG_ACT_NONE = 0, HG_ACT_RELU = 1, HG_ACT_GELU_TANH = 2, HG_ACT_SILU = 3 };
 /* OCP E5M2 decode (exact) and RNE encode (overflow to inf, NaN -> NaN),

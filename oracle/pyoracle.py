@@ -24,7 +24,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 UNIFORM = 0
 NORMAL = 1
 # hg_gemm_ex codes (oracle.h; the values of include/hipgemm.h's)
-FMT_E4M3, FMT_E5M2 = 0, 1
+FMT_E4M3, FMT_E5M2, FMT_FP4 = 0, 1, 4
 OUT_BF16, OUT_F16, OUT_F32, OUT_FP8 = 0, 1, 2, 3
 ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3
 
@@ -61,6 +61,8 @@ class Oracle:
                      "hg_f32_to_f16_n"):
             getattr(L, name).argtypes = [_vp, _vp, ctypes.c_size_t]
             getattr(L, name).restype = None
+        L.hg_fp4_to_f32.argtypes = [ctypes.c_uint8]
+        L.hg_fp4_to_f32.restype = ctypes.c_float
         L.hg_rand64.restype = ctypes.c_uint64
         L.hg_rand64.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
         L.hg_fill_e4m3.argtypes = [_vp, ctypes.c_size_t, ctypes.c_uint64,
@@ -137,6 +139,12 @@ class Oracle:
         self.lib.hg_f32_to_f16_n(_ptr(x), _ptr(out), x.size)
         return out
 
+    def fp4_to_f32(self, nibbles: np.ndarray) -> np.ndarray:
+        """OCP E2M1 values of nibble codes 0..15 (hg_fp4_to_f32)."""
+        return np.array([self.lib.hg_fp4_to_f32(int(v) & 15) for v in
+                         np.asarray(nibbles).reshape(-1)],
+                        np.float32).reshape(np.shape(nibbles))
+
     def decode(self, x: np.ndarray, fmt: int) -> np.ndarray:
         """fp32 values of 8-bit operands in format fmt (FMT_E4M3 / FMT_E5M2)."""
         return self.e5m2_to_f32(x) if fmt == FMT_E5M2 else self.e4m3_to_f32(x)
@@ -204,12 +212,16 @@ class Oracle:
                 bias: Optional[np.ndarray] = None,
                 scale_out: float = 1.0) -> np.ndarray:
         """Output bits of the hipgemm_gemm semantics (oracle.h: hg_gemm_ex):
-        uint16 (bf16 / f16), uint32 (fp32 bits) or uint8 (e4m3)."""
+        uint16 (bf16 / f16), uint32 (fp32 bits) or uint8 (e4m3).  fp4
+        operands (a_fmt = b_fmt = FMT_FP4): A and B hold K / 2 bytes per
+        row, two elements per byte."""
         A = np.ascontiguousarray(A)
         B = np.ascontiguousarray(B)
-        M, K = A.shape
+        M, Kb = A.shape
         N = B.shape[0]
-        assert B.shape[1] == K
+        assert B.shape[1] == Kb
+        assert (a_fmt == FMT_FP4) == (b_fmt == FMT_FP4)
+        K = 2 * Kb if a_fmt == FMT_FP4 else Kb
 
         def vec(v, n):
             if v is None:
@@ -219,7 +231,7 @@ class Oracle:
             return v
         sr, sc, bb = vec(scale_rows, M), vec(scale_cols, N), vec(bias, N)
         C = np.empty((M, N), {OUT_F32: np.uint32, OUT_FP8: np.uint8}.get(out, np.uint16))
-        self.lib.hg_gemm_ex(_ptr(A), _ptr(B), _ptr(C), M, N, K, K, K, N,
+        self.lib.hg_gemm_ex(_ptr(A), _ptr(B), _ptr(C), M, N, K, Kb, Kb, N,
                             a_fmt, b_fmt, out, act, scale_a, scale_b,
                             None if sr is None else _ptr(sr),
                             None if sc is None else _ptr(sc),

@@ -474,3 +474,34 @@ def test_gemm_mx_pinned(oracle):
     sa2[3, 2] = 255
     nan = (oracle.gemm_mx(A, B, sa2, sb) & 0x7FFF) > 0x7F80
     assert nan[3].all() and not nan[np.arange(M) != 3].any()
+
+
+def test_fp4_decode_and_gemm_pinned(oracle):
+    """OCP E2M1: the value table of the OCP Microscaling v1.0 spec (written
+    out, not derived); the fp4 GEMM against fp64 sums of the decoded
+    values; nibble order: swapping the nibbles of every byte of both
+    operands is a common permutation of K (same result), of one operand
+    only it is not."""
+    table = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+    got = oracle.fp4_to_f32(np.arange(16))
+    assert list(got[:8]) == table and list(-got[8:]) == table
+    assert np.signbit(got[8])  # 0x8 is -0
+    rng = np.random.default_rng(61)
+    M, N, K = 37, 29, 160
+    A = rng.integers(0, 256, (M, K // 2)).astype(np.uint8)
+    B = rng.integers(0, 256, (N, K // 2)).astype(np.uint8)
+
+    def unpack(X):
+        return np.stack([X & 15, X >> 4], axis=2).reshape(X.shape[0], -1)
+    t = got.astype(np.float64)
+    want = (t[unpack(A)] @ t[unpack(B)].T).astype(np.float32)
+    C = oracle.gemm_ex(A, B, a_fmt=po.FMT_FP4, b_fmt=po.FMT_FP4, out=po.OUT_F32)
+    assert np.array_equal(C.view(np.float32), want)
+    swap = lambda X: ((X & 15) << 4 | (X >> 4)).astype(np.uint8)
+    assert np.array_equal(oracle.gemm_ex(swap(A), swap(B), a_fmt=4, b_fmt=4,
+                                         out=po.OUT_F32), C)
+    assert not np.array_equal(oracle.gemm_ex(swap(A), B, a_fmt=4, b_fmt=4,
+                                             out=po.OUT_F32), C)
+    # bf16 output of the same sums: the bf16 rounding of the fp32 values
+    assert np.array_equal(oracle.gemm_ex(A, B, a_fmt=4, b_fmt=4),
+                          oracle.f32_to_bf16(want))
