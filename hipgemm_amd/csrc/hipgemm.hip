@@ -103,7 +103,9 @@ hipError_t launch_tiled(int variant, GemmArgs g, hk::Key key,
   int threads = Cfg4w::kThreads;
   switch (variant) {
     case HIPGEMM_VARIANT_TILE128:
-      fn = key.ext ? hk::tile128_ext(key) : hk::tile128_plain(key);
+      fn = g.mx.a   ? hk::tile128_mx(key)
+           : key.ext ? hk::tile128_ext(key)
+                     : hk::tile128_plain(key);
       threads = CfgT128::kThreads;
       break;
     case HIPGEMM_VARIANT_8WAVE:
@@ -234,7 +236,7 @@ hipError_t launch_t128_split(GemmArgs g, const T128Plan& p, void* ws,
   g.split.slices = p.slices;
   g.split.slice_steps = p.slice_steps;
   g.split.partial = static_cast<float*>(ws);
-  const void* fn = hk::tile128_split(key);
+  const void* fn = g.mx.a ? hk::tile128_split_mx(key) : hk::tile128_split(key);
   if (!fn) return hipErrorInvalidValue;
   void* args[] = {&g};
   hipError_t e = hipLaunchKernel(fn, dim3(g.workers), dim3(CfgT128::kThreads),
@@ -284,7 +286,7 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   const bool fp4 = d.a_format == HIPGEMM_FMT_FP4_E2M1 ||
                    d.b_format == HIPGEMM_FMT_FP4_E2M1;
   if (fp4) {
-    if (d.a_format != d.b_format || K % 32 != 0 || d.mx_scale_a || d.mx_scale_b ||
+    if (d.a_format != d.b_format || K % 32 != 0 ||
         (variant != HIPGEMM_VARIANT_AUTO && variant != HIPGEMM_VARIANT_TILE128))
       return hipErrorInvalidValue;
     K /= 2;
@@ -319,19 +321,21 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   // epilogue only.
   if (variant == HIPGEMM_VARIANT_4WAVE && (ext || fmt != 0))
     return hipErrorInvalidValue;
-  // MX block scales: the 4-wave 16x16x128 schedule, per-tensor epilogue.
+  // MX block scales: the 4-wave 16x16x128 and 128 x 128 schedules,
+  // per-tensor epilogue (K in elements a multiple of 32: bytes of 16 for fp4).
   const bool mx = d.mx_scale_a || d.mx_scale_b;
-  if (mx && (!d.mx_scale_a || !d.mx_scale_b || K % 32 != 0 || ext ||
+  if (mx && (!d.mx_scale_a || !d.mx_scale_b || K % (fp4 ? 16 : 32) != 0 || ext ||
              !aligned(d.mx_scale_a, 16) || !aligned(d.mx_scale_b, 16) ||
              (variant != HIPGEMM_VARIANT_AUTO &&
-              variant != HIPGEMM_VARIANT_4WAVE_MFMA16)))
+              variant != HIPGEMM_VARIANT_4WAVE_MFMA16 &&
+              variant != HIPGEMM_VARIANT_TILE128)))
     return hipErrorInvalidValue;
   const int n1 = (variant == HIPGEMM_VARIANT_AUTO && !mx && !fp4 && K > 0)
                      ? split_columns(M, N, cu_count())
                      : 0;
-  variant = mx    ? HIPGEMM_VARIANT_4WAVE_MFMA16
-            : fp4 ? HIPGEMM_VARIANT_TILE128
-                  : resolve_variant(variant, M, N, K);
+  variant = fp4 ? HIPGEMM_VARIANT_TILE128 : resolve_variant(variant, M, N, K);
+  // MX: the 128 x 128 schedule where AUTO picks it, else the 4-wave one.
+  if (mx && variant != HIPGEMM_VARIANT_TILE128) variant = HIPGEMM_VARIANT_4WAVE_MFMA16;
   if (variant == HIPGEMM_VARIANT_8WAVE && d.out_dtype >= HIPGEMM_OUT_F32)
     variant = HIPGEMM_VARIANT_4WAVE_MFMA16;  // AUTO's 8-wave choice
   if (K == 0) lda = ldb = 16;  // nothing is read; keep the offset math inert
@@ -539,8 +543,13 @@ size_t hipgemm_gemm_workspace_size(const hipgemm_gemm_desc* d) {
     return 0;
   const bool fp4 = d->a_format == HIPGEMM_FMT_FP4_E2M1 ||
                    d->b_format == HIPGEMM_FMT_FP4_E2M1;
-  if (d->mx_scale_a || d->mx_scale_b) return 0;  // the 4-wave schedule
   if (fp4) return plan_t128(d->M, d->N, d->K / 2, cu_count()).ws_bytes;
+  if (d->mx_scale_a || d->mx_scale_b) {  // 128 x 128 where AUTO picks it
+    const int v = resolve_variant(d->variant, d->M, d->N, d->K);
+    return v == HIPGEMM_VARIANT_TILE128
+               ? plan_t128(d->M, d->N, d->K, cu_count()).ws_bytes
+               : 0;
+  }
   return hipgemm_workspace_size(d->M, d->N, d->K, d->variant);
 }
 

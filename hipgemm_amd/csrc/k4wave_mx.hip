@@ -1,5 +1,5 @@
-// The 4-wave 16x16x128 schedule with MX block scales (per-tensor epilogue),
-// for every operand-format pair, and the scale-packing kernel.
+// The schedules with MX block scales (per-tensor epilogue): the 4-wave
+// 16x16x128 one and the 128 x 128 one, and the scale-packing kernel.
 #include "kernels.hpp"
 
 namespace hipgemm {
@@ -12,6 +12,19 @@ template <bool kVec, int kFmt>
 __global__ __launch_bounds__(256, 1) void k_fp8_gemm_4wave_mx(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg4w::kLdsBytes];
   gemm_4wave_body<kVec, 16, false, kFmt, kActNone, kOutBf16, true>(g, (lds_u8*)lds);
+}
+
+// The 128 x 128 schedule with MX block scales (per-tensor epilogue), for
+// every operand-format pair including fp4 x fp4; whole K and K-slices.
+template <bool kVec, int kFmt>
+__global__ __launch_bounds__(256, 1) void k_fp8_gemm_t128_mx(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[CfgT128::kLdsBytes];
+  gemm_t128_body<kVec, false, kFmt, kActNone, kOutBf16, false, true>(g, (lds_u8*)lds);
+}
+template <int kFmt>
+__global__ __launch_bounds__(256, 1) void k_fp8_gemm_t128_split_mx(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[CfgT128::kLdsBytes];
+  gemm_t128_body<true, false, kFmt, kActNone, kOutBf16, true, true>(g, (lds_u8*)lds);
 }
 
 // One thread per packed byte (layout of MxArgs): byte f of step st of lane l
@@ -38,6 +51,21 @@ const void* four_wave_mx(const Key& k) {
       return (const void*)&k_fp8_gemm_4wave_mx<decltype(V)::value == 1,
                                                decltype(F)::value>;
     });
+  });
+}
+
+const void* tile128_mx(const Key& k) {
+  return sel_fmt(k.fmt, [&](auto F) {
+    return sel2(k.vec, [&](auto V) {
+      return (const void*)&k_fp8_gemm_t128_mx<decltype(V)::value == 1,
+                                              decltype(F)::value>;
+    });
+  });
+}
+
+const void* tile128_split_mx(const Key& k) {
+  return sel_fmt(k.fmt, [&](auto F) {
+    return (const void*)&k_fp8_gemm_t128_split_mx<decltype(F)::value>;
   });
 }
 

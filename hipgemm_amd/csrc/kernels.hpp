@@ -38,6 +38,8 @@ const void* skinny_plain(int kmb, const Key& k);    // kskinny_plain.hip
 const void* skinny_ext(int kmb, const Key& k);      // kskinny_ext.hip
 const void* skinny_reduce(int kf, const Key& k);    // kskinny_plain.hip
 const void* four_wave_mx(const Key& k);             // k4wave_mx.hip
+const void* tile128_mx(const Key& k);               // k4wave_mx.hip
+const void* tile128_split_mx(const Key& k);         // k4wave_mx.hip
 const void* tile128_plain(const Key& k);            // kt128_plain.hip
 const void* tile128_ext_narrow(const Key& k);       // kt128_ext.hip
 const void* tile128_ext_wide(const Key& k);         // kt128_ext_wide.hip

@@ -156,7 +156,9 @@ typedef struct hipgemm_gemm_desc {
    * neither; K % 32 == 0, 16-byte aligned.  Each element is multiplied by its
    * block's scale before the products are summed; the per-tensor scales
    * still apply.  Not combined with the row / column / bias / activation /
-   * fp16 options; schedules AUTO and HIPGEMM_VARIANT_4WAVE_MFMA16. */
+   * output-type options; schedules AUTO (the 128 x 128 one where AUTO picks
+   * it, else the 4-wave one), HIPGEMM_VARIANT_4WAVE_MFMA16 and
+   * HIPGEMM_VARIANT_TILE128 (which also takes fp4 operands: MXFP4). */
   const void *mx_scale_a, *mx_scale_b;
   /* Device scalar or NULL (1.0) multiplying activation(v) before the
    * conversion; FP8_E4M3 output only (NULL otherwise), 4-byte aligned. */

@@ -69,12 +69,17 @@ struct CfgT128 {
 
 // kSplit: work units are (tile, K-slice) pairs (g.split); each writes its
 // fp32 partial tile instead of C, and gemm_t128_reduce_body sums them.
+// kMx: MX block scales from g.mx (the packed layout of MxArgs; per-tensor
+// epilogue).  Each step also loads, for the next step, each operand's 16
+// scale bytes of the lane into registers (one buffer load per operand).
 template <bool kVec, bool kExt = false, int kFmt = 0, int kAct = kActNone,
-          int kOut = kOutBf16, bool kSplit = false>
+          int kOut = kOutBf16, bool kSplit = false, bool kMx = false>
 __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   using Cfg = CfgT128;
   constexpr int S = Cfg::kStages;
-  constexpr int kD = Cfg::kDmaPerStep;
+  constexpr int kDma = Cfg::kDmaPerStep;       // DMA per wave per step
+  constexpr int kD = kDma + (kMx ? 2 : 0);     // memory operations per step
+  static_assert(!(kMx && kExt), "MX: per-tensor epilogue");
   constexpr int kScaleDma = kExt ? 3 : 0;
   // Stores per wave per tile: 8 x 16 bytes of C (2-byte types, staged),
   // 16 x 16 bytes of partial, or 16 straight from the accumulators (fp32 /
@@ -126,10 +131,11 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
     __amdgpu_buffer_rsrc_t a, b;
     uint32_t k0;
     int kend;
+    int tm, tn;  // tile coordinates (kMx); tm = -1: no unit
   };
   auto src_of = [&](int unit) {
     if (unit >= walk.end)
-      return Src{make_rsrc(g.A, 0u), make_rsrc(g.B, 0u), 0u, 0};
+      return Src{make_rsrc(g.A, 0u), make_rsrc(g.B, 0u), 0u, 0, -1, 0};
     const int tile = kSplit ? unit % tiles : unit;
     const int slice = kSplit ? unit / tiles : 0;
     const TileCoord c = grouped_tile(tile, tiles_m, tiles_n, g.group_m);
@@ -140,7 +146,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
                          (uint32_t)ra * (uint32_t)g.lda),
                make_rsrc(g.B + (size_t)c.n * Cfg::kBN * g.ldb,
                          (uint32_t)rb * (uint32_t)g.ldb),
-               (uint32_t)k0, min(K, k0 + steps * Cfg::kBK)};
+               (uint32_t)k0, min(K, k0 + steps * Cfg::kBK), c.m, c.n};
   };
   Src cur = src_of(t);
   Src nxt = src_of(t + walk.stride);
@@ -175,6 +181,36 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   const uint32_t off_b =
       (uint32_t)(Cfg::kAStage + (wn * 64 + r16) * Cfg::kBK + rslot * 16);
   i32x8 fa[2][4], fb[2][4];
+  // kMx: the lane's 16 scale bytes of A and of B_T for the step of each
+  // register set (see mx_load).
+  i32x4 mxa[2] = {}, mxb[2] = {};
+  // Scale words of tile-local step d (d >= steps_pad: the next unit's step
+  // d - steps_pad) into set `set`.  The packed layout holds, per 128-row
+  // group W and per pair p of 128-element MFMA steps, 16 bytes per lane
+  // (step 0 of the pair, then step 1; 8 fragments of 16 rows each): for
+  // fp4 a 128-byte step is one pair (its two MFMA take halves 0 and 1),
+  // for 8-bit operands half of one.  W = the tile's row (A) or column (B)
+  // index.  Groups past M / N, pairs past K and missing units read zero.
+  auto mx_load = [&](int d, int set) {
+    const bool next = d >= steps_pad;
+    const Src& s = next ? nxt : cur;
+    const int gs = (int)(s.k0 / Cfg::kBK) + (next ? d - steps_pad : d);  // byte-step
+    const int kel = is_fp4(kFmt) ? 2 * K : K;  // K in elements
+    const int P = mx_pairs(kel);
+    const int p = is_fp4(kFmt) ? gs : gs / 2;
+    const MxArgs mx = kernel_mx();
+    const bool live = s.tm >= 0 && p < P;
+    const uint32_t vo = (uint32_t)lane * 16u;
+    const __amdgpu_buffer_rsrc_t ra =
+        make_rsrc(mx.a, live ? (uint32_t)mx_packed_bytes(M, kel) : 0u);
+    const __amdgpu_buffer_rsrc_t rb =
+        make_rsrc(mx.b, live ? (uint32_t)mx_packed_bytes(N, kel) : 0u);
+    const int tm = live ? s.tm : 0, tn = live ? s.tn : 0;
+    mxa[set] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+        ra, vo + (uint32_t)((tm * P + p) * 1024), 0, 0));
+    mxb[set] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+        rb, vo + (uint32_t)((tn * P + p) * 1024), 0, 0));
+  };
   auto read_step = [&](int stage, int set) {
     const lds_u8* base = lds + stage * Cfg::kStage;
 #pragma unroll
@@ -198,6 +234,18 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   auto step = [&](int set, int rstage, int d, int dstage) {
     const lds_u8* rb = lds + rstage * Cfg::kStage;
     i32x4 rd[16];
+    // kMx: this wave's scale words of the step (fp4: halves 0 and 1; 8-bit:
+    // half `set` of the pair), chosen once.
+    uint32_t wa0 = 0, wa1 = 0, wb0 = 0, wb1 = 0;
+    if constexpr (kMx) {
+      const int h0 = is_fp4(kFmt) ? 0 : 2 * set;
+      wa0 = (uint32_t)(wm ? mxa[set][h0 + 1] : mxa[set][h0]);
+      wb0 = (uint32_t)(wn ? mxb[set][h0 + 1] : mxb[set][h0]);
+      if constexpr (is_fp4(kFmt)) {
+        wa1 = (uint32_t)(wm ? mxa[set][3] : mxa[set][2]);
+        wb1 = (uint32_t)(wn ? mxb[set][3] : mxb[set][2]);
+      }
+    }
     sched_fence();
 #pragma unroll
     for (int n = 0; n < 16; ++n) {
@@ -205,13 +253,26 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
       if constexpr (is_fp4(kFmt)) {
         // fp4: 256 elements per 128-byte step, two MFMA per block -- the
         // fragments' low halves (K-chunk g) and high halves (chunk g + 4);
-        // the instruction reads four registers of each operand.
+        // the instruction reads four registers of each operand.  kMx: half
+        // h uses scale word 2 h + (the wave's 64-row half), byte i / j.
         const i32x8& x = fb[set][j];
         const i32x8& y = fa[set][i];
-        acc[i][j] = mfma_16x16x128<kFmtFp4, kFmtFp4>(x, y, acc[i][j]);
-        acc[i][j] = mfma_16x16x128<kFmtFp4, kFmtFp4>(
-            __builtin_shufflevector(x, x, 4, 5, 6, 7, 0, 1, 2, 3),
-            __builtin_shufflevector(y, y, 4, 5, 6, 7, 0, 1, 2, 3), acc[i][j]);
+        const i32x8 xh = __builtin_shufflevector(x, x, 4, 5, 6, 7, 0, 1, 2, 3);
+        const i32x8 yh = __builtin_shufflevector(y, y, 4, 5, 6, 7, 0, 1, 2, 3);
+        if constexpr (kMx) {
+          acc[i][j] = mfma_16x16x128_mx<kFmtFp4, kFmtFp4>(x, y, acc[i][j], wb0, wa0,
+                                                          j, i);
+          acc[i][j] = mfma_16x16x128_mx<kFmtFp4, kFmtFp4>(xh, yh, acc[i][j], wb1, wa1,
+                                                          j, i);
+        } else {
+          acc[i][j] = mfma_16x16x128<kFmtFp4, kFmtFp4>(x, y, acc[i][j]);
+          acc[i][j] = mfma_16x16x128<kFmtFp4, kFmtFp4>(xh, yh, acc[i][j]);
+        }
+      } else if constexpr (kMx) {
+        // 8-bit: the step is half `set` of its pair (units start on even
+        // steps and each trip takes two steps).
+        acc[i][j] = mfma_16x16x128_mx<fmt_b(kFmt), fmt_a(kFmt)>(
+            fb[set][j], fa[set][i], acc[i][j], wb0, wa0, j, i);
       } else {
         acc[i][j] = mfma_16x16x128<fmt_b(kFmt), fmt_a(kFmt)>(fb[set][j], fa[set][i],
                                                              acc[i][j]);
@@ -230,6 +291,11 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
       }
       sched_fence();
     }
+    // kMx: the scales of the step after next, into this step's set (its
+    // MFMA are issued): loaded two steps ahead, they retire with the DMA
+    // the waits already cover instead of making the next step wait for
+    // every DMA issued before them.
+    if constexpr (kMx) mx_load(d - (S - 3), set);
     const int o = set ^ 1;
     fa[o][0] = join(rd[0], rd[1]);
 #pragma unroll
@@ -260,15 +326,21 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
     dma4(rb, stg + 1024, co);
   };
 
-  // Prologue of the first tile: steps 0 .. S - 2, then the reads of step 0.
+  // Prologue of the first tile: (kMx: the scales of step 0,) steps
+  // 0 .. S - 2, then the reads of step 0.
+  if constexpr (kMx) {
+    mx_load(0, 0);
+    mx_load(1, 1);
+  }
 #pragma unroll
   for (int d = 0; d < S - 1; ++d) dma_step(d, d);
-  wait_vmcnt<(S - 2) * kD>();
+  wait_vmcnt<(S - 2) * kDma>();
   barrier();
   read_step(0, 0);
 
   int base = 0;          // stage of the tile's step 0
   bool stores = false;   // the previous tile's C stores are in flight
+  bool first = true;     // the first tile (its first steps' DMA: prologue)
   for (;;) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -280,12 +352,15 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int kk = k + h;
-        // Step kk + 1 landed: newer than it are steps kk + 2 .. kk + S - 2,
-        // and, during the first S - 2 steps of a tile after the first, the
-        // previous tile's stores (issued after this tile's first S - 1
-        // steps' DMA); kExt's three scale loads only make this wait longer.
+        // Step kk + 1 landed: newer than it are steps kk + 2 .. kk + S - 2
+        // (kD operations each; in the prologue kDma), and, during the first
+        // S - 2 steps of a tile after the first, the previous tile's stores
+        // (issued after this tile's first S - 1 steps' DMA); kExt's three
+        // scale loads only make this wait longer.
         if (stores && kk < S - 2)
           wait_vmcnt<(S - 3) * kD + kStores>();
+        else if (first && kk < S - 2)
+          wait_vmcnt<(S - 3) * kDma>();
         else
           wait_vmcnt<(S - 3) * kD>();
         barrier();
@@ -428,6 +503,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
     cur = nxt;
     nxt = src_of(t + walk.stride);
     stores = kSplit || kVec;
+    first = false;
   }
   // The last tile's look-ahead DMA (empty ranges) still count in vmcnt.
   wait_vmcnt<0>();

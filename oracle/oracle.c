@@ -484,6 +484,18 @@ void hg_gemm_mx(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
                 const uint8_t *sa, int ldsa, const uint8_t *sb, int ldsb,
                 float scale_a, float scale_b) {
   const float *la = lut_of(a_fmt), *lb = lut_of(b_fmt);
+  /* fp4: one byte per element (the nibble), as in hg_gemm_ex. */
+  uint8_t *Au = NULL, *Bu = NULL;
+  if (a_fmt == HG_FMT_FP4) {
+    Au = unpack_fp4(A, M, K, lda);
+    A = Au;
+    lda = K;
+  }
+  if (b_fmt == HG_FMT_FP4) {
+    Bu = unpack_fp4(B_T, N, K, ldb);
+    B_T = Bu;
+    ldb = K;
+  }
   float *Af = (float *)malloc((size_t)(M > 0 ? M : 1) * (K > 0 ? K : 1) * sizeof(float));
   float *Bt = (float *)malloc((size_t)(N > 0 ? N : 1) * (K > 0 ? K : 1) * sizeof(float));
   if (!Af || !Bt) abort();
@@ -522,6 +534,8 @@ void hg_gemm_mx(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
   }
   free(Af);
   free(Bt);
+  free(Au);
+  free(Bu);
 }
 
 void hg_gemm_fast(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,

@@ -242,17 +242,20 @@ class Oracle:
                 sb: np.ndarray, a_fmt: int = FMT_E4M3, b_fmt: int = FMT_E4M3,
                 scale_a: float = 1.0, scale_b: float = 1.0) -> np.ndarray:
         """bf16 bits of the MX-scaled product (oracle.h: hg_gemm_mx); sa: M x
-        ceil(K/32) E8M0 bytes, sb: N x ceil(K/32)."""
+        ceil(K/32) E8M0 bytes, sb: N x ceil(K/32), K in elements (fp4: A and
+        B hold K / 2 bytes per row)."""
         A = np.ascontiguousarray(A)
         B = np.ascontiguousarray(B)
-        M, K = A.shape
+        M, Kb = A.shape
         N = B.shape[0]
+        assert (a_fmt == FMT_FP4) == (b_fmt == FMT_FP4)
+        K = 2 * Kb if a_fmt == FMT_FP4 else Kb
         kb = (K + 31) // 32
         sa = np.ascontiguousarray(sa, np.uint8)
         sb = np.ascontiguousarray(sb, np.uint8)
-        assert B.shape[1] == K and sa.shape == (M, kb) and sb.shape == (N, kb)
+        assert B.shape[1] == Kb and sa.shape == (M, kb) and sb.shape == (N, kb)
         C = np.empty((M, N), np.uint16)
-        self.lib.hg_gemm_mx(_ptr(A), _ptr(B), _ptr(C), M, N, K, K, K, N,
+        self.lib.hg_gemm_mx(_ptr(A), _ptr(B), _ptr(C), M, N, K, Kb, Kb, N,
                             a_fmt, b_fmt, _ptr(sa), kb, _ptr(sb), kb,
                             scale_a, scale_b)
         return C

@@ -194,14 +194,16 @@ def test_gemm_desc_entry_validation():
 
 def test_fp4_entry_validation():
     """fp4 operands: both fp4, K (elements) a multiple of 32, lda / ldb in
-    bytes >= K / 2, AUTO or the 128 x 128 schedule, no MX; the descriptor's
+    bytes >= K / 2, AUTO or the 128 x 128 schedule (MX scales too, with the
+    per-tensor epilogue); the descriptor's
     workspace query plans the 128 x 128 schedule on K / 2 bytes."""
     base = dict(A=FAKE, B_T=FAKE, C=FAKE, M=300, N=300, K=256, lda=128,
                 ldb=128, ldc=300, a_format=4, b_format=4)
     assert hg.gemm_desc_raw(hg.GemmDesc(**dict(base, M=0))) == 0
     for bad in (dict(b_format=0), dict(a_format=1), dict(K=240), dict(lda=112),
                 dict(variant=2), dict(variant=3), dict(variant=4),
-                dict(mx_scale_a=FAKE, mx_scale_b=FAKE)):
+                dict(mx_scale_a=FAKE, mx_scale_b=FAKE, variant=2),
+                dict(mx_scale_a=FAKE, mx_scale_b=FAKE, bias=FAKE)):
         assert hg.gemm_desc_raw(hg.GemmDesc(**dict(base, **bad))) == INVALID, bad
     L = hg.lib()
     # 256 x 4096 x 28672 elements = 14336 bytes per row: 2 x 32 tiles of 128,

@@ -38,8 +38,11 @@ def np_pack(S, rows, K):
     return out
 
 
-def run(torch, A, B, sa, sb, fa=0, fb=0, s_a=None, variant=0, ldc_pad=24):
-    M, K = A.shape
+def run(torch, A, B, sa, sb, fa=0, fb=0, s_a=None, variant=0, ldc_pad=24,
+        K=None):
+    """K: elements per row (default the bytes of A's rows; fp4: twice)."""
+    M, Kb = A.shape
+    K = K or Kb
     N = B.shape[0]
     ldc = N + ldc_pad
     a, b = to_dev(torch, A), to_dev(torch, B)
@@ -48,8 +51,8 @@ def run(torch, A, B, sa, sb, fa=0, fb=0, s_a=None, variant=0, ldc_pad=24):
     tsa = torch.tensor([s_a], device="cuda") if s_a is not None else None
     buf = torch.full((M + 4, ldc), CANARY, dtype=torch.int16, device="cuda")
     d = hg.GemmDesc(A=a.data_ptr(), B_T=b.data_ptr(),
-                    C=buf.data_ptr() + 2 * ldc * 2, M=M, N=N, K=K, lda=K,
-                    ldb=K, ldc=ldc, a_format=fa, b_format=fb,
+                    C=buf.data_ptr() + 2 * ldc * 2, M=M, N=N, K=K, lda=Kb,
+                    ldb=Kb, ldc=ldc, a_format=fa, b_format=fb,
                     scale_a=tsa.data_ptr() if tsa is not None else 0,
                     variant=variant, mx_scale_a=pa.data_ptr(),
                     mx_scale_b=pb.data_ptr())
@@ -79,16 +82,18 @@ def test_pack_layout(gpu, rows, K):
     assert np.array_equal(got.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("variant", [2, 5], ids=["mfma16", "tile128"])
 @pytest.mark.parametrize("fa,fb", [(0, 0), (1, 0), (0, 1), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(300, 260, 224), (512, 512, 1024),
-                                   (257, 1000, 96), (1100, 1300, 4128)])
-def test_mx_ternary_bit_exact(gpu, oracle, M, N, K, fa, fb):
-    say(f"case mx-ternary a={fa} b={fb} M={M} N={N} K={K} seed=91")
+                                   (257, 1000, 96), (1100, 1300, 4128),
+                                   (200, 300, 4096)])
+def test_mx_ternary_bit_exact(gpu, oracle, M, N, K, fa, fb, variant):
+    say(f"case [v{variant}] mx-ternary a={fa} b={fb} M={M} N={N} K={K} seed=91")
     rng = np.random.default_rng(91)
     A = TERN[fa][rng.integers(0, 3, (M, K))]
     B = TERN[fb][rng.integers(0, 3, (N, K))]
     sa, sb = scales(rng, M, K), scales(rng, N, K)
-    C, guard = run(gpu, A, B, sa, sb, fa, fb, s_a=0.75)
+    C, guard = run(gpu, A, B, sa, sb, fa, fb, s_a=0.75, variant=variant)
     assert guard, "write outside the M x N window"
     want = oracle.gemm_mx(A, B, sa, sb, fa, fb, scale_a=0.75)
     assert np.array_equal(C, want), f"{int((C != want).sum())} of {C.size} differ"
@@ -143,6 +148,25 @@ def test_mx_unit_scales_equal_plain(gpu, oracle):
     say(f"    vs plain: max_rel={max_rel:.3e} exact={exact:.6f}")
     assert max_rel <= REL_TOL
     assert compare(C, oracle.gemm(A, B))[0] <= REL_TOL
+
+
+@pytest.mark.parametrize("variant", [0, 5], ids=["auto", "tile128"])
+@pytest.mark.parametrize("M,N,K", [(300, 260, 256), (129, 1000, 96),
+                                   (1100, 700, 4128), (200, 300, 4096)])
+def test_mxfp4_bit_exact(gpu, oracle, M, N, K, variant):
+    """MXFP4: fp4 operands (random bytes) with block scales 2^-1 .. 2^1 on
+    the 128 x 128 schedule (whole K and K-slices): products are multiples of
+    2^-4 below 144, sums below 2^20 for K <= 4128, exact in fp32 in any
+    order -- bit-exact against hg_gemm_mx."""
+    say(f"case [v{variant}] mxfp4 M={M} N={N} K={K} seed=121")
+    rng = np.random.default_rng(121)
+    A = rng.integers(0, 256, (M, K // 2)).astype(np.uint8)
+    B = rng.integers(0, 256, (N, K // 2)).astype(np.uint8)
+    sa, sb = scales(rng, M, K, 126, 129), scales(rng, N, K, 126, 129)
+    C, guard = run(gpu, A, B, sa, sb, 4, 4, s_a=0.5, variant=variant, K=K)
+    assert guard, "write outside the M x N window"
+    want = oracle.gemm_mx(A, B, sa, sb, 4, 4, scale_a=0.5)
+    assert np.array_equal(C, want), f"{int((C != want).sum())} of {C.size} differ"
 
 
 def test_mx_nan_scale(gpu, oracle):
