@@ -96,9 +96,12 @@ hipError_t launch_tiled(int variant, GemmArgs g, hk::Key key,
   const int cus = cu_count();
   const int grid = tiles < cus ? tiles : cus;
   g.workers = grid;
-  // 2-byte types: 16-byte stores of 8 staged elements; fp32 / e4m3: one
-  // store of 4 elements straight from the accumulators.
-  key.vec = vec_ok(key.out, g.N, g.ldc, g.C, key.out >= kOutF32 ? 4 : 8);
+  // 2-byte types: 16-byte stores of 8 staged elements; fp32: one store of 4
+  // elements straight from the accumulators; e4m3: 16 staged elements on
+  // the 4-wave schedule, 4 from the accumulators on the 128 x 128 one.
+  const bool t128 = variant == HIPGEMM_VARIANT_TILE128;
+  key.vec = vec_ok(key.out, g.N, g.ldc, g.C,
+                   key.out == kOutF8 ? (t128 ? 4 : 16) : key.out == kOutF32 ? 4 : 8);
   const void* fn = nullptr;
   int threads = Cfg4w::kThreads;
   switch (variant) {

@@ -13,12 +13,14 @@ Importing this module registers, in the ``hipgemm`` namespace:
   torch.ops.hipgemm.gemm(a, b_t, scale_a=None, scale_b=None, scale_rows=None,
                          scale_cols=None, bias=None, activation="none",
                          out_f16=False, variant=0, out_dtype=None,
-                         scale_out=None)
+                         scale_out=None, mx_scale_a=None, mx_scale_b=None)
       the general entry point (hipgemm_gemm): a / b_t float8_e4m3fn or
-      float8_e5m2 (uint8 bytes: e4m3), fused bias and activation ("none",
-      "relu", "silu", "gelu_tanh"); output bf16, fp16 (out_f16 or
-      out_dtype), fp32 or float8_e4m3fn (out_dtype; saturating, after
-      multiplying by the 1-element scale_out).
+      float8_e5m2 (uint8 bytes: e4m3), or both float4_e2m1fn_x2 (K / 2
+      bytes per row); fused bias and activation ("none", "relu", "silu",
+      "gelu_tanh"); output bf16, fp16 (out_f16 or out_dtype), fp32 or
+      float8_e4m3fn (out_dtype; saturating, after multiplying by the
+      1-element scale_out); MX block scales packed by
+      hipgemm_amd.mx_pack_scales (mx_scale_a / mx_scale_b, uint8).
 
 All have fake (meta) implementations, so they trace under torch.compile,
 torch.export and FakeTensorMode without running, and they run inside CUDA
@@ -90,11 +92,14 @@ def gemm(a: torch.Tensor, b_t: torch.Tensor,
          bias: Optional[torch.Tensor] = None, activation: str = "none",
          out_f16: bool = False, variant: int = 0,
          out_dtype: Optional[torch.dtype] = None,
-         scale_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+         scale_out: Optional[torch.Tensor] = None,
+         mx_scale_a: Optional[torch.Tensor] = None,
+         mx_scale_b: Optional[torch.Tensor] = None) -> torch.Tensor:
     return _gemm(a, b_t, out_dtype=_out_dtype(out_f16, out_dtype),
                  scale_a=scale_a, scale_b=scale_b, scale_rows=scale_rows,
                  scale_cols=scale_cols, bias=bias, activation=activation,
-                 variant=variant, scale_out=scale_out)
+                 variant=variant, scale_out=scale_out, mx_scale_a=mx_scale_a,
+                 mx_scale_b=mx_scale_b)
 
 
 def _out_dtype(out_f16, out_dtype):
@@ -109,7 +114,8 @@ def _out_dtype(out_f16, out_dtype):
 @gemm.register_fake
 def _gemm_fake(a, b_t, scale_a=None, scale_b=None, scale_rows=None,
                scale_cols=None, bias=None, activation="none", out_f16=False,
-               variant=0, out_dtype=None, scale_out=None):
+               variant=0, out_dtype=None, scale_out=None, mx_scale_a=None,
+               mx_scale_b=None):
     _check_shapes(a, b_t)
     if activation not in ACTIVATIONS:
         raise HipGemmError(f"unknown activation {activation!r}")

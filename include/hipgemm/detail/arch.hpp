@@ -87,6 +87,10 @@ __device__ __forceinline__ u32x2 lds_read8(const lds_u8* p) {
   return *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(p);
 }
 
+__device__ __forceinline__ void lds_write4(lds_u8* p, uint32_t v) {
+  *reinterpret_cast<__attribute__((address_space(3))) uint32_t*>(p) = v;
+}
+
 __device__ __forceinline__ void lds_write8(lds_u8* p, u32x2 v) {
   *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(p) = v;
 }

@@ -697,7 +697,52 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                      pack_bf16x2(acc_read(a[2]) * scale, acc_read(a[3]) * scale)};
     };
 
-    if constexpr (kExt && kOut >= kOutF32) {
+    if constexpr (kExt && kOut == kOutF8 && kVecStore) {
+      // e4m3 output, 16-column groups (N, ldc multiples of 16): 32 rows at a
+      // time through the wave's own LDS (128 bytes per row; the 4-byte piece
+      // x = 4 j + l / 16 of row r at slot x ^ 4 ((r / 2) % 8): each write
+      // instruction covers 16 rows x 4 pieces, each read 8 rows x 8 lanes of
+      // 16 bytes -- both conflict-free), then 16-byte stores of whole
+      // 128-byte row segments (8 rows per instruction).
+      lds_u8* stg = lds + Cfg::kStoreBase + wave * Cfg::kStoreStage;
+      const int wr = elane & 15, wg = elane >> 4;
+      const int q = elane & 7, rsub = elane >> 3;
+      const uint32_t vcol = (uint32_t)(rsub * g.ldc + wn * 128 + 16 * q);
+      const uint32_t col_oob = oob_unless(16 * q, cols_left);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int bi = 2 * i + ii, r = 16 * ii + wr;
+            const f32x4& a = acc16[bi][j];
+            const uint32_t w = ev.e4m3x4(ev.template value4<kAct>(
+                acc_read(a[0]), acc_read(a[1]), acc_read(a[2]), acc_read(a[3]), bi, j));
+            lds_write4(stg + r * 128 + (((4 * j + wg) ^ (4 * ((r >> 1) & 7))) * 4), w);
+            sched_fence();  // bound the live range: one block at a time
+          }
+        compiler_fence();
+        i32x4 v[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const int r = 8 * p + rsub;
+          v[p] = lds_read16(stg + r * 128 + ((q ^ ((r >> 1) & 7)) * 16));
+        }
+        compiler_fence();
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          int row8 = 32 * i + 8 * p;
+          asm volatile("" : "+s"(row8));  // recompute per store, never hoist
+          const int srow = __builtin_amdgcn_readfirstlane((wm * 128 + row8) * g.ldc);
+          __builtin_amdgcn_raw_buffer_store_b128(
+              v[p], rsrc_c, vcol | col_oob | oob_unless(row8 + rsub, rows_left), srow,
+              kStoreC);
+        }
+        compiler_fence();
+        sched_fence();
+      }
+    } else if constexpr (kExt && kOut >= kOutF32) {
       // fp32 / e4m3 output: straight from the accumulators, no staging --
       // block (i, j): lane l -> row 16 i + l % 16, columns 16 j + 4 (l / 16)
       // .. + 3, one 16-byte (fp32) or 4-byte (e4m3) store per lane, or one
