@@ -641,6 +641,16 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     for (int kt0 = 2; kt0 < kt_pad; kt0 += 2) step_pair(kt0, std::false_type{});
 
     last_tail();
+    // The tail's accumulator is read only by the epilogue's explicit
+    // v_accvgpr_read, which hazard tracking does not see: an empty asm that
+    // takes it ties the MFMA to this point, so that no pass sinks it into the
+    // epilogue past mfma_drain() (with a branch in the epilogue, machine
+    // sinking moved it next to the first read, which then read a stale
+    // accumulator).
+    if constexpr (k16)
+      asm volatile("" : "+a"(acc16[7][7]));
+    else
+      asm volatile("" : "+a"(acc[3][3]));
     sched_fence();
 
     // ---- epilogue --------------------------------------------------------
@@ -912,10 +922,16 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       }
       }
     } else {
-      // N, ldc or C's alignment rule out 16-byte stores: 2-byte stores
-      // straight from the accumulators, lane masks as out-of-range offsets.
+      // N, ldc or C's alignment rule out 16-byte stores: stores straight
+      // from the accumulators, lane masks as out-of-range offsets -- one
+      // 8-byte store of four columns per lane and block when N and ldc are
+      // multiples of 4 and C is 8-byte aligned (a wave-uniform choice; at
+      // 8192 x 8188 x 8192 2-byte stores ran at a third of the aligned
+      // rate), else one 2-byte store per element.
       if constexpr (k16) {
         // block (i, j): lane l -> row 16 i + l%16, columns 16 j + 4(l/16) + r
+        const bool four = ((g.N | g.ldc) & 3) == 0 &&
+                          (reinterpret_cast<uintptr_t>(g.C) & 7) == 0;
         const uint32_t vlane =
             (uint32_t)(((elane & 15) * g.ldc + wn * 128 + 4 * (elane >> 4)) * 2);
 #pragma unroll
@@ -929,13 +945,19 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
             const int c = 16 * j + 4 * (elane >> 4);
             const f32x4& a = acc16[i][j];
             const u32x2 v = pack16(a, i, j);
+            if (four) {
+              __builtin_amdgcn_raw_buffer_store_b64(
+                  v, rsrc_c, (vrow | oob_unless(c, cols_left)) + 16 * j * 2, srow,
+                  kStoreC);
+            } else {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const uint32_t w = (r < 2 ? v.x : v.y) >> (16 * (r & 1));
-              __builtin_amdgcn_raw_buffer_store_b16(
-                  (unsigned short)w, rsrc_c,
-                  (vrow | oob_unless(c + r, cols_left)) + (16 * j + r) * 2,
-                  srow, kStoreC);
+              for (int r = 0; r < 4; ++r) {
+                const uint32_t w = (r < 2 ? v.x : v.y) >> (16 * (r & 1));
+                __builtin_amdgcn_raw_buffer_store_b16(
+                    (unsigned short)w, rsrc_c,
+                    (vrow | oob_unless(c + r, cols_left)) + (16 * j + r) * 2,
+                    srow, kStoreC);
+              }
             }
             sched_fence();  // bound the live range: one block at a time
           }
