@@ -203,7 +203,8 @@ def test_config5c_auto_split(gpu, oracle):
 
 @pytest.mark.parametrize("M,N,K", [(300, 260, 208), (1, 1, 16), (257, 255, 80),
                                    (17, 513, 48), (513, 17, 1040),
-                                   (256, 256, 16), (4000, 5000, 64)])
+                                   (256, 256, 16), (4000, 5000, 64),
+                                   (300, 258, 208)])
 def test_canaries_no_write_outside(gpu, oracle, M, N, K, variant):
     """C lives inside a larger buffer (2 guard rows above and below, 24 guard
     columns right); every guard element must keep its canary bit-exactly."""
