@@ -12,11 +12,15 @@ reference's bench.cpp:24 does the same).
 
 Prints ONE JSON line on stdout (rank 0, N = 1):
   value      whole-job TFLOP/s = 2*M*N*K*steps / wall time of the timed loop
+  prewarm    the declared steady-state pre-warm that ran before the
+             --warmup launches (--prewarm-seconds of back-to-back launches)
   roofline   the GEMM kernel's average launch duration from one pair of HIP
              events on its stream around the timed loop -> achieved TFLOP/s
              against the 5.0 PFLOP/s dense-FP8 MFMA peak; `traffic` (HBM bytes
-             per launch) comes from the committed rocprofv3 FETCH_SIZE /
-             WRITE_SIZE summary for this workload when one exists
+             per launch, rocprofv3 FETCH_SIZE / WRITE_SIZE) and
+             `mfma_busy_pct` come from the committed counter summary of this
+             workload (profiles/counters.json -> `counters_source`) when one
+             exists
   cpu_baseline  the reference's CPU GEMM (test.cpp:19-30, built from its
              sources into oracle/_ref) -- or the oracle port of it when that
              build is absent -- timed on a row slab of the same workload
@@ -49,6 +53,11 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--prewarm-seconds", type=float, default=3.0,
+                    help="steady-state pre-warm before the --warmup launches: "
+                         "back-to-back launches for at least this much wall "
+                         "time, so that the timed loop runs at the clock the "
+                         "GPU settles at under this load (0 = none)")
     ap.add_argument("--shape", default="8192,8192,8192",
                     help="M,N,K of the timed GEMM")
     ap.add_argument("--variant", default="auto")
@@ -63,18 +72,28 @@ def parse():
     return ap.parse_args()
 
 
-def traffic_for(workload: str, variant: str):
-    """HBM bytes per launch from the committed rocprof summary, if any."""
-    path = os.path.join(ROOT, "profiles", "traffic.json")
-    if not os.path.exists(path):
-        return None
+def counters_for(workload: str, variant: str) -> dict:
+    """The committed rocprofv3 counter summary of this workload and schedule
+    (profiles/counters.json), or {}: HBM bytes per launch (FETCH_SIZE /
+    WRITE_SIZE scaled by a copy kernel), MFMA-busy %, and the file they come
+    from."""
+    path = os.path.join(ROOT, "profiles", "counters.json")
     try:
         with open(path) as f:
-            table = json.load(f)
-        ent = table.get(workload, {}).get(variant)
-        return None if ent is None else ent.get("hbm_bytes_per_launch")
+            return json.load(f).get(workload, {}).get(variant, {}) or {}
     except (OSError, ValueError):
-        return None
+        return {}
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(A_host, B_host, M, N, K, target_s):
@@ -114,7 +133,7 @@ def cpu_baseline(A_host, B_host, M, N, K, target_s):
     tflops = 2.0 * rows * N * K / t / 1e12
     return {
         "value": round(tflops, 6), "unit": "TFLOP/s", "cores": cores,
-        "kind": kind,
+        "cpu_model": cpu_model(), "kind": kind,
         "sample": (f"rows 0..{rows - 1} of the {M}x{N}x{K} workload "
                    f"({rows}x{N}x{K}, {t:.1f} s, {what}); TFLOP/s of the "
                    f"slab, which equals the full-size rate (cost is linear "
@@ -122,16 +141,42 @@ def cpu_baseline(A_host, B_host, M, N, K, target_s):
     }
 
 
-def time_kernel(launch, warmup, steps, stream):
+def prewarm(launch, seconds):
+    """Back-to-back launches until at least `seconds` of wall time have
+    passed (checked between chunks of about 0.1 s).  The GPU ramps its clock
+    and settles its power state over the first few thousand launches of a
+    heavy kernel; this runs the timed loop at the steady state.  Returns
+    (launches, seconds)."""
+    import torch
+    if seconds <= 0:
+        return 0, 0.0
+    t0 = time.perf_counter()
+    n, chunk = 0, 4
+    while True:
+        c0 = time.perf_counter()
+        for _ in range(chunk):
+            launch(n)
+            n += 1
+        torch.cuda.synchronize()
+        now = time.perf_counter()
+        if now - t0 >= seconds:
+            return n, now - t0
+        per = (now - c0) / chunk
+        chunk = max(1, min(100000, int(0.1 / max(per, 1e-7))))
+
+
+def time_kernel(launch, warmup, steps, stream, prewarm_s=0.0):
     """The contract's timed loop, then a per-launch pass for diagnostics.
 
-    Timed loop: `steps` launches back to back with nothing between them,
+    Pre-warm (prewarm_s seconds of launches, then `warmup` more), then the
+    timed loop: `steps` launches back to back with nothing between them,
     bracketed by a device synchronize on both sides; wall time from the host
     clock and, over the same region, one pair of HIP events on the launch
     stream (-> average time per launch).  Per-launch pass: the same number of
     launches, each between its own event pair (median, best, drift)."""
     import numpy as np
     import torch
+    pre_n, pre_s = prewarm(launch, prewarm_s)
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()
@@ -154,6 +199,7 @@ def time_kernel(launch, warmup, steps, stream):
     torch.cuda.synchronize()
     per = np.array([a.elapsed_time(b) for a, b in ev])
     return {"wall_ms": wall * 1e3 / steps, "event_ms": event_ms,
+            "prewarm_launches": pre_n, "prewarm_s": pre_s,
             "median_ms": float(np.median(per)), "best_ms": float(per.min()),
             "tenths": [float(p.mean()) for p in
                        np.array_split(per, min(10, len(per)))]}
@@ -231,7 +277,8 @@ def main():
         del src, dst
 
     flop = 2.0 * M * N * K
-    res = time_kernel(launch, args.warmup, args.steps, stream)
+    res = time_kernel(launch, args.warmup, args.steps, stream,
+                      args.prewarm_seconds)
     ms_per_step = res["wall_ms"]
     value = flop / (ms_per_step * 1e-3) / 1e12
     avg_ms = res["event_ms"]
@@ -240,6 +287,8 @@ def main():
         f"ms/launch by events -> {value:.1f} TFLOP/s wall, {achieved:.1f} "
         f"by events; per-launch pass median={res['median_ms']:.4f} "
         f"best={res['best_ms']:.4f}")
+    log(f"bench: pre-warm {res['prewarm_launches']} launches in "
+        f"{res['prewarm_s']:.2f} s before the {args.warmup} warm-up launches")
     log("bench: per-launch ms by tenth of the per-launch pass: "
         + " ".join(f"{x:.4f}" for x in res["tenths"]))
 
@@ -248,25 +297,31 @@ def main():
     # written once.  Below the ridge point (peak flop / peak bytes) the
     # kernel is bounded by HBM, above it by the MFMA.
     alg_bytes = M * K + N * K + 2 * M * N
+    ctr = counters_for(workload, vname)
+    measured = {"traffic": ctr.get("hbm_bytes_per_launch"),
+                "mfma_busy_pct": ctr.get("mfma_busy_pct"),
+                "counters_source": ctr.get("source")}
     if flop / max(alg_bytes, 1) < PEAK_FP8_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9):
         gbs = alg_bytes / (avg_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(gbs, 1),
                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": round(gbs / PEAK_HBM_GBS, 4),
-                    "traffic": traffic_for(workload, vname),
-                    "algorithmic_bytes": alg_bytes}
+                    **measured, "algorithmic_bytes": alg_bytes}
     else:
         roofline = {"bound": "mfma", "achieved": round(achieved, 3),
                     "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
-                    "traffic": traffic_for(workload, vname)}
+                    **measured}
     result = {
-        "metric": "FP8 GEMM TFLOP/s at M=N=K=8192 (% of dense FP8 peak)",
+        "metric": ("FP8 GEMM TFLOP/s at M=N=K=8192 (% of dense FP8 peak) "
+                   "+ MFMA busy %"),
         "value": round(value, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "prewarm": {"seconds": round(res["prewarm_s"], 3),
+                    "launches": res["prewarm_launches"]},
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",

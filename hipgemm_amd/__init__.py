@@ -467,10 +467,16 @@ def fp8_gemm_bf16_rowcol(a, b_t, scale_rows=None, scale_cols=None, out=None,
     return out
 
 
-# Zero-filled workspaces for the split-K schedule, one per (device, stream):
-# calls on one stream are ordered, so they may share one; every call leaves
-# it zero-filled again.
+# Workspaces of the split-K schedules, one per (device, stream): calls on one
+# stream are ordered, so they may share one (include/hipgemm.h: the counter
+# region is zero between calls whatever schedule ran last).  A workspace is
+# never freed once created: a CUDA graph captured with it keeps its address,
+# so a smaller one stays alive (in _retired) when a larger one replaces it.
+# Growth at least doubles the size, which bounds the retired bytes by the
+# live ones.  Creating or growing one while the stream is being captured is
+# refused: the allocation and its zero fill would only be recorded, not run.
 _workspaces: dict = {}
+_retired: list = []
 
 
 def _workspace(device, stream, nbytes: int):
@@ -478,9 +484,17 @@ def _workspace(device, stream, nbytes: int):
     key = (device.index, stream.cuda_stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise HipGemmError(
+                f"a {nbytes}-byte workspace is needed on this stream while it "
+                "is being captured; run the same call once before capture so "
+                "that the workspace exists", hipErrorInvalidValue)
+        size = nbytes if ws is None else max(nbytes, 2 * ws.numel())
         with torch.cuda.stream(stream):
-            ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-        _workspaces[key] = ws
+            new = torch.zeros(size, dtype=torch.uint8, device=device)
+        if ws is not None:
+            _retired.append(ws)
+        _workspaces[key] = ws = new
     return ws
 
 

@@ -140,6 +140,15 @@ hipError_t launch_tiled(int variant, GemmArgs g, hk::Key key,
 // column tile of CfgSkinny::bn(kmb) columns (enough workgroups to give every
 // CU one), and the workspace it needs (arrival counters, then the partial
 // tiles).
+//
+// Workspace layout, shared by every schedule so that calls of different
+// schedules may share one workspace: bytes [0, HIPGEMM_WS_COUNTER_BYTES)
+// are arrival counters, zero between calls (a call that uses them leaves
+// them zero; no call writes anything else there); partial tiles start at
+// HIPGEMM_WS_COUNTER_BYTES and are fully written before they are read.
+constexpr size_t kWsCounterBytes = HIPGEMM_WS_COUNTER_BYTES;
+constexpr int kWsMaxCounters = (int)(kWsCounterBytes / sizeof(int));
+
 struct SkinnyPlan {
   int kmb, bn, tiles_n, slices, slice_steps;
   size_t counter_bytes, ws_bytes;
@@ -154,11 +163,13 @@ SkinnyPlan plan_skinny(int M, int N, int K) {
   const int target = cu_count();
   int slices = (target + p.tiles_n - 1) / p.tiles_n;
   if (slices > steps) slices = steps;
-  if (slices < 1) slices = 1;
+  // One counter per column tile: more tiles than the counter region holds
+  // (never with slices > 1 on a GPU of at most 4096 CUs) run unsplit.
+  if (slices < 1 || p.tiles_n > kWsMaxCounters) slices = 1;
   p.slice_steps = steps > 0 ? (steps + slices - 1) / slices : 0;
   p.slices = p.slice_steps > 0 ? (steps + p.slice_steps - 1) / p.slice_steps : 1;
   if (p.slices > 1) {
-    p.counter_bytes = ((size_t)p.tiles_n * sizeof(int) + 255) / 256 * 256;
+    p.counter_bytes = kWsCounterBytes;
     p.ws_bytes = p.counter_bytes + (size_t)p.tiles_n * p.slices * p.kmb * 16 *
                                        p.bn * sizeof(float);
   }
@@ -225,7 +236,9 @@ T128Plan plan_t128(int M, int N, int K, int cus) {
   if (sl < 2) return p;
   p.slices = sl;
   p.slice_steps = ss;
-  p.ws_bytes = (size_t)tiles * sl * 65536;
+  // Partial tiles after the counter region (which this schedule leaves
+  // untouched).
+  p.ws_bytes = kWsCounterBytes + (size_t)tiles * sl * 65536;
   return p;
 }
 
@@ -238,7 +251,7 @@ hipError_t launch_t128_split(GemmArgs g, const T128Plan& p, void* ws,
   g.workers = units < cus ? units : cus;
   g.split.slices = p.slices;
   g.split.slice_steps = p.slice_steps;
-  g.split.partial = static_cast<float*>(ws);
+  g.split.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWsCounterBytes);
   const void* fn = g.mx.a ? hk::tile128_split_mx(key) : hk::tile128_split(key);
   if (!fn) return hipErrorInvalidValue;
   void* args[] = {&g};
@@ -382,8 +395,15 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
       if (ws_bytes < need) return hipErrorInvalidValue;
       return go(ws);
     }
+    // No workspace given: a stream-ordered allocation (and a clear of the
+    // counters) for this call -- not while the stream is being captured,
+    // where they would be recorded into the caller's graph.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t r = hipStreamIsCapturing(stream, &cap);
+    if (r != hipSuccess) return r;
+    if (cap != hipStreamCaptureStatusNone) return hipErrorInvalidValue;
     void* tmp = nullptr;
-    hipError_t r = hipMallocAsync(&tmp, need, stream);
+    r = hipMallocAsync(&tmp, need, stream);
     if (r != hipSuccess) return r;
     if (zero > 0) r = hipMemsetAsync(tmp, 0, zero, stream);
     if (r == hipSuccess) r = go(tmp);

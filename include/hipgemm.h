@@ -45,6 +45,13 @@ extern "C" {
 
 #define HIPGEMM_VERSION 100 /* 1.0.0 */
 
+/* Workspace layout (every schedule): the first HIPGEMM_WS_COUNTER_BYTES
+ * bytes hold arrival counters that must be zero before a workspace's first
+ * use; every call leaves them zero again and writes nothing else there.
+ * Partial tiles follow; calls overwrite them before reading them.  So one
+ * workspace serves calls of every shape and schedule in turn. */
+#define HIPGEMM_WS_COUNTER_BYTES 16384
+
 /* Schedules.  AUTO picks by shape (hipgemm_select_variant). */
 enum {
   HIPGEMM_VARIANT_AUTO = 0,
@@ -182,13 +189,18 @@ hipError_t hipgemm_fp8_gemm_bf16(const void *A, const void *B_T, void *C,
  * hipgemm_fp8_gemm_bf16 with a caller-provided workspace.  A schedule that
  * needs scratch memory (hipgemm_workspace_size(M, N, K, variant) > 0: the
  * skinny split-K schedule keeps its per-tile arrival counters and fp32
- * partial tiles there) uses `workspace` instead of taking a stream-ordered
- * allocation (hipMallocAsync / hipFreeAsync) on `stream` for the call, as
- * hipgemm_fp8_gemm_bf16 does.  The workspace must be 256-byte aligned,
- * zero-filled before its first use, and at least that size; every call
- * leaves it zero-filled again.  Calls that may run concurrently must not
+ * partial tiles there, the 128 x 128 schedule's K-slices their partial
+ * tiles) uses `workspace` instead of taking a stream-ordered allocation
+ * (hipMallocAsync, a clear of the counters, hipFreeAsync) on `stream` for
+ * the call, as hipgemm_fp8_gemm_bf16 does.  The workspace must be 256-byte
+ * aligned and at least that size, and its first HIPGEMM_WS_COUNTER_BYTES
+ * bytes zero before its first use (every call leaves them zero: see
+ * HIPGEMM_WS_COUNTER_BYTES).  Calls that may run concurrently must not
  * share a workspace.  Returns hipErrorInvalidValue if it is missing or too
  * small when needed.
+ * While `stream` is being captured into a graph, an entry point that would
+ * allocate a workspace for the call (none given, one needed) returns
+ * hipErrorInvalidValue instead: pass a workspace there.
  * Replaces: the same reference launch (the reference has no workspace and no
  * split-K path).
  */

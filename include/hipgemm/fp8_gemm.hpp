@@ -12,7 +12,9 @@
 //     (fp8_4wave.hpp:334-338), launched exactly as the callers do:
 //       <<<(M * N) / (256 * 256), 256>>>      (test.cpp:79, bench.cpp:55/78)
 //     C = A . B_T^T with A M x K row-major, B_T N x K row-major (K
-//     contiguous), C M x N row-major bf16, fp32 accumulation.
+//     contiguous), C M x N row-major bf16, fp32 accumulation;
+//   * its sibling fp8_gemm_4wave_256x256x128_ref with the same signature
+//     (fp8_4wave.hpp:594-598), launched the same way.
 //
 // Behavioural differences, all on inputs where the reference is wrong or
 // undefined: any grid size >= 1 is correct (the first min(grid, 256)
@@ -64,5 +66,44 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4wave_256x256x128(
                       SplitArgs{}};
   // 16-byte epilogue stores: N a multiple of 8 (C itself must be 16-byte
   // aligned, as every hipMalloc'd buffer is).
+  gemm_4wave_body<N % 8 == 0, 16>(args, (lds_u8*)lds);
+}
+
+// The reference header's second kernel,
+//   template <int M, int N, int K> __global__ __launch_bounds__(256, 1)
+//   void fp8_gemm_4wave_256x256x128_ref(const fp8*, const fp8*, bf16*)
+// (fp8_4wave.hpp:594-598): its "simple" 4-wave kernel, one 256 x 256 tile per
+// workgroup, launched like the main one (<<<(M * N) / 65536, 256>>>).  Same
+// name, template parameters and pointer signature, so callers that name it
+// compile unchanged.  Here it is the same 4-wave schedule run without the
+// persistent worker cap: every workgroup of the caller's grid is a worker,
+// so a grid of one workgroup per tile gives each workgroup exactly one tile
+// (the reference's _ref decomposition); other grids stay correct, as for the
+// main kernel.  Output rounding is round-to-nearest-even, as in the
+// reference's _ref epilogue (fp8_4wave.hpp:693-696).
+template <int M, int N, int K>
+__global__ __launch_bounds__(256, 1) void fp8_gemm_4wave_256x256x128_ref(
+    const fp8* __restrict A, const fp8* __restrict B_T, bf16* __restrict C) {
+  static_assert(M > 0 && N > 0 && K > 0, "shape must be positive");
+  static_assert(K % 16 == 0, "K must be a multiple of 16 (16-byte rows)");
+  using namespace hipgemm::detail;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg4w::kLdsBytes];
+  constexpr int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
+  const GemmArgs args{reinterpret_cast<const uint8_t*>(A),
+                      reinterpret_cast<const uint8_t*>(B_T),
+                      reinterpret_cast<uint16_t*>(C),
+                      nullptr,
+                      nullptr,
+                      M,
+                      N,
+                      K,
+                      K,
+                      K,
+                      N,
+                      default_group_m(tiles_m, tiles_n),
+                      0,  // workers: the whole grid
+                      EpiArgs{},
+                      MxArgs{},
+                      SplitArgs{}};
   gemm_4wave_body<N % 8 == 0, 16>(args, (lds_u8*)lds);
 }

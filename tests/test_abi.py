@@ -50,13 +50,27 @@ def test_version_and_variants():
 def test_tile128_k_split_workspace():
     """The 128 x 128 schedule splits K when its tiles fill at most a quarter
     of the (256) CUs and K has 16+ steps: 256 x 4096 x 14336 is 2 x 32 tiles,
-    4 slices of 28 steps, one 64 KiB partial per (tile, slice)."""
-    assert hg.workspace_size(256, 4096, 14336, 5) == 64 * 4 * 65536
-    assert hg.workspace_size(256, 4096, 14336, 0) == 64 * 4 * 65536  # AUTO
+    4 slices of 28 steps, one 64 KiB partial per (tile, slice), after the
+    counter region every workspace starts with (HIPGEMM_WS_COUNTER_BYTES)."""
+    ctr = 16384
+    assert hg.workspace_size(256, 4096, 14336, 5) == ctr + 64 * 4 * 65536
+    assert hg.workspace_size(256, 4096, 14336, 0) == ctr + 64 * 4 * 65536  # AUTO
     assert hg.workspace_size(256, 8192, 8192, 5) == 0    # 128 tiles: no split
     assert hg.workspace_size(256, 4096, 1920, 5) == 0    # 15 steps: no split
     # 300 x 1000 x 4112: 3 x 8 tiles, 33 steps -> 4 slices of 10 steps
-    assert hg.workspace_size(300, 1000, 4112, 5) == 24 * 4 * 65536
+    assert hg.workspace_size(300, 1000, 4112, 5) == ctr + 24 * 4 * 65536
+
+
+def test_workspace_counter_region():
+    """Every schedule's workspace starts with the same counter region; the
+    skinny schedule's partial tiles follow it (128 x 8192 x 8192: 64 column
+    tiles of 128 x 4 K-slices, 64 KiB each)."""
+    ctr = 16384
+    text = open(hg._HEADER).read()
+    assert f"#define HIPGEMM_WS_COUNTER_BYTES {ctr}" in text
+    assert hg.workspace_size(128, 8192, 8192, 3) == ctr + 64 * 4 * 65536
+    # 16 rows: 32 tiles of 256 columns x 8 slices, 16 x 256 fp32 each
+    assert hg.workspace_size(16, 8192, 8192, 3) == ctr + 32 * 8 * 16384
 
 
 def test_split_columns_plan():
@@ -211,10 +225,10 @@ def test_fp4_entry_validation():
     d = hg.GemmDesc(**dict(base, M=256, N=4096, K=28672, lda=14336, ldb=14336,
                            ldc=4096))
     assert L.hipgemm_gemm_workspace_size(ctypes.byref(d)) == \
-        hg.workspace_size(256, 4096, 14336, 5) == 64 * 4 * 65536
+        hg.workspace_size(256, 4096, 14336, 5) == 16384 + 64 * 4 * 65536
     d8 = hg.GemmDesc(**dict(base, a_format=0, b_format=0, M=256, N=4096,
                             K=14336, lda=14336, ldb=14336, ldc=4096))
-    assert L.hipgemm_gemm_workspace_size(ctypes.byref(d8)) == 64 * 4 * 65536
+    assert L.hipgemm_gemm_workspace_size(ctypes.byref(d8)) == 16384 + 64 * 4 * 65536
 
 
 def test_mx_entry_validation():
