@@ -42,7 +42,7 @@ _LIB_PATH = os.path.join(_HERE, "libhipgemm.so")
 _HEADER = os.path.join(_ROOT, "include", "hipgemm.h")
 
 VARIANTS = {"auto": 0, "4wave": 1, "4wave_mfma16": 2, "skinny": 3, "8wave": 4,
-            "tile128": 5}
+            "tile128": 5, "strip": 6}
 
 # include/hipgemm.h codes
 FMT_E4M3, FMT_E5M2, FMT_FP4_E2M1 = 0, 1, 4

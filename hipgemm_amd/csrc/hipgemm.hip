@@ -205,6 +205,64 @@ hipError_t launch_skinny(const GemmArgs& a, const SkinnyPlan& p, void* ws,
                          dim3(CfgSkinny::kThreads), args, 0, stream);
 }
 
+// Plan of the column-strip schedule (gemm_strip.hpp): 16-row blocks of M,
+// strips of 16 knb columns, and K-slices per strip when the strips alone
+// give fewer workgroups than CUs (each wave keeps at least one step of a
+// slice); the workspace holds the counters and one partial strip per
+// (strip, slice).
+struct StripPlan {
+  int kmb, knb, tiles_n, slices, slice_steps;
+  size_t ws_bytes;
+};
+
+StripPlan plan_strip(int M, int N, int K, int knb) {
+  StripPlan p{};
+  p.kmb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+  p.knb = knb;
+  const int bn = 16 * knb;
+  p.tiles_n = (N + bn - 1) / bn;
+  const int steps = (K + CfgStrip::kBK - 1) / CfgStrip::kBK;
+  const int cus = cu_count();
+  int slices = (cus + p.tiles_n - 1) / p.tiles_n;
+  if (slices > steps / 4) slices = steps / 4;
+  if (slices < 1 || p.tiles_n > kWsMaxCounters) slices = 1;
+  p.slice_steps = steps > 0 ? (steps + slices - 1) / slices : 0;
+  p.slices = p.slice_steps > 0 ? (steps + p.slice_steps - 1) / p.slice_steps : 1;
+  if (p.slices > 1)
+    p.ws_bytes = kWsCounterBytes + (size_t)p.tiles_n * p.slices *
+                                       CfgStrip::partial_bytes(p.kmb, p.knb);
+  return p;
+}
+
+// The strip width.  Every strip reads all of A's rows over its K range
+// through its CU's L1, so A's share of a CU's traffic grows with M / BN:
+// 32 columns up to 32 rows, 64 above.  Measured (one process, 8192 x 8192
+// B_T): 64 rows 21.0 us with 64 columns against 21.7 with 32; 16 rows
+// 12.9 us either way.
+int strip_knb(int M, int N, int K) {
+  (void)N, (void)K;
+  return M > 32 ? 4 : 2;
+}
+
+hipError_t launch_strip(const GemmArgs& a, const StripPlan& p, void* ws,
+                        hk::Key key, hipStream_t stream) {
+  StripArgs g{a.A, a.B, a.C, a.scale_a, a.scale_b, a.M, a.N, a.K,
+              a.lda, a.ldb, a.ldc, p.slices, p.slice_steps, nullptr, nullptr,
+              a.epi};
+  if (p.slices > 1) {
+    g.arrivals = static_cast<int*>(ws);
+    g.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWsCounterBytes);
+  }
+  // One store per lane of 4 columns that never straddle N.
+  key.vec = vec_ok(key.out, a.N, a.ldc, a.C, 4);
+  const void* fn = key.ext ? hk::strip_ext(p.kmb, p.knb, key)
+                           : hk::strip_plain(p.kmb, p.knb, key);
+  if (!fn) return hipErrorInvalidValue;
+  void* args[] = {&g};
+  return hipLaunchKernel(fn, dim3(p.tiles_n * p.slices), dim3(CfgStrip::kThreads),
+                         args, 0, stream);
+}
+
 int resolve_variant(int variant, int M, int N, int K);
 
 // K-split plan of the 128 x 128 schedule: when its tiles fill at most a
@@ -310,7 +368,8 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   const int es = out_bytes(d.out_dtype);
   hipError_t e = validate(d.A, d.B_T, d.C, M, N, K, lda, ldb, d.ldc, variant, es);
   if (e != hipSuccess) return e;
-  if (variant == HIPGEMM_VARIANT_SKINNY && M > CfgSkinny::kMaxM)
+  if ((variant == HIPGEMM_VARIANT_SKINNY && M > CfgSkinny::kMaxM) ||
+      (variant == HIPGEMM_VARIANT_STRIP && M > CfgStrip::kMaxM))
     return hipErrorInvalidValue;
   void* ws = d.workspace;
   const size_t ws_bytes = d.workspace_bytes;
@@ -417,6 +476,11 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
         return launch_skinny(g, p, w, key, stream);
       });
     }
+    case HIPGEMM_VARIANT_STRIP: {
+      const StripPlan p = plan_strip(M, N, K, strip_knb(M, N, K));
+      return with_workspace(p.ws_bytes, p.slices > 1 ? kWsCounterBytes : 0,
+                            [&](void* w) { return launch_strip(g, p, w, key, stream); });
+    }
     case HIPGEMM_VARIANT_TILE128: {
       const T128Plan p = plan_t128(M, N, K, cu_count());
       if (p.slices == 1) return launch_tiled(variant, g, key, stream);
@@ -472,8 +536,13 @@ int resolve_variant(int variant, int M, int N, int K) {
 extern "C" {
 
 int hipgemm_select_variant(int M, int N, int K) {
-  // Up to 128 rows the GEMM is a stream over B_T: the split-K schedule
-  // spreads it over every CU.  Above, the 4-wave 16x16x128 schedule (1-2 %
+  // Up to 128 rows the GEMM is a stream over B_T.  Up to 64 rows the
+  // column-strip schedule (whole-line DMA of B_T, no split-K partials when
+  // N / 32 fills the CUs): 16 x 8192 x 8192 12.9 us against 17.8 on the
+  // split-K schedule, 32 rows 15.1 against 21.6, 64 rows 21.0 against 24.9.
+  // From 65 to 128 rows the split-K schedule, whose 128-column tiles read A
+  // a quarter as often as a 32-column strip (128 x 8192 x 8192: 30.8 us
+  // against 37.3 with 32 columns, 31.4 with 64).  Above, the 4-wave 16x16x128 schedule (1-2 %
   // ahead of the 8-wave one from 4096^3 up, and at 4000 x 5000 x 3584),
   // except for short K on few tiles (a fraction of one round over the CUs),
   // where the 8-wave one is 3-12 % ahead (2048^3, 512^3).  Measured on
@@ -485,6 +554,7 @@ int hipgemm_select_variant(int M, int N, int K) {
   // and 128 x 128 schedules for a short last round (hipgemm_split_columns);
   // this returns the 4-wave one then.
   (void)K;
+  if (M <= 64) return HIPGEMM_VARIANT_STRIP;
   if (M <= CfgSkinny::kMaxM) return HIPGEMM_VARIANT_SKINNY;
   if (ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN) <= cu_count())
     return HIPGEMM_VARIANT_TILE128;
@@ -580,6 +650,8 @@ size_t hipgemm_workspace_size(int M, int N, int K, int variant) {
   if (M <= 0 || N <= 0 || K < 0) return 0;
   const int v = resolve_variant(variant, M, N, K);
   if (v == HIPGEMM_VARIANT_TILE128) return plan_t128(M, N, K, cu_count()).ws_bytes;
+  if (v == HIPGEMM_VARIANT_STRIP)
+    return M > CfgStrip::kMaxM ? 0 : plan_strip(M, N, K, strip_knb(M, N, K)).ws_bytes;
   if (v != HIPGEMM_VARIANT_SKINNY) return 0;
   if (M > CfgSkinny::kMaxM) return 0;
   return plan_skinny(M, N, K).ws_bytes;
@@ -606,6 +678,8 @@ const char* hipgemm_variant_name(int variant) {
       return "8wave_256x256x128_mfma16";
     case HIPGEMM_VARIANT_TILE128:
       return "4wave_128x128x128_mfma16";
+    case HIPGEMM_VARIANT_STRIP:
+      return "strip_32_mfma16";
     default:
       return nullptr;
   }

@@ -9,6 +9,7 @@
 
 #include "hipgemm/detail/gemm_8wave.hpp"
 #include "hipgemm/detail/gemm_skinny.hpp"
+#include "hipgemm/detail/gemm_strip.hpp"
 #include "hipgemm/detail/gemm_t128.hpp"
 
 namespace hipgemm {
@@ -37,6 +38,8 @@ const void* eight_wave_ext_f16(const Key& k);       // k8wave_ext_f16.hip
 const void* skinny_plain(int kmb, const Key& k);    // kskinny_plain.hip
 const void* skinny_ext(int kmb, const Key& k);      // kskinny_ext.hip
 const void* skinny_reduce(int kf, const Key& k);    // kskinny_plain.hip
+const void* strip_plain(int kmb, int knb, const Key& k);  // kstrip_plain.hip
+const void* strip_ext(int kmb, int knb, const Key& k);    // kstrip_ext.hip
 const void* four_wave_mx(const Key& k);             // k4wave_mx.hip
 const void* tile128_mx(const Key& k);               // k4wave_mx.hip
 const void* tile128_split_mx(const Key& k);         // k4wave_mx.hip

@@ -65,7 +65,7 @@ enum {
   HIPGEMM_VARIANT_4WAVE_MFMA16 = 2,
   /* M <= 128 only: split-K over every CU for the HBM-bound skinny shapes,
    * operands streamed straight into registers, a deterministic in-kernel
-   * reduction of the K-slices.  AUTO's choice for M <= 128.  Needs a
+   * reduction of the K-slices.  AUTO's choice for 64 < M <= 128.  Needs a
    * workspace (hipgemm_workspace_size) when it splits K. */
   HIPGEMM_VARIANT_SKINNY = 3,
   /* 512 threads (8 waves, two per SIMD, in two groups that alternate
@@ -82,7 +82,14 @@ enum {
    * fit in one round over the CUs.  No reference counterpart (the reference
    * has 256 x 256 tiles only). */
   HIPGEMM_VARIANT_TILE128 = 5,
-  HIPGEMM_VARIANT_COUNT = 6
+  /* M <= 128 only: 256 threads, each workgroup a strip of 32 columns of C
+   * (64 above 32 rows) over all of K (over a K-slice, with a workspace,
+   * when the strips alone are fewer than the CUs), its 4 waves each a
+   * quarter of the K-steps, summed in LDS; B_T streamed by whole-line DMA
+   * into LDS, A straight into registers.  AUTO's choice for M <= 64.  No
+   * reference counterpart. */
+  HIPGEMM_VARIANT_STRIP = 6,
+  HIPGEMM_VARIANT_COUNT = 7
 };
 
 /* Operand formats (OCP 8-bit floating point v1.0; OCP Microscaling v1.0
@@ -247,6 +254,7 @@ hipError_t hipgemm_fp8_gemm_bf16_rowcol(const void *A, const void *B_T, void *C,
  * store_rt, :214-238, converts the accumulator straight to bf16).
  */
 hipError_t hipgemm_gemm(const hipgemm_gemm_desc *desc, hipStream_t stream);
+
 
 /*
  * MX scale packing.  hipgemm_mx_scales_bytes: bytes of the packed layout for

@@ -36,7 +36,8 @@ def test_version_and_variants():
     assert hg.variant_name(3).startswith("skinny")
     assert hg.variant_name(4).startswith("8wave")
     assert hg.variant_name(5).startswith("4wave_128x128")
-    assert hg.variant_name(6) is None
+    assert hg.variant_name(6).startswith("strip")
+    assert hg.variant_name(7) is None
     assert hg.select_variant(8192, 8192, 8192) == 2
     assert hg.select_variant(4000, 5000, 3584) == 2
     # 128 x 128 tiles in one round over the (256, without a device) CUs
@@ -44,6 +45,8 @@ def test_version_and_variants():
     assert hg.select_variant(512, 512, 512) == 5
     assert hg.select_variant(2048, 4096, 2048) == 4
     assert hg.select_variant(128, 8192, 8192) == 3
+    assert hg.select_variant(64, 8192, 8192) == 6
+    assert hg.select_variant(16, 8192, 8192) == 6
     assert hg.select_variant(129, 8192, 8192) == 5   # 2 x 64 tiles of 128
 
 
@@ -127,15 +130,20 @@ def test_workspace_size_and_validation():
     the workspace entry point rejects a missing, misaligned or short one
     before launching anything."""
     skinny = hg.VARIANTS["skinny"]
-    assert hg.select_variant(16, 8192, 8192) == skinny
+    strip = hg.VARIANTS["strip"]
+    assert hg.select_variant(100, 8192, 8192) == skinny
     assert hg.select_variant(129, 8192, 8192) != skinny
-    need = hg.workspace_size(16, 8192, 8192, 0)
+    need = hg.workspace_size(100, 8192, 8192, 0)
     assert need > 0 and need % 256 == 0
-    assert hg.workspace_size(16, 8192, 8192, skinny) == need
+    assert hg.workspace_size(100, 8192, 8192, skinny) == need
+    # The strip schedule needs none when N / 32 fills the (256) CUs, and
+    # counters plus 2 slices x 128 strips x 16 x 32 fp32 at N = 4096.
+    assert hg.workspace_size(16, 8192, 8192, 0) == 0
+    assert hg.workspace_size(16, 4096, 8192, strip) == 16384 + 2 * 128 * 2048
     assert hg.workspace_size(512, 8192, 8192, 0) == 0   # 4-wave: none
     assert hg.workspace_size(16, 300, 64, 0) == 0       # one K-step: no split
     assert hg.workspace_size(0, 8192, 8192, 0) == 0
-    args = (FAKE, FAKE, FAKE, 16, 8192, 8192, 8192, 8192, 8192, 0, 0)
+    args = (FAKE, FAKE, FAKE, 100, 8192, 8192, 8192, 8192, 8192, 0, 0)
     assert hg.gemm_raw_ws(*args, 0, 0, need) == INVALID          # no workspace
     assert hg.gemm_raw_ws(*args, 0, FAKE, need - 256) == INVALID  # too small
     assert hg.gemm_raw_ws(*args, 0, FAKE + 64, need) == INVALID   # misaligned
@@ -160,7 +168,8 @@ def test_rowcol_entry_validation():
                                   p["rows"], p["cols"], p["variant"], 0, 0, 0)
 
     for bad in (dict(rows=FAKE + 2), dict(cols=FAKE + 1),
-                dict(variant=hg.VARIANTS["4wave"]), dict(variant=6),
+                dict(variant=hg.VARIANTS["4wave"]), dict(variant=7),
+                dict(variant=hg.VARIANTS["strip"]),  # M = 300 > 128
                 dict(K=40, lda=48, ldb=48), dict(ldc=299), dict(A=0),
                 dict(variant=hg.VARIANTS["skinny"])):  # M = 300 > 128
         assert call(**bad) == INVALID, bad

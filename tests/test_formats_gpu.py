@@ -25,7 +25,7 @@ TERN = {po.FMT_E4M3: np.array([0xB8, 0x00, 0x38], np.uint8),   # -1, 0, +1
 FMTS = [(0, 0), (1, 0), (0, 1), (1, 1)]
 TILED = [pytest.param(0, id="auto"), pytest.param(2, id="mfma16"),
          pytest.param(4, id="8wave"), pytest.param(5, id="tile128")]
-ALL = TILED + [pytest.param(3, id="skinny")]
+ALL = TILED + [pytest.param(3, id="skinny"), pytest.param(6, id="strip")]
 
 
 def ternary(fmt, shape, seed):
@@ -40,7 +40,8 @@ def general(oracle, fmt, shape, seed):
 
 
 def shape_for(variant, M, N, K):
-    return (min(M, 96), N, K) if variant == hg.VARIANTS["skinny"] else (M, N, K)
+    skinny = variant in (hg.VARIANTS["skinny"], hg.VARIANTS["strip"])
+    return (min(M, 96), N, K) if skinny else (M, N, K)
 
 
 def run(torch, A, B, *, fa=0, fb=0, out=0, act=0, sa=None, sb=None, sr=None,

@@ -30,6 +30,8 @@ CANARY = {4: 0x7FA5A5A5, 1: 0xA5}
 CASES = [pytest.param(0, (520, 600, 336), id="auto"),
          pytest.param(2, (520, 600, 336), id="mfma16"),
          pytest.param(3, (96, 1000, 528), id="skinny"),
+         pytest.param(6, (96, 1000, 528), id="strip"),
+         pytest.param(6, (20, 9000, 1040), id="strip-wide"),
          pytest.param(5, (300, 520, 336), id="tile128"),
          pytest.param(5, (300, 1000, 4112), id="tile128-ksplit")]
 
@@ -118,7 +120,7 @@ def test_e4m3_conversion_pinned(gpu, oracle, variant):
     bias = np.concatenate([special, sweep]).astype(np.float32)
     N = bias.size + (-bias.size) % 8
     bias = np.pad(bias, (0, N - bias.size))
-    M, K = (64 if variant == 3 else 256), 128
+    M, K = (64 if variant in (3, 6) else 256), 128
     say(f"case [v{variant}] e4m3-pin M={M} N={N} K={K}")
     A = np.zeros((M, K), np.uint8)
     B = ternary(0, (N, K), 94)

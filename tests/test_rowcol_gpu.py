@@ -24,7 +24,7 @@ TERNARY = np.array([0xB8, 0x00, 0x38], np.uint8)  # -1, 0, +1
 # Every schedule the row/column entry point accepts (AUTO resolves per shape).
 VARIANTS = [pytest.param(0, id="auto"), pytest.param(2, id="mfma16"),
             pytest.param(4, id="8wave"), pytest.param(3, id="skinny"),
-            pytest.param(5, id="tile128")]
+            pytest.param(5, id="tile128"), pytest.param(6, id="strip")]
 
 
 def ternary(shape, seed):
@@ -50,7 +50,7 @@ def scaled_rel(C, want, sr, sc):
 
 
 def usable(variant, M):
-    return variant != hg.VARIANTS["skinny"] or M <= 128
+    return variant not in (hg.VARIANTS["skinny"], hg.VARIANTS["strip"]) or M <= 128
 
 
 def run_rowcol(torch, A, B, sr, sc, variant, ldc=None):
@@ -102,7 +102,7 @@ def test_rowcol_ternary_bit_exact(gpu, oracle, M, N, K, variant):
 def test_rowcol_one_side_null(gpu, oracle, variant, which):
     """A NULL vector means all ones: equal to the oracle with that vector
     omitted, and with both NULL equal to the unscaled per-tensor oracle."""
-    M, N, K = (96, 700, 528) if variant == 3 else (320, 700, 528)
+    M, N, K = (96, 700, 528) if variant in (3, 6) else (320, 700, 528)
     say(f"case [v{variant}] rowcol-null-{which} M={M} N={N} K={K} seed=45")
     A, B = ternary((M, K), 45), ternary((N, K), 46)
     sr = scales(M, 47) if which == "rows" else None
@@ -144,7 +144,7 @@ def test_rowcol_special_scales(gpu, oracle, variant):
     """Zero, huge and tiny scales: products that overflow to inf, 0 * inf =
     NaN where the sum is zero, subnormal products -- bit-exact with ternary
     inputs, NaN positions included."""
-    M, N, K = (64, 300, 272) if variant == 3 else (300, 300, 272)
+    M, N, K = (64, 300, 272) if variant in (3, 6) else (300, 300, 272)
     say(f"case [v{variant}] rowcol-special M={M} N={N} K={K} seed=52")
     A, B = ternary((M, K), 52), ternary((N, K), 53)
     # 2^-126 * 0.25 and 2^-130 (itself subnormal) give subnormal products

@@ -1,5 +1,6 @@
-"""GPU parity of the skinny split-K schedule (HIPGEMM_VARIANT_SKINNY, M <= 128)
-against the CPU oracle, through the C ABI.
+"""GPU parity of the skinny schedules (M <= 128) against the CPU oracle, through
+the C ABI: the split-K schedule (HIPGEMM_VARIANT_SKINNY) and the column-strip
+schedule (HIPGEMM_VARIANT_STRIP).
 
 The schedule sums K-slices in a fixed order, so results are deterministic but
 not the sequential fp32 sum: general inputs are checked with the north_star
@@ -16,6 +17,8 @@ from util import REL_TOL, compare, from_dev_bf16, say, scale_tensor, to_dev
 pytestmark = pytest.mark.gpu
 
 SKINNY = hg.VARIANTS["skinny"]
+STRIP = hg.VARIANTS["strip"]
+BOTH = [pytest.param(SKINNY, id="splitk"), pytest.param(STRIP, id="strip")]
 CANARY = 0x7FA5
 TERNARY = np.array([0xB8, 0x00, 0x38], np.uint8)  # -1, 0, +1
 
@@ -50,30 +53,34 @@ def run_ws(torch, A, B, M, N, K, ldc=None, sa=None, sb=None, variant=SKINNY,
     return np.ascontiguousarray(got[2:M + 2, :N]), guard, ws
 
 
+@pytest.mark.parametrize("variant", BOTH)
 @pytest.mark.parametrize("M,N,K", [
     (1, 300, 16), (16, 8192, 8192), (17, 1000, 272), (33, 4100, 1040),
-    (64, 512, 4096), (100, 2050, 528), (128, 8192, 8192), (5, 260, 8192)])
-def test_skinny_ternary_bit_exact(gpu, oracle, M, N, K):
+    (64, 512, 4096), (100, 2050, 528), (128, 8192, 8192), (5, 260, 8192),
+    (32, 8192, 8192), (128, 2048, 8192), (20, 16384, 1024), (48, 70, 4112)])
+def test_skinny_ternary_bit_exact(gpu, oracle, M, N, K, variant):
     torch = gpu
-    say(f"case skinny-ternary M={M} N={N} K={K} seed=21 "
-        f"ws={hg.workspace_size(M, N, K, SKINNY)}")
+    say(f"case skinny-ternary [v{variant}] M={M} N={N} K={K} seed=21 "
+        f"ws={hg.workspace_size(M, N, K, variant)}")
     A, B = ternary((M, K), 21), ternary((N, K), 22)
     ldc = N + 12 if N % 4 else N + 8  # N % 4 != 0 takes the 2-byte stores
-    C, guard, _ = run_ws(torch, A, B, M, N, K, ldc=ldc, sa=0.5, sb=4.0)
+    C, guard, _ = run_ws(torch, A, B, M, N, K, ldc=ldc, sa=0.5, sb=4.0,
+                         variant=variant)
     assert guard, "write outside M x N"
     want = oracle.gemm(A, B, 0.5, 4.0)
     assert np.array_equal(C, want)
 
 
+@pytest.mark.parametrize("variant", BOTH)
 @pytest.mark.parametrize("M,N,K", [(16, 8192, 8192), (128, 8192, 8192),
-                                   (40, 3000, 2064)])
-def test_skinny_uniform_within_tolerance(gpu, oracle, M, N, K):
+                                   (40, 3000, 2064), (64, 28672, 4096)])
+def test_skinny_uniform_within_tolerance(gpu, oracle, M, N, K, variant):
     torch = gpu
     sa, sb = oracle.draw_scale(51), oracle.draw_scale(52)
-    say(f"case skinny-uniform M={M} N={N} K={K} seed=5 sa={sa} sb={sb}")
+    say(f"case skinny-uniform [v{variant}] M={M} N={N} K={K} seed=5 sa={sa} sb={sb}")
     A = oracle.fill((M, K), 5001, po.UNIFORM, -1.0, 1.0)
     B = oracle.fill((N, K), 5002, po.UNIFORM, -1.0, 1.0)
-    C, guard, _ = run_ws(torch, A, B, M, N, K, sa=sa, sb=sb)
+    C, guard, _ = run_ws(torch, A, B, M, N, K, sa=sa, sb=sb, variant=variant)
     assert guard
     max_rel, exact, _ = compare(C, oracle.gemm(A, B, sa, sb))
     say(f"    max_rel={max_rel:.3e} exact={exact:.6f}")
@@ -102,12 +109,13 @@ def test_skinny_deterministic_and_workspace_left_zero(gpu, oracle):
 
 def test_skinny_plain_entry_allocates_its_workspace(gpu, oracle):
     """hipgemm_fp8_gemm_bf16 (no workspace argument) takes a stream-ordered
-    allocation for the split-K schedule; AUTO picks that schedule for
-    M <= 128; the result equals the workspace entry point's."""
+    allocation for a schedule that splits K (AUTO picks the strip schedule
+    for M <= 64, here with 4 K-slices); the result equals the workspace
+    entry point's."""
     torch = gpu
     M, N, K = 16, 2048, 4096
     say(f"case skinny-plain M={M} N={N} K={K}")
-    assert hg.select_variant(M, N, K) == SKINNY
+    assert hg.select_variant(M, N, K) == STRIP
     A = oracle.fill((M, K), 71, po.UNIFORM, -1.0, 1.0)
     B = oracle.fill((N, K), 72, po.UNIFORM, -1.0, 1.0)
     a, b = to_dev(torch, A), to_dev(torch, B)
@@ -117,7 +125,8 @@ def test_skinny_plain_entry_allocates_its_workspace(gpu, oracle):
                        torch.cuda.current_stream().cuda_stream)
     assert code == 0
     torch.cuda.synchronize()
-    C_ws, _, _ = run_ws(torch, A, B, M, N, K)
+    assert hg.workspace_size(M, N, K, 0) > 0
+    C_ws, _, _ = run_ws(torch, A, B, M, N, K, variant=STRIP)
     assert np.array_equal(from_dev_bf16(out), C_ws)
 
 

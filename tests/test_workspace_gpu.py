@@ -42,13 +42,17 @@ def test_one_workspace_prefill_then_decode(gpu, oracle):
         rows = np.array([0, 1, 127, 128, 200, 255], np.int32)
         assert np.array_equal(from_dev_bf16(out)[rows],
                               oracle.gemm_rows(A, B, rows, 1.0, 1.0))
-        # Then the skinny schedule's in-kernel reduction (arrival counters)
-        # on the same stream, hence the same workspace.
-        for M2 in (16, 32, 16):
-            M2, N2, K2 = M2, 8192, 8192
-            say(f"case ws-shared decode {M2}x{N2}x{K2}")
+        # Then in-kernel reductions with arrival counters on the same
+        # stream, hence the same workspace: the split-K schedule (16, 32
+        # rows) and the strip schedule with K-slices (4096 columns).
+        for M2, N2, K2, v in ((16, 8192, 8192, 3), (32, 8192, 8192, 3),
+                              (16, 4096, 8192, 6), (16, 8192, 8192, 3),
+                              (48, 2048, 8192, 6)):
+            say(f"case ws-shared decode {M2}x{N2}x{K2} variant {v}")
+            assert hg.workspace_size(M2, N2, K2, v) > 16384
             A2, B2 = ternary((M2, K2), 93), ternary((N2, K2), 94)
-            out2 = hg.fp8_gemm_bf16(to_dev(torch, A2), to_dev(torch, B2))
+            out2 = hg.fp8_gemm_bf16(to_dev(torch, A2), to_dev(torch, B2),
+                                    variant=v)
             torch.cuda.synchronize()
             assert np.array_equal(from_dev_bf16(out2), oracle.gemm(A2, B2))
 
