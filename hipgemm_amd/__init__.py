@@ -31,7 +31,7 @@ __all__ = [
     "variant_name", "version", "tile_order", "lds_slot", "VARIANTS",
     "declared_symbols", "gemm_raw_ws", "workspace_size",
     "fp8_gemm_bf16_rowcol", "gemm_raw_rowcol", "GemmDesc", "gemm_desc_raw",
-    "gemm", "FMT_E4M3", "FMT_E5M2", "FMT_FP4_E2M1", "OUT_BF16", "OUT_F16", "OUT_F32",
+    "gemm", "gemm_desc_noalloc_raw", "FMT_E4M3", "FMT_E5M2", "FMT_FP4_E2M1", "OUT_BF16", "OUT_F16", "OUT_F32",
     "OUT_FP8_E4M3", "ACTIVATIONS",
     "mx_scales_bytes", "mx_pack_scales",
 ]
@@ -127,6 +127,8 @@ def lib() -> ctypes.CDLL:
     L.hipgemm_fp8_gemm_bf16_rowcol.restype = ci
     L.hipgemm_gemm.argtypes = [ctypes.POINTER(GemmDesc), vp]
     L.hipgemm_gemm.restype = ci
+    L.hipgemm_gemm_noalloc.argtypes = [ctypes.POINTER(GemmDesc), vp]
+    L.hipgemm_gemm_noalloc.restype = ci
     L.hipgemm_mx_scales_bytes.argtypes = [ci, ci]
     L.hipgemm_mx_scales_bytes.restype = ctypes.c_size_t
     L.hipgemm_mx_pack_scales.argtypes = [vp, ci, ci, ci, vp, vp]
@@ -202,6 +204,12 @@ def gemm_raw_rowcol(a_ptr: int, b_ptr: int, c_ptr: int, M: int, N: int,
 def gemm_desc_raw(desc: "GemmDesc", stream: int = 0) -> int:
     """Call hipgemm_gemm; returns hipError_t."""
     return int(lib().hipgemm_gemm(ctypes.byref(desc), stream or None))
+
+
+def gemm_desc_noalloc_raw(desc: "GemmDesc", stream: int = 0) -> int:
+    """Call hipgemm_gemm_noalloc (the library's static per-GPU scratch
+    instead of a workspace; desc.workspace must be 0); returns hipError_t."""
+    return int(lib().hipgemm_gemm_noalloc(ctypes.byref(desc), stream or None))
 
 
 def mx_scales_bytes(rows: int, K: int) -> int:

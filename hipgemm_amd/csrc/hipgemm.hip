@@ -8,8 +8,25 @@
 
 #include <atomic>
 #include <cstdint>
+#include <mutex>
 
 #include "kernels.hpp"
+
+// Scratch memory of hipgemm_gemm_noalloc: a static device array, one copy
+// per GPU the library runs on, held until the process ends (no allocation
+// call ever creates or frees it).  Laid out as any workspace: arrival
+// counters first (zero between calls), then partial tiles.  Host code never
+// uses this name as an address: its per-device address comes from
+// hipGetSymbolAddress (scratch_on_device below).
+static __device__ __align__(256) uint8_t scratch[HIPGEMM_NOALLOC_SCRATCH_BYTES];
+
+// Clears n 4-byte words (the scratch counters at first use on a device): a
+// kernel, not a memset, so that it may also be recorded into a graph.
+__global__ void clear_words(uint32_t* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
 
 namespace {
 
@@ -348,11 +365,48 @@ int split_columns(int M, int N, int cus) {
 
 bool valid_code(int v, int count) { return v >= 0 && v < count; }
 
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) on its first use; at that first use the
+// counter region is also cleared on `stream`, ahead of the call that needs
+// it (the array is zero-initialised when the code object is loaded; the
+// clear makes that explicit).  Returns nullptr with *err set on failure.
+void* scratch_on_device(hipStream_t stream, hipError_t* err) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<void*> ptrs[kMaxDevices];
+  static std::mutex init;
+  int dev = 0;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  void* p = ptrs[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  std::lock_guard<std::mutex> lock(init);
+  p = ptrs[dev].load(std::memory_order_relaxed);
+  if (p) return p;
+  *err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (*err != hipSuccess || !p) {
+    if (*err == hipSuccess) *err = hipErrorInvalidSymbol;
+    return nullptr;
+  }
+  const int words = (int)(HIPGEMM_WS_COUNTER_BYTES / sizeof(uint32_t));
+  uint32_t* w = static_cast<uint32_t*>(p);
+  void* args[] = {&w, (void*)&words};
+  *err = hipLaunchKernel((const void*)clear_words, dim3(16), dim3(256), args,
+                         0, stream);
+  if (*err != hipSuccess) return nullptr;
+  ptrs[dev].store(p, std::memory_order_release);
+  return p;
+}
+
 // Shared body of the GEMM entry points.  `ws` may be null when `ws_given` is
 // false: a schedule that needs a workspace then takes a stream-ordered
 // allocation for the call.
+// dry_run: validate only, launch nothing.
 hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
-                    hipStream_t stream) {
+                    hipStream_t stream, bool dry_run = false) {
   int M = d.M, N = d.N, K = d.K, lda = d.lda, ldb = d.ldb, variant = d.variant;
   if (!valid_code(d.out_dtype, 4)) return hipErrorInvalidValue;
   // fp4 operands: both, K a multiple of 32 elements, the 128 x 128
@@ -445,6 +499,7 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   key.ext = ext;
   key.act = d.activation;
   key.out = d.out_dtype;
+  if (dry_run) return hipSuccess;
   // A schedule that needs `need` bytes of workspace (the first `zero` of
   // them zero-filled): the caller's, or a stream-ordered allocation for the
   // call.
@@ -644,6 +699,27 @@ size_t hipgemm_gemm_workspace_size(const hipgemm_gemm_desc* d) {
                : 0;
   }
   return hipgemm_workspace_size(d->M, d->N, d->K, d->variant);
+}
+
+hipError_t hipgemm_gemm_noalloc(const hipgemm_gemm_desc* desc,
+                                hipStream_t stream) {
+  if (!desc || desc->size != sizeof(hipgemm_gemm_desc) || desc->workspace ||
+      desc->workspace_bytes)
+    return hipErrorInvalidValue;
+  const size_t need = hipgemm_gemm_workspace_size(desc);
+  if (need > (size_t)HIPGEMM_NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;
+  hipgemm_gemm_desc d = *desc;
+  if (need > 0) {
+    // Argument errors come back before the scratch is touched.
+    hipError_t e = run_gemm(d, false, stream, true);
+    if (e != hipSuccess) return e;
+    d.workspace = scratch_on_device(stream, &e);
+    if (!d.workspace) return e;
+    d.workspace_bytes = HIPGEMM_NOALLOC_SCRATCH_BYTES;
+  }
+  // need == 0: no schedule on this path uses a workspace (none is given,
+  // so none can be allocated either).
+  return run_gemm(d, true, stream);
 }
 
 size_t hipgemm_workspace_size(int M, int N, int K, int variant) {

@@ -255,6 +255,29 @@ hipError_t hipgemm_fp8_gemm_bf16_rowcol(const void *A, const void *B_T, void *C,
  */
 hipError_t hipgemm_gemm(const hipgemm_gemm_desc *desc, hipStream_t stream);
 
+/*
+ * hipgemm_gemm that allocates nothing: schedules that need scratch memory
+ * (the skinny schedule's split-K counters and partial tiles, the 128 x 128
+ * schedule's K-slices) use a static device array of the library,
+ * HIPGEMM_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on that
+ * GPU until the process ends; no call makes an allocation or a memset.
+ * desc->workspace must be NULL and desc->workspace_bytes 0.  Returns
+ * hipErrorInvalidValue when the descriptor is invalid (as hipgemm_gemm) or
+ * when the call would need more scratch than HIPGEMM_NOALLOC_SCRATCH_BYTES
+ * (hipgemm_gemm_workspace_size(desc) tells; never on MI355X, whose largest
+ * need is 32 MiB plus the counter region).  Every call on one GPU shares
+ * that GPU's array and leaves its counters at zero: calls on one stream
+ * are ordered, but calls that may overlap on one GPU (other streams,
+ * threads or processes' graphs replayed concurrently) race on it.  Its
+ * first call on a GPU looks the array's address up (hipGetSymbolAddress)
+ * and clears its counters with a kernel on `stream`.
+ * No reference counterpart (the reference's kernel needs no scratch).  For
+ * callers that cannot allocate device memory: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.
+ */
+#define HIPGEMM_NOALLOC_SCRATCH_BYTES (HIPGEMM_WS_COUNTER_BYTES + (32u << 20))
+hipError_t hipgemm_gemm_noalloc(const hipgemm_gemm_desc *desc,
+                                hipStream_t stream);
 
 /*
  * MX scale packing.  hipgemm_mx_scales_bytes: bytes of the packed layout for
