@@ -31,7 +31,8 @@ __all__ = [
     "variant_name", "version", "tile_order", "lds_slot", "VARIANTS",
     "declared_symbols", "gemm_raw_ws", "workspace_size",
     "fp8_gemm_bf16_rowcol", "gemm_raw_rowcol", "GemmDesc", "gemm_desc_raw",
-    "gemm", "gemm_desc_noalloc_raw", "FMT_E4M3", "FMT_E5M2", "FMT_FP4_E2M1", "OUT_BF16", "OUT_F16", "OUT_F32",
+    "gemm", "gemm_desc_noalloc_raw", "FMT_E4M3", "FMT_E5M2", "FMT_FP6_E2M3",
+    "FMT_FP6_E3M2", "FMT_FP4_E2M1", "OUT_BF16", "OUT_F16", "OUT_F32",
     "OUT_FP8_E4M3", "ACTIVATIONS",
     "mx_scales_bytes", "mx_pack_scales",
 ]
@@ -45,7 +46,7 @@ VARIANTS = {"auto": 0, "4wave": 1, "4wave_mfma16": 2, "skinny": 3, "8wave": 4,
             "tile128": 5, "strip": 6}
 
 # include/hipgemm.h codes
-FMT_E4M3, FMT_E5M2, FMT_FP4_E2M1 = 0, 1, 4
+FMT_E4M3, FMT_E5M2, FMT_FP6_E2M3, FMT_FP6_E3M2, FMT_FP4_E2M1 = 0, 1, 2, 3, 4
 OUT_BF16, OUT_F16, OUT_F32, OUT_FP8_E4M3 = 0, 1, 2, 3
 ACTIVATIONS = {None: 0, "none": 0, "relu": 1, "gelu_tanh": 2, "silu": 3}
 
@@ -432,6 +433,12 @@ def gemm(a, b_t, *, a_format: int = FMT_E4M3, b_format: int = FMT_E4M3,
         out, variant, stream, out_dtype)
     if a_format == FMT_FP4_E2M1 or b_format == FMT_FP4_E2M1:
         K *= 2  # elements: two per byte
+    elif a_format in (FMT_FP6_E2M3, FMT_FP6_E3M2):
+        if K % 3:
+            raise HipGemmError("fp6 operands hold 4 elements per 3 bytes: the "
+                               "row length in bytes must be a multiple of 3",
+                               hipErrorInvalidValue)
+        K = K // 3 * 4  # elements: four per three bytes
     d = GemmDesc(A=a.data_ptr(), B_T=b_t.data_ptr(), C=out.data_ptr(), M=M,
                  N=N, K=K, lda=lda, ldb=ldb, ldc=ldc, a_format=a_format,
                  b_format=b_format,

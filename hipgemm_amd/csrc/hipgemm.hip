@@ -296,11 +296,12 @@ struct T128Plan {
   size_t ws_bytes = 0;
 };
 
-T128Plan plan_t128(int M, int N, int K, int cus) {
+// step_bytes: bytes of a row per K-step (96 for fp6 operands, else 128).
+T128Plan plan_t128(int M, int N, int K, int cus, int step_bytes = CfgT128::kBK) {
   T128Plan p;
   const int tiles = ((M + CfgT128::kBM - 1) / CfgT128::kBM) *
                     ((N + CfgT128::kBN - 1) / CfgT128::kBN);
-  const int steps = (K + CfgT128::kBK - 1) / CfgT128::kBK;
+  const int steps = (K + step_bytes - 1) / step_bytes;
   p.slice_steps = steps;
   if (tiles <= 0 || 4 * tiles > cus || steps < 16) return p;
   int sl = cus / tiles < steps / 8 ? cus / tiles : steps / 8;
@@ -410,14 +411,26 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   int M = d.M, N = d.N, K = d.K, lda = d.lda, ldb = d.ldb, variant = d.variant;
   if (!valid_code(d.out_dtype, 4)) return hipErrorInvalidValue;
   // fp4 operands: both, K a multiple of 32 elements, the 128 x 128
-  // schedule; from here on K counts bytes of a row (K / 2).
+  // schedule; from here on K counts bytes of a row (K / 2).  fp6 operands:
+  // both (either variant each), K a multiple of 64 elements (48 bytes), the
+  // 128 x 128 schedule; K counts bytes (3 K / 4).
   const bool fp4 = d.a_format == HIPGEMM_FMT_FP4_E2M1 ||
                    d.b_format == HIPGEMM_FMT_FP4_E2M1;
+  auto is6 = [](int f) {
+    return f == HIPGEMM_FMT_FP6_E2M3 || f == HIPGEMM_FMT_FP6_E3M2;
+  };
+  const bool fp6 = is6(d.a_format) || is6(d.b_format);
   if (fp4) {
     if (d.a_format != d.b_format || K % 32 != 0 ||
         (variant != HIPGEMM_VARIANT_AUTO && variant != HIPGEMM_VARIANT_TILE128))
       return hipErrorInvalidValue;
     K /= 2;
+  }
+  if (fp6) {
+    if (!is6(d.a_format) || !is6(d.b_format) || K % 64 != 0 ||
+        (variant != HIPGEMM_VARIANT_AUTO && variant != HIPGEMM_VARIANT_TILE128))
+      return hipErrorInvalidValue;
+    K = K / 4 * 3;
   }
   const int es = out_bytes(d.out_dtype);
   hipError_t e = validate(d.A, d.B_T, d.C, M, N, K, lda, ldb, d.ldc, variant, es);
@@ -429,7 +442,7 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   const size_t ws_bytes = d.workspace_bytes;
   if (ws_given && ws_bytes > 0 && (!ws || !aligned(ws, 256)))
     return hipErrorInvalidValue;
-  if ((!fp4 && (!valid_code(d.a_format, 2) || !valid_code(d.b_format, 2))) ||
+  if ((!fp4 && !fp6 && (!valid_code(d.a_format, 2) || !valid_code(d.b_format, 2))) ||
       !valid_code(d.activation, 4))
     return hipErrorInvalidValue;
   // The output scale belongs to the e4m3 output; fp32 / e4m3 outputs are not
@@ -445,7 +458,10 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   const bool ext = d.scale_rows || d.scale_cols || d.bias ||
                    d.activation != HIPGEMM_ACT_NONE ||
                    d.out_dtype != HIPGEMM_OUT_BF16;
-  const int fmt = fp4 ? kFmtPairFp4 : d.a_format | (d.b_format << 1);
+  const int fmt = fp4   ? kFmtPairFp4
+                  : fp6 ? kFmtPairFp6 + (d.a_format == HIPGEMM_FMT_FP6_E3M2) +
+                              2 * (d.b_format == HIPGEMM_FMT_FP6_E3M2)
+                        : d.a_format | (d.b_format << 1);
   // The 32x32x64 schedule is built for e4m3 x e4m3 with the per-tensor
   // epilogue only.
   if (variant == HIPGEMM_VARIANT_4WAVE && (ext || fmt != 0))
@@ -453,16 +469,16 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   // MX block scales: the 4-wave 16x16x128 and 128 x 128 schedules,
   // per-tensor epilogue (K in elements a multiple of 32: bytes of 16 for fp4).
   const bool mx = d.mx_scale_a || d.mx_scale_b;
-  if (mx && (!d.mx_scale_a || !d.mx_scale_b || K % (fp4 ? 16 : 32) != 0 || ext ||
+  if (mx && (fp6 || !d.mx_scale_a || !d.mx_scale_b || K % (fp4 ? 16 : 32) != 0 || ext ||
              !aligned(d.mx_scale_a, 16) || !aligned(d.mx_scale_b, 16) ||
              (variant != HIPGEMM_VARIANT_AUTO &&
               variant != HIPGEMM_VARIANT_4WAVE_MFMA16 &&
               variant != HIPGEMM_VARIANT_TILE128)))
     return hipErrorInvalidValue;
-  const int n1 = (variant == HIPGEMM_VARIANT_AUTO && !mx && !fp4 && K > 0)
+  const int n1 = (variant == HIPGEMM_VARIANT_AUTO && !mx && !fp4 && !fp6 && K > 0)
                      ? split_columns(M, N, cu_count())
                      : 0;
-  variant = fp4 ? HIPGEMM_VARIANT_TILE128 : resolve_variant(variant, M, N, K);
+  variant = fp4 || fp6 ? HIPGEMM_VARIANT_TILE128 : resolve_variant(variant, M, N, K);
   // MX: the 128 x 128 schedule where AUTO picks it, else the 4-wave one.
   if (mx && variant != HIPGEMM_VARIANT_TILE128) variant = HIPGEMM_VARIANT_4WAVE_MFMA16;
   if (variant == HIPGEMM_VARIANT_8WAVE && d.out_dtype >= HIPGEMM_OUT_F32)
@@ -537,7 +553,7 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
                             [&](void* w) { return launch_strip(g, p, w, key, stream); });
     }
     case HIPGEMM_VARIANT_TILE128: {
-      const T128Plan p = plan_t128(M, N, K, cu_count());
+      const T128Plan p = plan_t128(M, N, K, cu_count(), fp6 ? 96 : CfgT128::kBK);
       if (p.slices == 1) return launch_tiled(variant, g, key, stream);
       return with_workspace(p.ws_bytes, 0, [&](void* w) {
         return launch_t128_split(g, p, w, key, stream);
@@ -692,6 +708,9 @@ size_t hipgemm_gemm_workspace_size(const hipgemm_gemm_desc* d) {
   const bool fp4 = d->a_format == HIPGEMM_FMT_FP4_E2M1 ||
                    d->b_format == HIPGEMM_FMT_FP4_E2M1;
   if (fp4) return plan_t128(d->M, d->N, d->K / 2, cu_count()).ws_bytes;
+  const bool fp6 = d->a_format == HIPGEMM_FMT_FP6_E2M3 ||
+                   d->a_format == HIPGEMM_FMT_FP6_E3M2;
+  if (fp6) return plan_t128(d->M, d->N, d->K / 4 * 3, cu_count(), 96).ws_bytes;
   if (d->mx_scale_a || d->mx_scale_b) {  // 128 x 128 where AUTO picks it
     const int v = resolve_variant(d->variant, d->M, d->N, d->K);
     return v == HIPGEMM_VARIANT_TILE128

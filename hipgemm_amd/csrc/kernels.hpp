@@ -74,6 +74,18 @@ const void* sel_fmt(int v, F&& f) {
     default: return nullptr;
   }
 }
+// The 128 x 128 schedule's pairs: those of sel_fmt and fp6 x fp6
+// (kFmtPairFp6 + 0..3).
+template <class F>
+const void* sel_fmt_t128(int v, F&& f) {
+  switch (v) {
+    case 8: return f(ic<8>{});
+    case 9: return f(ic<9>{});
+    case 10: return f(ic<10>{});
+    case 11: return f(ic<11>{});
+    default: return sel_fmt(v, f);
+  }
+}
 template <class F>
 const void* sel4(int v, F&& f) {
   switch (v) {

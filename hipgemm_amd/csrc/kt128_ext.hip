@@ -18,7 +18,7 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm_t128_ext(GemmArgs g) {
 }  // namespace
 
 const void* tile128_ext_narrow(const Key& k) {
-  return sel_fmt(k.fmt, [&](auto F) {
+  return sel_fmt_t128(k.fmt, [&](auto F) {
     return sel4(k.act, [&](auto A) {
       return sel2(k.out, [&](auto O) {
         return sel2(k.vec, [&](auto V) {

@@ -1,5 +1,5 @@
 // The 128 x 128-tile schedule with the per-tensor epilogue, for every
-// operand-format pair.
+// operand-format pair (fp4 x fp4 and fp6 x fp6 included).
 #include "kernels.hpp"
 
 namespace hipgemm {
@@ -30,7 +30,7 @@ __global__ __launch_bounds__(64) void k_fp8_gemm_t128_reduce(GemmArgs g) {
 }  // namespace
 
 const void* tile128_split(const Key& k) {
-  return sel_fmt(k.fmt, [&](auto F) {
+  return sel_fmt_t128(k.fmt, [&](auto F) {
     return (const void*)&k_fp8_gemm_t128_split<decltype(F)::value>;
   });
 }
@@ -45,7 +45,7 @@ const void* tile128_reduce(const Key& k) {
 }
 
 const void* tile128_plain(const Key& k) {
-  return sel_fmt(k.fmt, [&](auto F) {
+  return sel_fmt_t128(k.fmt, [&](auto F) {
     return sel2(k.vec, [&](auto V) {
       return (const void*)&k_fp8_gemm_t128<decltype(V)::value == 1, decltype(F)::value>;
     });

@@ -93,15 +93,24 @@ enum {
 };
 
 /* Operand formats (OCP 8-bit floating point v1.0; OCP Microscaling v1.0
- * for E2M1).  FP4_E2M1: 1 sign, 2 exponent (bias 1), 1 mantissa bit --
- * 0, 0.5, 1, 1.5, 2, 3, 4, 6 and their negatives -- two per byte, element
- * 2i in the low nibble of byte i of a row; A and B_T both FP4_E2M1 (not
- * mixed with the 8-bit formats), K (in elements) a multiple of 32, lda /
- * ldb in bytes (>= K / 2), schedules AUTO and TILE128. */
+ * for E2M3, E3M2 and E2M1).  FP4_E2M1: 1 sign, 2 exponent (bias 1), 1
+ * mantissa bit -- 0, 0.5, 1, 1.5, 2, 3, 4, 6 and their negatives -- two per
+ * byte, element 2i in the low nibble of byte i of a row; A and B_T both
+ * FP4_E2M1 (not mixed with the other formats), K (in elements) a multiple
+ * of 32, lda / ldb in bytes (>= K / 2), schedules AUTO and TILE128.
+ * FP6_E2M3 (1 sign, 2 exponent bits, bias 1, 3 mantissa bits; largest 7.5)
+ * and FP6_E3M2 (1 sign, 3 exponent bits, bias 3, 2 mantissa bits; largest
+ * 28), no inf or NaN: four per three bytes, packed LSB first -- element k
+ * of a row is bits [6k, 6k + 6) of the row read as one little-endian bit
+ * string; A and B_T both fp6 (either variant each), K (in elements) a
+ * multiple of 64, lda / ldb in bytes (>= 3K / 4, multiples of 16),
+ * schedules AUTO and TILE128, no MX block scales. */
 enum {
-  HIPGEMM_FMT_E4M3 = 0,    /* E4M3FN: bias 7, max 448, NaN 0x7F/0xFF, no inf */
-  HIPGEMM_FMT_E5M2 = 1,    /* E5M2: bias 15, max 57344, IEEE inf and NaN     */
-  HIPGEMM_FMT_FP4_E2M1 = 4 /* E2M1: max 6, no inf or NaN                      */
+  HIPGEMM_FMT_E4M3 = 0,     /* E4M3FN: bias 7, max 448, NaN 0x7F/0xFF, no inf */
+  HIPGEMM_FMT_E5M2 = 1,     /* E5M2: bias 15, max 57344, IEEE inf and NaN     */
+  HIPGEMM_FMT_FP6_E2M3 = 2, /* E2M3: max 7.5, no inf or NaN                   */
+  HIPGEMM_FMT_FP6_E3M2 = 3, /* E3M2: max 28, no inf or NaN                    */
+  HIPGEMM_FMT_FP4_E2M1 = 4  /* E2M1: max 6, no inf or NaN                     */
 };
 
 /* Output types of hipgemm_gemm.  BF16, F16: round to nearest even; F32: the

@@ -100,15 +100,22 @@ __device__ __forceinline__ i32x8 join(i32x4 lo, i32x4 hi) {
 }
 
 // Operand formats of the f8f6f4 MFMA family (its cbsz / blgp immediates):
-// OCP E4M3 (fp8), OCP E5M2 (bf8) and OCP E2M1 (fp4, two per byte).
-constexpr int kFmtE4M3 = 0, kFmtE5M2 = 1, kFmtFp4 = 4;
+// OCP E4M3 (fp8), OCP E5M2 (bf8), OCP E2M3 and E3M2 (fp6, four per three
+// bytes) and OCP E2M1 (fp4, two per byte).
+constexpr int kFmtE4M3 = 0, kFmtE5M2 = 1, kFmtFp6E2M3 = 2, kFmtFp6E3M2 = 3,
+              kFmtFp4 = 4;
 // A kernel's operand-format pair kFmt: 0-3, bit 0 the 8-bit format of A,
-// bit 1 that of B_T (0 = e4m3 x e4m3); kFmtPairFp4, fp4 x fp4.
+// bit 1 that of B_T (0 = e4m3 x e4m3); kFmtPairFp4, fp4 x fp4;
+// kFmtPairFp6 + 0-3, fp6 x fp6, bit 0 set for E3M2 A, bit 1 for E3M2 B_T.
 constexpr int kFmtPairFp4 = 4;
+constexpr int kFmtPairFp6 = 8;
 __host__ __device__ constexpr bool is_fp4(int f) { return f == kFmtPairFp4; }
-__host__ __device__ constexpr int fmt_a(int f) { return is_fp4(f) ? kFmtFp4 : f & 1; }
+__host__ __device__ constexpr bool is_fp6(int f) { return (f & ~3) == kFmtPairFp6; }
+__host__ __device__ constexpr int fmt_a(int f) {
+  return is_fp4(f) ? kFmtFp4 : is_fp6(f) ? kFmtFp6E2M3 + (f & 1) : f & 1;
+}
 __host__ __device__ constexpr int fmt_b(int f) {
-  return is_fp4(f) ? kFmtFp4 : (f >> 1) & 1;
+  return is_fp4(f) ? kFmtFp4 : is_fp6(f) ? kFmtFp6E2M3 + ((f >> 1) & 1) : (f >> 1) & 1;
 }
 
 // D[32x32] += X[32x64] . Y[32x64]^T -> fp32, X in format kFx, Y in kFy.

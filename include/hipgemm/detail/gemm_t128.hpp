@@ -77,6 +77,12 @@ template <bool kVec, bool kExt = false, int kFmt = 0, int kAct = kActNone,
 __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   using Cfg = CfgT128;
   constexpr int S = Cfg::kStages;
+  // fp6 operands: a step is 128 elements, 96 bytes of a row (one MFMA per
+  // block), held in LDS slots 0-5 of the 128-byte row (slots 6 and 7 stay
+  // unfetched).  Other formats: 128 bytes.
+  constexpr bool k6 = is_fp6(kFmt);
+  constexpr int kStepBytes = k6 ? 96 : Cfg::kBK;
+  static_assert(!(k6 && kMx), "MX: 8-bit and fp4 operands");
   constexpr int kDma = Cfg::kDmaPerStep;       // DMA per wave per step
   constexpr int kD = kDma + (kMx ? 2 : 0);     // memory operations per step
   static_assert(!(kMx && kExt), "MX: per-tensor epilogue");
@@ -96,7 +102,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   const int tiles_n = (N + Cfg::kBN - 1) / Cfg::kBN;
   const int tiles = tiles_m * tiles_n;
   const int units = kSplit ? tiles * g.split.slices : tiles;
-  const int steps = kSplit ? g.split.slice_steps : (K + Cfg::kBK - 1) / Cfg::kBK;
+  const int steps = kSplit ? g.split.slice_steps : (K + kStepBytes - 1) / kStepBytes;
   const int steps_pad = max(S, (steps + 1) & ~1);
   const int workers = g.workers > 0 ? min((int)gridDim.x, g.workers)
                                     : (int)gridDim.x;
@@ -141,12 +147,12 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
     const TileCoord c = grouped_tile(tile, tiles_m, tiles_n, g.group_m);
     const int ra = min(Cfg::kBM, M - c.m * Cfg::kBM);
     const int rb = min(Cfg::kBN, N - c.n * Cfg::kBN);
-    const int k0 = slice * steps * Cfg::kBK;
+    const int k0 = slice * steps * kStepBytes;
     return Src{make_rsrc(g.A + (size_t)c.m * Cfg::kBM * g.lda,
                          (uint32_t)ra * (uint32_t)g.lda),
                make_rsrc(g.B + (size_t)c.n * Cfg::kBN * g.ldb,
                          (uint32_t)rb * (uint32_t)g.ldb),
-               (uint32_t)k0, min(K, k0 + steps * Cfg::kBK), c.m, c.n};
+               (uint32_t)k0, min(K, k0 + steps * kStepBytes), c.m, c.n};
   };
   Src cur = src_of(t);
   Src nxt = src_of(t + walk.stride);
@@ -157,9 +163,9 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   auto dma_one = [&](int d, int stage, int n) {
     const bool next = d >= steps_pad;
     const Src& s = next ? nxt : cur;
-    uint32_t k0 = s.k0 + (uint32_t)(next ? d - steps_pad : d) * Cfg::kBK;
+    uint32_t k0 = s.k0 + (uint32_t)(next ? d - steps_pad : d) * kStepBytes;
     asm volatile("" : "+s"(k0));
-    const bool ok = (int)(k0 + dchunk * 16) < s.kend;
+    const bool ok = (int)(k0 + dchunk * 16) < s.kend && (!k6 || dchunk < 6);
     lds_u8* base = lds + stage * Cfg::kStage;
     const int q = n & 3;
     if (n < 4)
@@ -180,6 +186,28 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   const uint32_t off_a = (uint32_t)((wm * 64 + r16) * Cfg::kBK + rslot * 16);
   const uint32_t off_b =
       (uint32_t)(Cfg::kAStage + (wn * 64 + r16) * Cfg::kBK + rslot * 16);
+  // fp6: lane group g holds elements 32 g .. 32 g + 31 of the step, bytes
+  // 24 g .. 24 g + 23 (element boundaries fall on multiples of 3 bytes), as
+  // three 8-byte LDS reads; piece p (byte b = 24 g + 8 p) of row r sits in
+  // slot (b / 16) ^ slot_xor(r), half (b / 8) % 2.  Each 32-lane half of a
+  // read covers 32 distinct 8-byte bank groups (the rows' slots differ per
+  // parity, the two lane groups' halves differ): conflict-free.
+  const uint32_t row_a = (uint32_t)((wm * 64 + r16) * Cfg::kBK);
+  const uint32_t row_b = (uint32_t)(Cfg::kAStage + (wn * 64 + r16) * Cfg::kBK);
+  uint32_t p6[3];
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    const int b = 24 * grp + 8 * q;
+    p6[q] = (uint32_t)((((b >> 4) ^ slot_xor(r16)) << 4) + (((b >> 3) & 1) << 3));
+  }
+  // Row offset of fragment f of a step (0: A0, 1-4: B0-B3, 5-7: A1-A3).
+  auto frag_row = [&](int f) -> uint32_t {
+    return f == 0 ? row_a : f <= 4 ? row_b + (f - 1) * 16 * Cfg::kBK
+                                   : row_a + (f - 4) * 16 * Cfg::kBK;
+  };
+  auto join6 = [](u32x2 a, u32x2 b, u32x2 c) {
+    return i32x8{(int)a.x, (int)a.y, (int)b.x, (int)b.y, (int)c.x, (int)c.y, 0, 0};
+  };
   i32x8 fa[2][4], fb[2][4];
   // kMx: the lane's 16 scale bytes of A and of B_T for the step of each
   // register set (see mx_load).
@@ -213,6 +241,18 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   };
   auto read_step = [&](int stage, int set) {
     const lds_u8* base = lds + stage * Cfg::kStage;
+    if constexpr (k6) {
+#pragma unroll
+      for (int f = 0; f < 8; ++f) {
+        const lds_u8* r = base + frag_row(f);
+        const i32x8 v = join6(lds_read8(r + p6[0]), lds_read8(r + p6[1]),
+                              lds_read8(r + p6[2]));
+        if (f == 0) fa[set][0] = v;
+        else if (f <= 4) fb[set][f - 1] = v;
+        else fa[set][f - 4] = v;
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t o = off_a + i * 16 * Cfg::kBK;
@@ -234,6 +274,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   auto step = [&](int set, int rstage, int d, int dstage) {
     const lds_u8* rb = lds + rstage * Cfg::kStage;
     i32x4 rd[16];
+    u32x2 rd6[24];
     // kMx: this wave's scale words of the step (fp4: halves 0 and 1; 8-bit:
     // half `set` of the pair), chosen once.
     uint32_t wa0 = 0, wa1 = 0, wb0 = 0, wb1 = 0;
@@ -278,13 +319,27 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
                                                              acc[i][j]);
       }
       // read n: fragment f (0: A0, 1-4: B0-B3, 5-7: A1-A3), half n % 2
+      // (fp6: pieces 0 and 1 for even n, piece 2 for odd n)
       const int f = n / 2;
-      const uint32_t o = f == 0   ? off_a
-                         : f <= 4 ? off_b + (f - 1) * 16 * Cfg::kBK
-                                  : off_a + (f - 4) * 16 * Cfg::kBK;
-      rd[n] = lds_read16(rb + ((n & 1) ? (o ^ 64u) : o));
+      if constexpr (k6) {
+        const lds_u8* r = rb + frag_row(f);
+        if ((n & 1) == 0) {
+          rd6[3 * f] = lds_read8(r + p6[0]);
+          rd6[3 * f + 1] = lds_read8(r + p6[1]);
+        } else {
+          rd6[3 * f + 2] = lds_read8(r + p6[2]);
+        }
+      } else {
+        const uint32_t o = f == 0   ? off_a
+                           : f <= 4 ? off_b + (f - 1) * 16 * Cfg::kBK
+                                    : off_a + (f - 4) * 16 * Cfg::kBK;
+        rd[n] = lds_read16(rb + ((n & 1) ? (o ^ 64u) : o));
+      }
       __builtin_amdgcn_sched_group_barrier(0x008, is_fp4(kFmt) ? 2 : 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (k6 && (n & 1) == 0)
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      else
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       if (n < 8) {
         dma_one(d, dstage, n);
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
@@ -297,6 +352,16 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
     // every DMA issued before them.
     if constexpr (kMx) mx_load(d - (S - 3), set);
     const int o = set ^ 1;
+    if constexpr (k6) {
+      fa[o][0] = join6(rd6[0], rd6[1], rd6[2]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        fb[o][j] = join6(rd6[3 + 3 * j], rd6[4 + 3 * j], rd6[5 + 3 * j]);
+#pragma unroll
+      for (int i = 1; i < 4; ++i)
+        fa[o][i] = join6(rd6[12 + 3 * i], rd6[13 + 3 * i], rd6[14 + 3 * i]);
+      return;
+    }
     fa[o][0] = join(rd[0], rd[1]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) fb[o][j] = join(rd[2 + 2 * j], rd[3 + 2 * j]);

@@ -236,6 +236,8 @@ float hg_draw_scale(uint64_t seed, double lo, double hi) {
 static float g_e4m3_lut[256];
 static float g_e5m2_lut[256];
 static float g_fp4_lut[256];   /* indexed by a nibble value 0..15 */
+static float g_e2m3_lut[256];  /* indexed by a 6-bit code 0..63 */
+static float g_e3m2_lut[256];
 static int g_lut_ready = 0;
 
 static void lut_init(void) {
@@ -247,6 +249,8 @@ static void lut_init(void) {
         g_e4m3_lut[i] = hg_e4m3_to_f32((uint8_t)i);
         g_e5m2_lut[i] = hg_e5m2_to_f32((uint8_t)i);
         g_fp4_lut[i] = hg_fp4_to_f32((uint8_t)(i & 15));
+        g_e2m3_lut[i] = hg_fp6_e2m3_to_f32((uint8_t)(i & 63));
+        g_e3m2_lut[i] = hg_fp6_e3m2_to_f32((uint8_t)(i & 63));
       }
       g_lut_ready = 1;
     }
@@ -255,7 +259,11 @@ static void lut_init(void) {
 
 static const float *lut_of(int fmt) {
   lut_init();
-  return fmt == HG_FMT_E5M2 ? g_e5m2_lut : fmt == HG_FMT_FP4 ? g_fp4_lut : g_e4m3_lut;
+  return fmt == HG_FMT_E5M2        ? g_e5m2_lut
+         : fmt == HG_FMT_FP4       ? g_fp4_lut
+         : fmt == HG_FMT_FP6_E2M3  ? g_e2m3_lut
+         : fmt == HG_FMT_FP6_E3M2  ? g_e3m2_lut
+                                   : g_e4m3_lut;
 }
 
 static inline uint16_t epilogue(float acc, float s) {
@@ -339,6 +347,40 @@ float hg_fp4_to_f32(uint8_t v) {
   return (v & 8) ? -mag : mag;
 }
 
+/* OCP FP6 (OCP Microscaling v1.0).  E2M3: 1 sign bit (5), 2 exponent bits
+ * (4:3, bias 1), 3 mantissa bits (2:0); exponent field 0 is subnormal,
+ * m / 8.  Largest 7.5.  E3M2: 1 sign bit (5), 3 exponent bits (4:2, bias 3),
+ * 2 mantissa bits (1:0); exponent field 0 is subnormal, m / 16.  Largest 28.
+ * Neither has Inf or NaN; the low 6 bits of v are the code. */
+float hg_fp6_e2m3_to_f32(uint8_t v) {
+  const int e = (v >> 3) & 3, m = v & 7;
+  const float mag = e == 0 ? 0.125f * (float)m : ldexpf(1.0f + 0.125f * (float)m, e - 1);
+  return (v & 32) ? -mag : mag;
+}
+float hg_fp6_e3m2_to_f32(uint8_t v) {
+  const int e = (v >> 2) & 7, m = v & 3;
+  const float mag = e == 0 ? 0.0625f * (float)m : ldexpf(1.0f + 0.25f * (float)m, e - 3);
+  return (v & 32) ? -mag : mag;
+}
+
+/* rows x K fp6 elements packed LSB first, element k of a row at bits
+ * [6k, 6k + 6) of the row's little-endian bit string (four elements in
+ * three bytes: element 4j + t in bits 6t .. 6t + 5 of bytes 3j .. 3j + 2
+ * read as a 24-bit little-endian word), row stride ld bytes -> rows x K
+ * bytes, one 6-bit code each. */
+static uint8_t *unpack_fp6(const uint8_t *X, int rows, int K, int ld) {
+  uint8_t *u = (uint8_t *)malloc((size_t)(rows > 0 ? rows : 1) * (K > 0 ? K : 1));
+  if (!u) abort();
+  for (int r = 0; r < rows; ++r)
+    for (int k = 0; k < K; ++k) {
+      const size_t bit = (size_t)6 * k;
+      const uint8_t *p = X + (size_t)r * ld + bit / 8;
+      const unsigned w = (unsigned)p[0] | ((bit % 8) > 2 ? (unsigned)p[1] << 8 : 0u);
+      u[(size_t)r * K + k] = (uint8_t)((w >> (bit % 8)) & 63u);
+    }
+  return u;
+}
+
 /* rows x K fp4 elements, two per byte (element 2i in the low nibble of byte
  * i of a row, row stride ld bytes) -> rows x K bytes, one nibble each. */
 static uint8_t *unpack_fp4(const uint8_t *X, int rows, int K, int ld) {
@@ -349,6 +391,22 @@ static uint8_t *unpack_fp4(const uint8_t *X, int rows, int K, int ld) {
       const uint8_t b = X[(size_t)r * ld + k / 2];
       u[(size_t)r * K + k] = (k & 1) ? (uint8_t)(b >> 4) : (uint8_t)(b & 15);
     }
+  return u;
+}
+
+/* Operand X of `rows` rows in format fmt: for fp4 and fp6 an unpacked copy,
+ * one code per byte (*X and *ld updated, the copy returned for freeing);
+ * NULL and no change for the 8-bit formats. */
+static uint8_t *unpack_sub8(const uint8_t **X, int fmt, int rows, int K, int *ld) {
+  uint8_t *u = NULL;
+  if (fmt == HG_FMT_FP4)
+    u = unpack_fp4(*X, rows, K, *ld);
+  else if (fmt == HG_FMT_FP6_E2M3 || fmt == HG_FMT_FP6_E3M2)
+    u = unpack_fp6(*X, rows, K, *ld);
+  if (u) {
+    *X = u;
+    *ld = K;
+  }
   return u;
 }
 
@@ -441,18 +499,9 @@ void hg_gemm_ex(const uint8_t *A, const uint8_t *B_T, void *C, int M,
                 int out, int act, float scale_a, float scale_b,
                 const float *scale_rows, const float *scale_cols,
                 const float *bias, float scale_out) {
-  /* fp4: one byte per element (the nibble), then the same path. */
-  uint8_t *Au = NULL, *Bu = NULL;
-  if (a_fmt == HG_FMT_FP4) {
-    Au = unpack_fp4(A, M, K, lda);
-    A = Au;
-    lda = K;
-  }
-  if (b_fmt == HG_FMT_FP4) {
-    Bu = unpack_fp4(B_T, N, K, ldb);
-    B_T = Bu;
-    ldb = K;
-  }
+  /* fp4 / fp6: one byte per element (the code), then the same path. */
+  uint8_t *Au = unpack_sub8(&A, a_fmt, M, K, &lda);
+  uint8_t *Bu = unpack_sub8(&B_T, b_fmt, N, K, &ldb);
   float *Bt = decode_bt_fmt(B_T, N, K, ldb, b_fmt);
   int *rows = (int *)malloc((size_t)(M > 0 ? M : 1) * sizeof(int));
   if (!Bt || !rows) abort();
@@ -484,18 +533,9 @@ void hg_gemm_mx(const uint8_t *A, const uint8_t *B_T, uint16_t *C, int M,
                 const uint8_t *sa, int ldsa, const uint8_t *sb, int ldsb,
                 float scale_a, float scale_b) {
   const float *la = lut_of(a_fmt), *lb = lut_of(b_fmt);
-  /* fp4: one byte per element (the nibble), as in hg_gemm_ex. */
-  uint8_t *Au = NULL, *Bu = NULL;
-  if (a_fmt == HG_FMT_FP4) {
-    Au = unpack_fp4(A, M, K, lda);
-    A = Au;
-    lda = K;
-  }
-  if (b_fmt == HG_FMT_FP4) {
-    Bu = unpack_fp4(B_T, N, K, ldb);
-    B_T = Bu;
-    ldb = K;
-  }
+  /* fp4 / fp6: one byte per element (the code), as in hg_gemm_ex. */
+  uint8_t *Au = unpack_sub8(&A, a_fmt, M, K, &lda);
+  uint8_t *Bu = unpack_sub8(&B_T, b_fmt, N, K, &ldb);
   float *Af = (float *)malloc((size_t)(M > 0 ? M : 1) * (K > 0 ? K : 1) * sizeof(float));
   float *Bt = (float *)malloc((size_t)(N > 0 ? N : 1) * (K > 0 ? K : 1) * sizeof(float));
   if (!Af || !Bt) abort();

@@ -111,12 +111,22 @@ void hg_gemm_rows_f64(const uint8_t *A, const uint8_t *B_T, double *acc_rows,
                       int ldb);
 
 /* ---- Extensions beyond the reference: other formats, fused epilogue ----- */
-enum { HG_FMT_E4M3 = 0, HG_FMT_E5M2 = 1, HG_FMT_FP4 = 4 };
+enum { HG_FMT_E4M3 = 0, HG_FMT_E5M2 = 1, HG_FMT_FP6_E2M3 = 2,
+       HG_FMT_FP6_E3M2 = 3, HG_FMT_FP4 = 4 };
 /* OCP E2M1 (FP4) decode of the low nibble of v; hg_gemm_ex takes fp4
  * operands (both) as two elements per byte, element 2i in the low nibble of
  * byte i, lda / ldb in bytes.  Pinned: the decode against the OCP MX v1.0
  * value table; the GEMM against fp64 sums of the decoded values. */
 float hg_fp4_to_f32(uint8_t v);
+/* OCP FP6 (MX v1.0) decodes of the low 6 bits of v: E2M3 (bias 1, largest
+ * 7.5) and E3M2 (bias 3, largest 28), no Inf or NaN.  hg_gemm_ex / hg_gemm_mx
+ * take fp6 operands (both fp6, either variant each) packed LSB first: element
+ * k of a row at bits [6k, 6k + 6) of the row's little-endian bit string
+ * (4 elements per 3 bytes), lda / ldb in bytes.  Pinned: the decodes against
+ * the OCP value tables written out; the unpacking against a bit-string
+ * restatement in numpy; the GEMM against fp64 sums (tests/test_oracle.py). */
+float hg_fp6_e2m3_to_f32(uint8_t v);
+float hg_fp6_e3m2_to_f32(uint8_t v);
 enum { HG_OUT_BF16 = 0, HG_OUT_F16 = 1, HG_OUT_F32 = 2, HG_OUT_FP8 = 3 };
 enum { HG_ACT_NONE = 0, HG_ACT_RELU = 1, HG_ACT_GELU_TANH = 2, HG_ACT_SILU = 3 };
 /* OCP E5M2 decode (exact) and RNE encode (overflow to inf, NaN -> NaN),

@@ -24,7 +24,19 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 UNIFORM = 0
 NORMAL = 1
 # hg_gemm_ex codes (oracle.h; the values of include/hipgemm.h's)
-FMT_E4M3, FMT_E5M2, FMT_FP4 = 0, 1, 4
+FMT_E4M3, FMT_E5M2, FMT_FP6_E2M3, FMT_FP6_E3M2, FMT_FP4 = 0, 1, 2, 3, 4
+FP6 = (FMT_FP6_E2M3, FMT_FP6_E3M2)
+
+
+def k_elements(fmt: int, row_bytes: int) -> int:
+    """Elements in a packed row of row_bytes bytes: fp4 two per byte, fp6
+    four per three bytes, the 8-bit formats one per byte."""
+    if fmt == FMT_FP4:
+        return 2 * row_bytes
+    if fmt in FP6:
+        assert row_bytes % 3 == 0
+        return row_bytes * 4 // 3
+    return row_bytes
 OUT_BF16, OUT_F16, OUT_F32, OUT_FP8 = 0, 1, 2, 3
 ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3
 
@@ -63,6 +75,9 @@ class Oracle:
             getattr(L, name).restype = None
         L.hg_fp4_to_f32.argtypes = [ctypes.c_uint8]
         L.hg_fp4_to_f32.restype = ctypes.c_float
+        for name in ("hg_fp6_e2m3_to_f32", "hg_fp6_e3m2_to_f32"):
+            getattr(L, name).argtypes = [ctypes.c_uint8]
+            getattr(L, name).restype = ctypes.c_float
         L.hg_rand64.restype = ctypes.c_uint64
         L.hg_rand64.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
         L.hg_fill_e4m3.argtypes = [_vp, ctypes.c_size_t, ctypes.c_uint64,
@@ -145,6 +160,14 @@ class Oracle:
                          np.asarray(nibbles).reshape(-1)],
                         np.float32).reshape(np.shape(nibbles))
 
+    def fp6_to_f32(self, codes: np.ndarray, fmt: int) -> np.ndarray:
+        """OCP FP6 values of 6-bit codes 0..63 (hg_fp6_e2m3_to_f32 /
+        hg_fp6_e3m2_to_f32)."""
+        fn = (self.lib.hg_fp6_e2m3_to_f32 if fmt == FMT_FP6_E2M3
+              else self.lib.hg_fp6_e3m2_to_f32)
+        return np.array([fn(int(v) & 63) for v in np.asarray(codes).reshape(-1)],
+                        np.float32).reshape(np.shape(codes))
+
     def decode(self, x: np.ndarray, fmt: int) -> np.ndarray:
         """fp32 values of 8-bit operands in format fmt (FMT_E4M3 / FMT_E5M2)."""
         return self.e5m2_to_f32(x) if fmt == FMT_E5M2 else self.e4m3_to_f32(x)
@@ -214,14 +237,16 @@ class Oracle:
         """Output bits of the hipgemm_gemm semantics (oracle.h: hg_gemm_ex):
         uint16 (bf16 / f16), uint32 (fp32 bits) or uint8 (e4m3).  fp4
         operands (a_fmt = b_fmt = FMT_FP4): A and B hold K / 2 bytes per
-        row, two elements per byte."""
+        row, two elements per byte; fp6 operands (both in FP6, either
+        variant): 3 K / 4 bytes per row, packed LSB first."""
         A = np.ascontiguousarray(A)
         B = np.ascontiguousarray(B)
         M, Kb = A.shape
         N = B.shape[0]
         assert B.shape[1] == Kb
         assert (a_fmt == FMT_FP4) == (b_fmt == FMT_FP4)
-        K = 2 * Kb if a_fmt == FMT_FP4 else Kb
+        assert (a_fmt in FP6) == (b_fmt in FP6)
+        K = k_elements(a_fmt, Kb)
 
         def vec(v, n):
             if v is None:
@@ -249,7 +274,8 @@ class Oracle:
         M, Kb = A.shape
         N = B.shape[0]
         assert (a_fmt == FMT_FP4) == (b_fmt == FMT_FP4)
-        K = 2 * Kb if a_fmt == FMT_FP4 else Kb
+        assert (a_fmt in FP6) == (b_fmt in FP6)
+        K = k_elements(a_fmt, Kb)
         kb = (K + 31) // 32
         sa = np.ascontiguousarray(sa, np.uint8)
         sb = np.ascontiguousarray(sb, np.uint8)

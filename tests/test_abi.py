@@ -240,6 +240,26 @@ def test_fp4_entry_validation():
     assert L.hipgemm_gemm_workspace_size(ctypes.byref(d8)) == 16384 + 64 * 4 * 65536
 
 
+def test_fp6_entry_validation():
+    """fp6 operands: both fp6 (either variant each), K (elements) a multiple
+    of 64, lda / ldb in bytes >= 3K / 4, AUTO or the 128 x 128 schedule, no
+    MX scales; the descriptor's workspace query plans the 128 x 128
+    schedule on 96-byte steps of 3K / 4 bytes."""
+    base = dict(A=FAKE, B_T=FAKE, C=FAKE, M=300, N=300, K=256, lda=192,
+                ldb=192, ldc=300, a_format=2, b_format=3)
+    assert hg.gemm_desc_raw(hg.GemmDesc(**dict(base, M=0))) == 0
+    for bad in (dict(b_format=0), dict(a_format=1), dict(a_format=4),
+                dict(K=224), dict(lda=176), dict(variant=2), dict(variant=3),
+                dict(variant=6), dict(mx_scale_a=FAKE, mx_scale_b=FAKE)):
+        assert hg.gemm_desc_raw(hg.GemmDesc(**dict(base, **bad))) == INVALID, bad
+    L = hg.lib()
+    # 256 x 2048 x 3072 elements = 2304 bytes per row: 2 x 16 tiles of 128,
+    # 24 steps of 96 bytes -> 3 slices of 8 steps
+    d = hg.GemmDesc(**dict(base, M=256, N=2048, K=3072, lda=2304, ldb=2304,
+                           ldc=2048))
+    assert L.hipgemm_gemm_workspace_size(ctypes.byref(d)) == 16384 + 32 * 3 * 65536
+
+
 def test_mx_entry_validation():
     """MX block scales: packed size, packing arguments, and the descriptor
     rules (both scales, K % 32, 16-byte alignment, no extended epilogue,

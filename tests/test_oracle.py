@@ -505,3 +505,75 @@ def test_fp4_decode_and_gemm_pinned(oracle):
     # bf16 output of the same sums: the bf16 rounding of the fp32 values
     assert np.array_equal(oracle.gemm_ex(A, B, a_fmt=4, b_fmt=4),
                           oracle.f32_to_bf16(want))
+
+
+# OCP Microscaling v1.0, FP6 value tables (magnitudes of codes 0..31, the
+# sign bit is 0x20), written out from the spec's definitions, not computed:
+# E2M3: exponent bias 1, 3 mantissa bits, subnormals m/8; E3M2: bias 3,
+# 2 mantissa bits, subnormals m/16.
+E2M3_TABLE = [0.0, 0.125, 0.25, 0.375, 0.5, 0.625, 0.75, 0.875,
+              1.0, 1.125, 1.25, 1.375, 1.5, 1.625, 1.75, 1.875,
+              2.0, 2.25, 2.5, 2.75, 3.0, 3.25, 3.5, 3.75,
+              4.0, 4.5, 5.0, 5.5, 6.0, 6.5, 7.0, 7.5]
+E3M2_TABLE = [0.0, 0.0625, 0.125, 0.1875, 0.25, 0.3125, 0.375, 0.4375,
+              0.5, 0.625, 0.75, 0.875, 1.0, 1.25, 1.5, 1.75,
+              2.0, 2.5, 3.0, 3.5, 4.0, 5.0, 6.0, 7.0,
+              8.0, 10.0, 12.0, 14.0, 16.0, 20.0, 24.0, 28.0]
+
+
+def fp6_unpack_bits(X: np.ndarray) -> np.ndarray:
+    """The packing rule restated on the bit string: element k of a row is
+    bits [6k, 6k + 6) of the row's bytes read as one little-endian bit
+    string (bit 0 = the low bit of byte 0)."""
+    bits = np.unpackbits(X, axis=1, bitorder="little")
+    k = bits.shape[1] // 6
+    b = bits[:, :6 * k].reshape(X.shape[0], k, 6).astype(np.uint8)
+    return (b * (1 << np.arange(6, dtype=np.uint8))).sum(axis=2).astype(np.uint8)
+
+
+@pytest.mark.parametrize("fmt,table", [(po.FMT_FP6_E2M3, E2M3_TABLE),
+                                       (po.FMT_FP6_E3M2, E3M2_TABLE)],
+                         ids=["e2m3", "e3m2"])
+def test_fp6_decode_pinned(oracle, fmt, table):
+    got = oracle.fp6_to_f32(np.arange(64), fmt)
+    assert list(got[:32]) == table and list(-got[32:]) == table
+    assert np.signbit(got[32])  # 0x20 is -0
+    # only the low 6 bits count
+    assert np.array_equal(oracle.fp6_to_f32(np.arange(64) + 64, fmt), got)
+
+
+@pytest.mark.parametrize("fa,fb", [(2, 2), (3, 3), (2, 3), (3, 2)])
+def test_fp6_gemm_pinned(oracle, fa, fb):
+    """The fp6 GEMM against fp64 sums of the table values of the codes the
+    bits-string restatement unpacks (exact: products are multiples of 2^-8
+    below 2^10, and these sums stay below 2^15).  Plausible packing slips
+    change the result: each 3-byte group read big-endian, or the four codes
+    of a group taken MSB first in one operand only (in both it is a common
+    permutation of K, which leaves the sums alone)."""
+    rng = np.random.default_rng(67)
+    M, N, K = 33, 21, 256
+    A = rng.integers(0, 256, (M, 3 * K // 4)).astype(np.uint8)
+    B = rng.integers(0, 256, (N, 3 * K // 4)).astype(np.uint8)
+    ta = np.array(E2M3_TABLE if fa == 2 else E3M2_TABLE, np.float64)
+    tb = np.array(E2M3_TABLE if fb == 2 else E3M2_TABLE, np.float64)
+    val = lambda t, c: np.where(c & 32, -t[c & 31], t[c & 31])
+    want = val(ta, fp6_unpack_bits(A)) @ val(tb, fp6_unpack_bits(B)).T
+    assert np.all(np.abs(want) < 2 ** 15)
+    C = oracle.gemm_ex(A, B, a_fmt=fa, b_fmt=fb, out=po.OUT_F32)
+    assert np.array_equal(C.view(np.float32), want.astype(np.float32))
+    def codes(X, big_endian=False, msb_first=False):
+        w = X.reshape(X.shape[0], -1, 3).astype(np.uint32)
+        if big_endian:
+            w = w[..., ::-1]
+        w = w[..., 0] | (w[..., 1] << 8) | (w[..., 2] << 16)
+        sh = [18 - 6 * t if msb_first else 6 * t for t in range(4)]
+        return np.stack([(w >> s) & 63 for s in sh], axis=2).reshape(
+            X.shape[0], -1).astype(np.uint8)
+    assert np.array_equal(codes(A), fp6_unpack_bits(A))
+    for ka, kb in [(dict(big_endian=True), dict(big_endian=True)),
+                   (dict(msb_first=True), {})]:
+        wrong = val(ta, codes(A, **ka)) @ val(tb, codes(B, **kb)).T
+        assert not np.array_equal(wrong.astype(np.float32), C.view(np.float32))
+    # bf16 output of the same sums
+    assert np.array_equal(oracle.gemm_ex(A, B, a_fmt=fa, b_fmt=fb),
+                          oracle.f32_to_bf16(want.astype(np.float32)))
