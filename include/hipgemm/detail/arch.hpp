@@ -176,6 +176,20 @@ __device__ __forceinline__ float acc_read(float a) {
   asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
   return v;
 }
+// 128-bit buffer store followed by two wait states.  A v_accvgpr_read (the
+// inline asm of acc_read, which the compiler's hazard check does not pad)
+// that overwrites a data VGPR of the store in the very next cycle has been
+// measured on gfx950 to replace that dword in some lanes with the new value.
+// The nop is volatile asm, which the compiler keeps in order with every
+// memory access and every other volatile asm, so each acc_read that follows
+// the store in program order also follows the nop.
+template <int kAux>
+__device__ __forceinline__ void store_b128(i32x4 v, __amdgpu_buffer_rsrc_t rsrc,
+                                           uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, voff, soff, kAux);
+  asm volatile("s_nop 1" ::: "memory");
+}
+
 // 32 wait states, issued in place: covers the MFMA-result-to-VALU-read
 // latency ahead of the first acc_read after an MFMA.
 __device__ __forceinline__ void mfma_drain() {

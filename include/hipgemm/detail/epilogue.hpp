@@ -242,8 +242,7 @@ __device__ __forceinline__ void store_out4(const EpiVec<kBR, kBC>& ev, float a0,
   const f32x4 v = ev.template value4<kActAny>(a0, a1, a2, a3, bi, bj);
   if (ev.out == kOutF32) {
     if constexpr (kVec) {
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), rsrc,
-                                             off | oob(c), 0, 0);
+      store_b128<0>(__builtin_bit_cast(i32x4, v), rsrc, off | oob(c), 0);
     } else {
       const i32x4 vb = __builtin_bit_cast(i32x4, v);  // whole-vector bit_cast
 #pragma unroll

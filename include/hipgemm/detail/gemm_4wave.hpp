@@ -745,9 +745,8 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
           int row8 = 32 * i + 8 * p;
           asm volatile("" : "+s"(row8));  // recompute per store, never hoist
           const int srow = __builtin_amdgcn_readfirstlane((wm * 128 + row8) * g.ldc);
-          __builtin_amdgcn_raw_buffer_store_b128(
-              v[p], rsrc_c, vcol | col_oob | oob_unless(row8 + rsub, rows_left), srow,
-              kStoreC);
+          store_b128<kStoreC>(
+              v[p], rsrc_c, vcol | col_oob | oob_unless(row8 + rsub, rows_left), srow);
         }
         compiler_fence();
         sched_fence();
@@ -773,9 +772,9 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                                                    i, j);
           if constexpr (kOut == kOutF32) {
             if constexpr (kVecStore) {
-              __builtin_amdgcn_raw_buffer_store_b128(
+              store_b128<kStoreC>(
                   __builtin_bit_cast(i32x4, v), rsrc_c,
-                  (vrow | oob_unless(c, cols_left)) + 16 * j * es, srow, kStoreC);
+                  (vrow | oob_unless(c, cols_left)) + 16 * j * es, srow);
             } else {
 #pragma unroll
               for (int e = 0; e < 4; ++e)
@@ -822,9 +821,9 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
           asm volatile("" : "+s"(row4));  // recompute per store, never hoist
           const int srow =
               __builtin_amdgcn_readfirstlane((wm * 128 + row4) * g.ldc * 2);
-          __builtin_amdgcn_raw_buffer_store_b128(
+          store_b128<kStoreC>(
               v[p], rsrc_c, vcol | col_oob | oob_unless(row4 + rsub, rows_left),
-              srow, kStoreC);
+              srow);
         }
       };
       if constexpr (k16) {
@@ -853,9 +852,9 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
           asm volatile("" : "+s"(row4));  // recompute per store, never hoist
           const int srow =
               __builtin_amdgcn_readfirstlane((wm * 128 + row4) * g.ldc * 2);
-          __builtin_amdgcn_raw_buffer_store_b128(
+          store_b128<kStoreC>(
               v, rsrc_c, vcol | col_oob | oob_unless(row4 + rsub, rows_left),
-              srow, kStoreC);
+              srow);
         };
 #pragma unroll
         for (int ii = 0; ii < 2; ++ii) {

@@ -292,9 +292,9 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
           asm volatile("" : "+s"(row8));
           const int srow =
               __builtin_amdgcn_readfirstlane((wm * 128 + row8) * g.ldc * 2);
-          __builtin_amdgcn_raw_buffer_store_b128(
+          store_b128<kStoreC>(
               v[p], rsrc_c, vcol | col_oob | oob_unless(row8 + rsub, rows_left),
-              srow, kStoreC);
+              srow);
         }
         compiler_fence();
         sched_fence();

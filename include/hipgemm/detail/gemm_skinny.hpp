@@ -270,8 +270,8 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
       for (int f = 0; f < kF; ++f) {
         const f32x4 v{acc_read(acc[m][f][0]), acc_read(acc[m][f][1]),
                       acc_read(acc[m][f][2]), acc_read(acc[m][f][3])};
-        __builtin_amdgcn_raw_buffer_store_b128(
-            __builtin_bit_cast(i32x4, v), rsrc_p, slot(m, f), mine, kCoherent);
+        store_b128<kCoherent>(
+            __builtin_bit_cast(i32x4, v), rsrc_p, slot(m, f), mine);
       }
     if (g.reduce_pass) return;
     wait_vmcnt<0>();

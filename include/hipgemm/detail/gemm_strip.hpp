@@ -240,9 +240,9 @@ __device__ __forceinline__ void gemm_strip_body(const StripArgs& g, lds_u8* lds)
     for (int u = 0; u < kMine; ++u) {
       const int b = wave + 4 * u;
       if (b < kBlocks)
-        __builtin_amdgcn_raw_buffer_store_b128(
+        store_b128<kCoherent>(
             __builtin_bit_cast(i32x4, sum[u]), rsrc_p,
-            (uint32_t)(b * 1024 + lane * 16), (uint32_t)(s * part), kCoherent);
+            (uint32_t)(b * 1024 + lane * 16), (uint32_t)(s * part));
     }
     wait_vmcnt<0>();
     barrier();

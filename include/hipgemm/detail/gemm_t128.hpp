@@ -447,9 +447,9 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          __builtin_amdgcn_raw_buffer_store_b128(
+          store_b128<0>(
               __builtin_bit_cast(i32x4, acc[i][j]), rp,
-              (uint32_t)((4 * i + j) * 1024 + lane * 16), 0, 0);
+              (uint32_t)((4 * i + j) * 1024 + lane * 16), 0);
     } else {
     const TileCoord tc = grouped_tile(t, tiles_m, tiles_n, g.group_m);
     const int rows_left = M - tc.m * Cfg::kBM - wm * 64;  // from wave row 0
@@ -494,9 +494,9 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
           const f32x4 v = ev.template value4<kAct>(a[0], a[1], a[2], a[3], i, j);
           if constexpr (kOut == kOutF32) {
             if constexpr (kVec) {
-              __builtin_amdgcn_raw_buffer_store_b128(
+              store_b128<kStoreC>(
                   __builtin_bit_cast(i32x4, v), rsrc_c,
-                  off | oob_unless(col, cols_left), 0, kStoreC);
+                  off | oob_unless(col, cols_left), 0);
             } else {
 #pragma unroll
               for (int e = 0; e < 4; ++e)
@@ -539,7 +539,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
         if (r & 1) v = i32x4{v[2], v[3], v[0], v[1]};
         const uint32_t off = (uint32_t)((r * g.ldc + 8 * c) * 2) |
                              oob_unless(r, rows_left) | oob_unless(8 * c, cols_left);
-        __builtin_amdgcn_raw_buffer_store_b128(v, rsrc_c, off, 0, kStoreC);
+        store_b128<kStoreC>(v, rsrc_c, off, 0);
       }
     } else {
 #pragma unroll
