@@ -28,7 +28,8 @@ from typing import Optional
 __all__ = [
     "HipGemmError", "lib", "lib_path", "fp8_gemm_bf16", "fp8_gemm",
     "fp8_gemm_4wave_256x256x128", "gemm_raw", "select_variant", "split_columns",
-    "variant_name", "version", "tile_order", "lds_slot", "VARIANTS",
+    "variant_name", "version", "tile_order", "lds_slot", "lds_slot_kpair",
+    "VARIANTS",
     "declared_symbols", "gemm_raw_ws", "workspace_size",
     "fp8_gemm_bf16_rowcol", "gemm_raw_rowcol", "GemmDesc", "gemm_desc_raw",
     "gemm", "gemm_desc_noalloc_raw", "FMT_E4M3", "FMT_E5M2", "FMT_FP6_E2M3",
@@ -153,6 +154,8 @@ def lib() -> ctypes.CDLL:
     L.hipgemm_tile_order.restype = ci
     L.hipgemm_lds_slot.argtypes = [ci, ci]
     L.hipgemm_lds_slot.restype = ci
+    L.hipgemm_lds_slot_kpair.argtypes = [ci, ci]
+    L.hipgemm_lds_slot_kpair.restype = ci
     _lib = L
     return L
 
@@ -278,6 +281,12 @@ def tile_order(grid: int, tiles_m: int, tiles_n: int, group_m: int = 0):
 
 def lds_slot(row: int, chunk: int) -> int:
     return int(lib().hipgemm_lds_slot(row, chunk))
+
+
+def lds_slot_kpair(row: int, chunk: int) -> int:
+    """Slot of K-chunk `chunk` of LDS row `row` in the instruction K order
+    (hipgemm_lds_slot_kpair)."""
+    return int(lib().hipgemm_lds_slot_kpair(row, chunk))
 
 
 # -- torch convenience layer ----------------------------------------------

@@ -807,4 +807,9 @@ int hipgemm_lds_slot(int row, int chunk) {
   return chunk ^ slot_xor(row);
 }
 
+int hipgemm_lds_slot_kpair(int row, int chunk) {
+  if (row < 0 || chunk < 0 || chunk > 7) return -1;
+  return kpair_slot(chunk) ^ slot_xor(row);
+}
+
 }  // extern "C"

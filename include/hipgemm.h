@@ -363,6 +363,16 @@ int hipgemm_tile_order(int grid, int tiles_m, int tiles_n, int group_m,
  */
 int hipgemm_lds_slot(int row, int chunk);
 
+/*
+ * The same for the instruction K order (MX block scales on either tiled
+ * schedule, every operand format of the 128x128 schedule but fp6, and the
+ * skinny schedule's A): the MFMA's lane group g holds K-chunks g
+ * and g + 4 of its row, stored where the plain order above keeps chunks 2g
+ * and 2g + 1, so both fetch the same LDS addresses.  -1 for out-of-range
+ * arguments.  No reference counterpart (its kernel has one K order).
+ */
+int hipgemm_lds_slot_kpair(int row, int chunk);
+
 #ifdef __cplusplus
 }
 #endif

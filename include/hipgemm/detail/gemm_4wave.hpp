@@ -284,9 +284,11 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // ---- DMA lane geometry: instruction q of wave w covers rows
   // (4q + w) * 8 .. +8; lane l takes row +l/8, slot l%8.  q in {0,1,4,5}
   // lands in rows 0-63 and 128-191 ("lo" group), q in {2,3,6,7} in rows
-  // 64-127 and 192-255 ("hi" group). ------------------------------------------
+  // 64-127 and 192-255 ("hi" group).  kMx stores the instruction K order of
+  // layout.hpp: slot l%8 holds K-chunk kpair_chunk((l%8) ^ slot_xor(row)).
   const int drow = lane >> 3;
-  const int dchunk = (lane & 7) ^ slot_xor(8 * (wave & 1) + drow);
+  const int dslot = (lane & 7) ^ slot_xor(8 * (wave & 1) + drow);
+  const int dchunk = kMx ? kpair_chunk(dslot) : dslot;
   uint32_t voff_a[8], voff_b[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
@@ -306,16 +308,17 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                             {lds + (off_a ^ 64u), lds + (off_a ^ 80u)}};
   const lds_u8* pb[2][2] = {{lds + off_b, lds + (off_b ^ 16u)},
                             {lds + (off_b ^ 64u), lds + (off_b ^ 80u)}};
-  // 16x16x128: fragment row lane%16; lane group g = lane/16 reads K-chunks
-  // 2g and 2g + 1 (32 bytes).  Any K order serves a plain product as long as
-  // A and B share it; block scales need the instruction's own: its lane
-  // group g holds K 16g .. 16g + 15 in the first four registers and
-  // 64 + 16g .. 64 + 16g + 15 in the last four, so kMx reads K-chunks g and
-  // g + 4 (each 16-lane group reads one chunk per row: conflict-free either
-  // way).
+  // 16x16x128: fragment row lane%16; lane group g = lane/16 reads slots 2g
+  // and 2g + 1 (before the XOR; 32 bytes).  Any K order serves a plain
+  // product as long as A and B share it: those slots hold K-chunks 2g and
+  // 2g + 1.  Block scales need the instruction's own order -- lane group g
+  // holds K 16g .. 16g + 15 in the first four registers and 64 + 16g ..
+  // 64 + 16g + 15 in the last four -- which kMx gets from the DMA side (the
+  // same slots then hold K-chunks g and g + 4).  Reading chunks g and g + 4
+  // from slots g and g + 4 instead cost 4 LDS conflict cycles per read.
   const int rrow16 = lane & 15;
-  const int rslot16 = ((kMx ? 1 : 2) * (lane >> 4)) ^ slot_xor(rrow16);
-  constexpr uint32_t kHalf16 = kMx ? 64u : 16u;  // chunk c -> c + 4 or c + 1
+  const int rslot16 = (2 * (lane >> 4)) ^ slot_xor(rrow16);
+  constexpr uint32_t kHalf16 = 16u;  // slot 2g -> 2g + 1
   const uint32_t off16_a =
       Cfg::kABase + (wm * 128 + rrow16) * Cfg::kBK + rslot16 * 16;
   const uint32_t off16_b =

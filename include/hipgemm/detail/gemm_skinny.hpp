@@ -147,10 +147,12 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
       voff_a[m] = (uint32_t)(16 * m + r16) * (uint32_t)g.lda + 16 * grp;
   }
 
-  // LDS A stages (kLdsA): BM rows x 128 B each, row r at 128 r, 16-byte slot
-  // x of the row holding K-chunk x ^ slot_xor(r) (conflict-free 16-row
-  // fragment reads).  DMA instruction q (8 rows) belongs to wave q % 4; its
-  // lane l fetches row 8q + l/8, chunk (l%8) ^ slot_xor(row) from global.
+  // LDS A stages (kLdsA): BM rows x 128 B each, row r at 128 r, in the
+  // instruction K order of layout.hpp: 16-byte slot x of the row holds
+  // K-chunk kpair_chunk(x ^ slot_xor(r)), so a lane group's chunks g and
+  // g + 4 sit at slots 2g and 2g + 1 (conflict-free 16-row fragment reads).
+  // DMA instruction q (8 rows) belongs to wave q % 4; its lane l fetches row
+  // 8q + l/8, chunk kpair_chunk((l%8) ^ slot_xor(row)) from global.
   constexpr int kStageA = kMB * 16 * Cfg::kBK;
   __shared__ __attribute__((aligned(1024))) uint8_t lds_a[kLdsA ? kDepth * kStageA : 16];
   const int drow = lane >> 3;
@@ -160,7 +162,7 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
     for (int i = 0; i < kDmaA; ++i) {
       const int row = 8 * (4 * i + wave) + drow;
       voff_dma[i] = (uint32_t)row * (uint32_t)g.lda +
-                    (uint32_t)(((lane & 7) ^ slot_xor(row & 15)) * 16);
+                    (uint32_t)(kpair_chunk((lane & 7) ^ slot_xor(row & 15)) * 16);
     }
   }
   const int sx16 = slot_xor(r16);
@@ -180,7 +182,7 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
       bq[d][f][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_b, voff_b[f] | oob1, k0 + 64, 0);
     }
     if constexpr (kLdsA) {
-      const uint32_t oobd = (16 * ((lane & 7) ^ slot_xor((8 * wave + drow) & 15)) < lim)
+      const uint32_t oobd = (16 * kpair_chunk((lane & 7) ^ slot_xor((8 * wave + drow) & 15)) < lim)
                                 ? 0u : kOobOffset;
 #pragma unroll
       for (int i = 0; i < kDmaA; ++i) {
@@ -210,8 +212,8 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
       i32x8 a;
       if constexpr (kLdsA) {
         const lds_u8* row = (const lds_u8*)lds_a + d * kStageA + (16 * m + r16) * Cfg::kBK;
-        a = join(lds_read16(row + ((grp ^ sx16) * 16)),
-                 lds_read16(row + (((4 + grp) ^ sx16) * 16)));
+        a = join(lds_read16(row + ((kpair_slot(grp) ^ sx16) * 16)),
+                 lds_read16(row + ((kpair_slot(grp + 4) ^ sx16) * 16)));
       } else {
         a = join(aq[d][m][0], aq[d][m][1]);
       }

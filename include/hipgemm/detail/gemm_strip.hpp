@@ -21,9 +21,14 @@
 //     ring of L + 1 stages private to the wave, with the non-temporal hint:
 //     measured on a 64 MiB B_T, whole lines with nt stream at 5.4 TB/s, the
 //     16-rows-by-64-bytes pattern of a direct register load at 4.5.  The
-//     stage rows are 128 bytes with the slot_xor swizzle (layout.hpp), so
-//     the MFMA operand reads (16 rows at one 16-byte chunk) are
-//     conflict-free.
+//     stage rows are 128 bytes with the slot_xor swizzle (layout.hpp) in
+//     the plain K order.  The MFMA operand reads (chunks g and g + 4 of 16
+//     rows per lane group g) then cost 4 LDS conflict cycles each; the
+//     instruction K order of layout.hpp removes them, but its DMA (each
+//     lane quad fetching two 32-byte pieces of a line instead of one
+//     64-byte run) measured 2.5 % slower on this HBM-bound kernel (same
+//     L1 request count, 6 % more address-stall cycles).  The LDS is a few
+//     percent busy here, so the conflicts cost nothing measurable.
 //   * A (at most 128 rows, read by every strip, so L2-resident) goes
 //     straight into registers, L steps ahead like B.
 //   * K order inside a step: lane group g = l / 16 of the MFMA holds

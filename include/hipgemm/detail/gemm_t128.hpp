@@ -29,10 +29,12 @@
 // loads.  Steps per tile are padded to an even count >= kStages (padding
 // steps read zeros).
 //
-// LDS layout: 128-byte rows with the slot_xor swizzle (layout.hpp).  A lane
-// reads K-chunks g and g + 4 of its row (g = lane / 16): the instruction's
-// own K order (lane group g holds K 16g .. 16g + 15 and 64 + 16g ..
-// 64 + 16g + 15), conflict-free (one chunk per 16-lane group).
+// LDS layout: 128-byte rows with the slot_xor swizzle in the instruction K
+// order (layout.hpp).  A lane reads K-chunks g and g + 4 of its row
+// (g = lane / 16; lane group g of the MFMA holds K 16g .. 16g + 15 and
+// 64 + 16g .. 64 + 16g + 15), stored at slots 2g and 2g + 1 before the XOR:
+// conflict-free.  (Stored at slots g and g + 4 they cost 4 conflict cycles
+// per ds_read_b128, measured.)
 //
 // Epilogue: acc * scale (or the extended epilogue, kExt) -> bf16 / fp16,
 // staged through the wave's own 8 KiB of LDS (8-byte pieces, piece p of row r
@@ -119,9 +121,12 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
 
   // ---- DMA lane geometry: instruction q (0..3) of wave w covers rows
   // (4q + w) * 8 .. + 8 of A (or B); lane l takes row + l / 8, 16-byte slot
-  // l % 8, which holds global K-chunk (l % 8) ^ slot_xor(row). -------------
+  // l % 8, which holds global K-chunk kpair_chunk((l % 8) ^ slot_xor(row))
+  // (the instruction K order of layout.hpp; fp6: chunk (l % 8) ^
+  // slot_xor(row)). ---------------------------------------------------------
   const int drow = lane >> 3;
-  const int dchunk = (lane & 7) ^ slot_xor(8 * (wave & 1) + drow);
+  const int dslot = (lane & 7) ^ slot_xor(8 * (wave & 1) + drow);
+  const int dchunk = k6 ? dslot : kpair_chunk(dslot);
   uint32_t voff_a[4], voff_b[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -182,7 +187,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   // ---- fragment reads: A rows 64 wm + 16 i + l % 16, B rows
   // 64 wn + 16 j + l % 16; K-chunks g and g + 4 (g = l / 16). -------------
   const int r16 = lane & 15, grp = lane >> 4;
-  const int rslot = grp ^ slot_xor(r16);
+  const int rslot = kpair_slot(grp) ^ slot_xor(r16);  // chunk g + 4: slot ^ 1
   const uint32_t off_a = (uint32_t)((wm * 64 + r16) * Cfg::kBK + rslot * 16);
   const uint32_t off_b =
       (uint32_t)(Cfg::kAStage + (wn * 64 + r16) * Cfg::kBK + rslot * 16);
@@ -256,12 +261,12 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t o = off_a + i * 16 * Cfg::kBK;
-      fa[set][i] = join(lds_read16(base + o), lds_read16(base + (o ^ 64u)));
+      fa[set][i] = join(lds_read16(base + o), lds_read16(base + (o ^ 16u)));
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t o = off_b + j * 16 * Cfg::kBK;
-      fb[set][j] = join(lds_read16(base + o), lds_read16(base + (o ^ 64u)));
+      fb[set][j] = join(lds_read16(base + o), lds_read16(base + (o ^ 16u)));
     }
   };
 
@@ -333,7 +338,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
         const uint32_t o = f == 0   ? off_a
                            : f <= 4 ? off_b + (f - 1) * 16 * Cfg::kBK
                                     : off_a + (f - 4) * 16 * Cfg::kBK;
-        rd[n] = lds_read16(rb + ((n & 1) ? (o ^ 64u) : o));
+        rd[n] = lds_read16(rb + ((n & 1) ? (o ^ 16u) : o));
       }
       __builtin_amdgcn_sched_group_barrier(0x008, is_fp4(kFmt) ? 2 : 1, 0);
       if (k6 && (n & 1) == 0)

@@ -8,16 +8,23 @@
 //    request a whole 128-byte line), so the permutation is applied on the
 //    global side: DMA lane l fetches chunk (l%8) ^ slot_xor(row).
 //
-//    slot_xor(r) = (r & 7) ^ ((r >> 3) & 1) depends on r mod 16 only and makes
-//    an MFMA operand fetch -- ds_read_b128 of 16 consecutive rows at one
-//    K-chunk per 16-lane group -- conflict-free whether the LDS serves 256 or
-//    128 bytes per cycle:
-//      - 256 B (16 lanes): a row's bank offset is 128 * (r & 1); for each
-//        parity the 8 rows of a 16-row block get 8 distinct slots;
-//      - 128 B (8 lanes): the 8 rows of an aligned 8-row block get 8
-//        distinct slots.
-//    tests/test_layout.py checks both properties exhaustively through the
-//    built library.
+//    slot_xor(r) = (r & 7) ^ ((r >> 3) & 1) depends on r mod 16 only.  An
+//    MFMA operand fetch reads 16 consecutive rows (lane % 16) per 16-lane
+//    group g.  Measured on gfx950 (SQ_LDS_BANK_CONFLICT of single
+//    ds_read_b128 patterns): the groups reading slots 2g ^ slot_xor(r) -- or
+//    (2g + 1) ^ slot_xor(r) -- cost no conflict cycle; slots g ^ slot_xor(r)
+//    or (g + 4) ^ slot_xor(r) cost 4 per instruction, with this or any other
+//    per-row XOR tried.  In the 8 slots of a 16-row block each row parity
+//    gets 8 distinct slots (tests/test_layout.py checks this through the
+//    built library).
+//
+//    Instruction K order.  The f8f6f4 MFMA's lane group g holds K-chunks g
+//    and g + 4 of its row (K 16g .. 16g + 15 and 64 + 16g .. 64 + 16g + 15).
+//    Kernels that need that order (block scales; fp4's two MFMA per step;
+//    operands paired with register-loaded ones) store chunk c at slot
+//    kpair_slot(c) ^ slot_xor(r): chunks g and g + 4 then sit at slots 2g and
+//    2g + 1 (before the XOR), the measured conflict-free reads.  Their DMA
+//    lane l fetches chunk kpair_chunk((l % 8) ^ slot_xor(row)).
 //
 // 2. Output tile order ("XCD-contiguous, grouped columns").
 //    The dispatcher hands workgroup b to XCD b % 8.  tile_of_block() first
@@ -40,6 +47,9 @@ namespace detail {
 constexpr int kNumXcds = 8;
 
 __host__ __device__ constexpr int slot_xor(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+// Instruction K order: slot (before the XOR) of K-chunk c, and its inverse.
+__host__ __device__ constexpr int kpair_slot(int c) { return ((c & 3) << 1) | (c >> 2); }
+__host__ __device__ constexpr int kpair_chunk(int s) { return ((s & 1) << 2) | (s >> 1); }
 
 struct TileCoord {
   int m, n;

@@ -1,13 +1,17 @@
 """LDS layout and workgroup->tile order, through the built library (no GPU).
 
 The kernel's LDS tile rows are 128 bytes (eight 16-byte slots).  hipgemm_lds_slot
-exposes the slot of (row, K-chunk); these tests check the properties the
-kernel relies on rather than restating the formula:
+(plain K order) and hipgemm_lds_slot_kpair (the MFMA's own K order) expose the
+slot of (row, K-chunk); these tests check the properties the kernels rely on
+rather than restating the formula:
   * each row's chunk->slot map is a permutation (DMA lands every chunk once);
-  * MFMA operand fetches (ds_read_b128, 16 consecutive rows at one chunk per
-    16-lane group, fragment bases at multiples of 32 rows) hit 16 distinct
-    16-byte bank groups per 256 bytes, and each 8-lane half hits 8 distinct
-    groups per 128 bytes -- conflict-free under either LDS width;
+  * MFMA operand fetches hit 16 distinct 16-byte bank groups per 256 bytes
+    in each 16-lane group (a necessary condition);
+  * the instruction-order fetch (lane group g: chunks g and g + 4) reads
+    exactly the addresses of the plain fetch of chunks 2g and 2g + 1 -- the
+    pattern measured conflict-free on gfx950 (SQ_LDS_BANK_CONFLICT), where
+    reading chunks g and g + 4 from the plain layout measured 4 conflict
+    cycles per ds_read_b128;
   * the tile order visits every tile exactly once for any grid size.
 """
 import itertools
@@ -55,6 +59,43 @@ def test_operand_fetch_bank_conflict_free(base):
         for g0 in range(0, 64, 8):
             grp = addrs[g0:g0 + 8]
             assert len({(a % 128) // 16 for a in grp}) == 8, (base, kh, t, g0)
+
+
+def test_kpair_slot_is_permutation_per_row():
+    for r in range(64):
+        assert sorted(hg.lds_slot_kpair(r, c) for c in range(SLOTS)) == \
+            list(range(SLOTS)), r
+    assert hg.lds_slot_kpair(-1, 0) == -1 and hg.lds_slot_kpair(0, SLOTS) == -1
+
+
+@pytest.mark.parametrize("base", [0, 16, 48, 112])
+def test_kpair_fetch_equals_plain_pair_fetch(base):
+    # 16x16x128 fetch: lane l reads row base + l%16; lane group g = l//16
+    # needs K-chunks g (first read) and g + 4 (second).  Plain order reads
+    # chunks 2g and 2g + 1 at the same lanes: the same addresses, read for
+    # read.
+    for first in (True, False):
+        kp = [(base + l % 16) * ROW +
+              hg.lds_slot_kpair(base + l % 16, (l // 16) + (0 if first else 4)) * 16
+              for l in range(64)]
+        plain = [(base + l % 16) * ROW +
+                 slot(base + l % 16, 2 * (l // 16) + (0 if first else 1)) * 16
+                 for l in range(64)]
+        assert kp == plain, (base, first)
+        for g0 in range(0, 64, 16):
+            assert len({(a % 256) // 16 for a in kp[g0:g0 + 16]}) == 16
+
+
+def test_kpair_dma_fill_covers_every_chunk_once():
+    # DMA lane l fetches the chunk stored at slot l%8 of row R0 + l//8.
+    for R0 in (0, 8, 16, 248):
+        seen = set()
+        for l in range(64):
+            r, s = R0 + l // 8, l % 8
+            c = [c for c in range(SLOTS) if hg.lds_slot_kpair(r, c) == s]
+            assert len(c) == 1
+            seen.add((r, c[0]))
+        assert len(seen) == 64
 
 
 def test_dma_fill_covers_every_chunk_once():
