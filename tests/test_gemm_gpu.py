@@ -139,12 +139,28 @@ def test_config3_8192_normal_scaled(gpu, oracle, variant):
     check_full(oracle, C, A, B, sa, sb)
 
 
+_CONFIG4 = {}
+
+
+def config4_inputs(oracle, M, N, K):
+    """One input set per shape, shared by the schedules (the fill is the
+    slow part of these tests)."""
+    if (M, N, K) not in _CONFIG4:
+        _CONFIG4.clear()
+        _CONFIG4[(M, N, K)] = gen(oracle, M, N, K, 4, po.NORMAL, 0.0, 0.5)
+    return _CONFIG4[(M, N, K)]
+
+
+@pytest.mark.parametrize("llm_variant", [pytest.param(0, id="auto"),
+                                         pytest.param(1, id="mfma32"),
+                                         pytest.param(4, id="8wave")])
 @pytest.mark.parametrize("M,N,K", [(8192, 28672, 8192), (8192, 8192, 28672)])
-def test_config4_llm_shapes(gpu, oracle, M, N, K):
+def test_config4_llm_shapes(gpu, oracle, M, N, K, llm_variant):
     sa, sb = oracle.draw_scale(41), oracle.draw_scale(42)
-    say(f"case config4 M={M} N={N} K={K} N(0,0.5) seed=4 sa={sa} sb={sb}")
-    A, B = gen(oracle, M, N, K, 4, po.NORMAL, 0.0, 0.5)
-    C = run_gpu(gpu, A, B, sa, sb)
+    say(f"case [v{llm_variant}] config4 M={M} N={N} K={K} N(0,0.5) seed=4 "
+        f"sa={sa} sb={sb}")
+    A, B = config4_inputs(oracle, M, N, K)
+    C = run_gpu(gpu, A, B, sa, sb, variant=llm_variant)
     check_rows(oracle, C, A, B, sa, sb, sample_rows(M, 4, 192))
     check_sums(oracle, C, A, B, np.float64(np.float32(sa) * np.float32(sb)))
 

@@ -6,9 +6,9 @@ kernel are timed by bench.time_kernel -- the bench's own protocol: warm-up,
 then back-to-back launches over rotating A/B sets of at least 512 MiB -- on
 the same inputs, stream and output buffer, in the same process.  The test
 prints the rates (the library's default choice and each schedule) and
-fails if the default falls below 90% of the reference (a regression gate,
-not the target).  Skipped where the reference
-build is absent.
+fails if the default falls below 97% of the reference (a regression gate;
+box-to-box spread is about 3 %, kernels measured in one process agree far
+closer).  Skipped where the reference build is absent.
 """
 from __future__ import annotations
 
@@ -66,12 +66,12 @@ def test_speed_vs_reference_kernel(gpu, M, N, K):
     # Two rounds in opposite orders so that no kernel always runs on the
     # hotter (later) GPU; each kernel's rate is the mean of its two rounds.
     kernels = [("reference", theirs)] + [
-        (hg.variant_name(v), mine_v(v)) for v in (0, 1, 2)]
+        (hg.variant_name(v), mine_v(v)) for v in (0, 1, 2, 4)]
     rates = {name: [] for name, _ in kernels}
     for rnd in range(2):
         for name, fn in (kernels if rnd == 0 else kernels[::-1]):
             say(f"speed {M}x{N}x{K}: round {rnd} {name}, {steps} steps")
-            r = bench.time_kernel(fn, steps, steps, stream)
+            r = bench.time_kernel(fn, steps, steps, stream, 0.5)
             rates[name].append(flop / (r["wall_ms"] * 1e-3) / 1e12)
     tr = sum(rates["reference"]) / 2
     for name, _ in kernels:
@@ -79,4 +79,4 @@ def test_speed_vs_reference_kernel(gpu, M, N, K):
         say(f"speed {M}x{N}x{K}: {name} {t:.1f} TFLOP/s (rounds "
             f"{rates[name][0]:.1f}, {rates[name][1]:.1f}); ratio {t / tr:.3f}")
     auto = sum(rates[hg.variant_name(0)]) / 2
-    assert auto >= 0.9 * tr
+    assert auto >= 0.97 * tr
