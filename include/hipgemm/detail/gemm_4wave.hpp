@@ -46,8 +46,9 @@
 // waiting for them; the next tile's first three barriers wait with vmcnt
 // 16 + 32 (the stores sit between the DMA groups each needs and the newer
 // DMAs), later ones with vmcnt 16.  vmcnt retires memory operations in issue
-// order, loads and stores alike.  The first tile of a workgroup waits for
-// all of its prologue DMA instead.
+// order, loads and stores alike.  The first tile of a workgroup has no stores
+// in flight: its prologue waits for step 0 only and its barriers use the
+// steady vmcnt 16.
 //
 // Global -> LDS: buffer_load_dwordx4 ... lds, 8 rows x 128 B per instruction
 // (whole 128-byte lines), 16 instructions per wave per step.  The buffer
@@ -559,6 +560,9 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     }
   };
 
+  // The previous tile's epilogue stores are in flight (every tile but the
+  // workgroup's first).
+  bool stores_in_flight = false;
   // Two pipeline steps kt0, kt0 + 1 (stages 0, 1).  kFirst: the tile's first
   // two steps, whose first three barriers wait past the previous tile's
   // epilogue stores.
@@ -579,7 +583,8 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       const int kt = kt0 + s;
       const bool tail = !(kFirst && s == 0);
       wait_lgkmcnt<0>();
-      if (kFirst) wait_vmcnt<kWaitAfterStores>(); else wait_vmcnt<kWaitSteady>();
+      if (kFirst && stores_in_flight) wait_vmcnt<kWaitAfterStores>();
+      else wait_vmcnt<kWaitSteady>();
       // After the wait (which counts only older operations): the six loads
       // at most make the tile's next two waits retire six more stores.
       if constexpr (kExt && kFirst)
@@ -595,7 +600,8 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       wait_lgkmcnt<0>();  // Q01
       quarter(true, 0, 0, 0, 1, 0, 1, s, kt + 2, s, 1, 0, w, w);
       wait_lgkmcnt<0>();
-      if (kFirst && s == 0) wait_vmcnt<kWaitAfterStores>(); else wait_vmcnt<kWaitSteady>();
+      if (kFirst && s == 0 && stores_in_flight) wait_vmcnt<kWaitAfterStores>();
+      else wait_vmcnt<kWaitSteady>();
       barrier();  // Q10
       quarter(true, 0, 1, 1, 0, 0, 0, s ^ 1, kt + 2, s, 1, 1, w, w);
       wait_lgkmcnt<0>();  // Q11
@@ -609,8 +615,14 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       for (int q = 0; q < 8; ++q) mxc[q] = mxn[q];
   };
 
-  // Prologue of the first tile: steps 0 and 1, all landed (so the relaxed
-  // waits of the first steps hold); a_lo(0), b_lo(0) into registers.
+  // Prologue of the first tile: steps 0 and 1 (groups A lo, B lo, B hi,
+  // A hi each), then a_lo(0), b_lo(0) into registers once step 0 landed:
+  // step 1's 16 DMAs are the newest and vmcnt retires in issue order.  The
+  // first tile has no epilogue stores in flight, so its waits are the
+  // steady ones (stores_in_flight false), which retire step 1's groups one
+  // half-step before they are read, as for any later step.  A single round
+  // over the CUs thus starts after one step of DMA instead of two.  kMx
+  // waits for everything: its scale loads follow the DMAs.
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
     dma_group(st, st, 0, 0);
@@ -618,8 +630,12 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     dma_group(st, st, 1, 1);
     dma_group(st, st, 0, 1);
   }
-  if constexpr (kMx) mx_load(0, mxc);
-  wait_vmcnt<0>();
+  if constexpr (kMx) {
+    mx_load(0, mxc);
+    wait_vmcnt<0>();
+  } else {
+    wait_vmcnt<kWaitSteady>();
+  }
   barrier();
   read_tile(0, 0, 0);
   read_tile(1, 0, 0);
@@ -995,6 +1011,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     }
     };  // store_tile
     store_tile();
+    stores_in_flight = true;
 
     t += walk.stride;
     if (t >= walk.end) break;
