@@ -177,8 +177,18 @@ SkinnyPlan plan_skinny(int M, int N, int K) {
   p.bn = CfgSkinny::bn(p.kmb);
   p.tiles_n = (N + p.bn - 1) / p.bn;
   const int steps = (K + CfgSkinny::kBK - 1) / CfgSkinny::kBK;
-  const int target = cu_count();
-  int slices = (target + p.tiles_n - 1) / p.tiles_n;
+  const int cus = cu_count();
+  int slices = (cus + p.tiles_n - 1) / p.tiles_n;
+  // Long slices: as many workgroups as two per CU hold (the kernel's LDS and
+  // registers allow two), when each slice keeps at least 12 steps to
+  // amortise its partial tile.  The second workgroup on a CU doubles the
+  // loads in flight there, and the per-CU miss path is this kernel's bound.
+  // Same process against one workgroup per CU: 128 x 8192 x 16384 +27 %,
+  // x 28672 +29 %, x 12288 +7 %, 128 x 4096 x 28672 +8 %; with 8 steps per
+  // slice (128 x 8192 x 8192) -2 %, with 4 (x 4096) -25 %.  The grid stays
+  // within 2 x CUs workgroups, so the workspace within 512 partial tiles.
+  const int slices2 = 2 * cus / p.tiles_n;
+  if (slices2 > slices && steps >= 12 * slices2) slices = slices2;
   if (slices > steps) slices = steps;
   // One counter per column tile: more tiles than the counter region holds
   // (never with slices > 1 on a GPU of at most 4096 CUs) run unsplit.

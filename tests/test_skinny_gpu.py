@@ -57,7 +57,9 @@ def run_ws(torch, A, B, M, N, K, ldc=None, sa=None, sb=None, variant=SKINNY,
 @pytest.mark.parametrize("M,N,K", [
     (1, 300, 16), (16, 8192, 8192), (17, 1000, 272), (33, 4100, 1040),
     (64, 512, 4096), (100, 2050, 528), (128, 8192, 8192), (5, 260, 8192),
-    (32, 8192, 8192), (128, 2048, 8192), (20, 16384, 1024), (48, 70, 4112)])
+    (32, 8192, 8192), (128, 2048, 8192), (20, 16384, 1024), (48, 70, 4112),
+    # long K: the split-K plan takes two workgroups per CU (8 and 16 slices)
+    (128, 8192, 12288), (96, 4096, 28672)])
 def test_skinny_ternary_bit_exact(gpu, oracle, M, N, K, variant):
     torch = gpu
     say(f"case skinny-ternary [v{variant}] M={M} N={N} K={K} seed=21 "
@@ -73,7 +75,8 @@ def test_skinny_ternary_bit_exact(gpu, oracle, M, N, K, variant):
 
 @pytest.mark.parametrize("variant", BOTH)
 @pytest.mark.parametrize("M,N,K", [(16, 8192, 8192), (128, 8192, 8192),
-                                   (40, 3000, 2064), (64, 28672, 4096)])
+                                   (40, 3000, 2064), (64, 28672, 4096),
+                                   (128, 8192, 16384)])
 def test_skinny_uniform_within_tolerance(gpu, oracle, M, N, K, variant):
     torch = gpu
     sa, sb = oracle.draw_scale(51), oracle.draw_scale(52)
