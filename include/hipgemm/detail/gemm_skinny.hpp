@@ -321,21 +321,19 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
           for (int f = 0; f < kF; ++f)
             v[u][m][f] = __builtin_bit_cast(
                 f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                           rsrc_p, slot(m, f),
+                           rsrc_p, slot(m, f) | (q0 + u < g.slices ? 0u : kOobOffset),
                            (uint32_t)min(q0 + u, g.slices - 1) * stride,
                            kCoherent));
-      // Slices past the last (their loads re-read it) add +0, which leaves
-      // every sum unchanged (a sum started at +0 is never -0).  A branch
-      // here instead lets the compiler sink each load into its branch and
-      // wait for it alone.
+      // Slices past the last load out of range: +0, no memory request, and
+      // adding it leaves every sum unchanged (a sum started at +0 is never
+      // -0).  A branch here instead lets the compiler sink each load into
+      // its branch and wait for it alone.
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const bool live = q0 + u < g.slices;
+      for (int u = 0; u < kBatch; ++u)
 #pragma unroll
         for (int m = 0; m < kMB; ++m)
 #pragma unroll
-          for (int f = 0; f < kF; ++f) sum[m][f] += live ? v[u][m][f] : f32x4{};
-      }
+          for (int f = 0; f < kF; ++f) sum[m][f] += v[u][m][f];
     }
   }
 #pragma unroll
@@ -416,15 +414,13 @@ __device__ __forceinline__ void gemm_skinny_reduce_body(const SkinnyArgs& g,
       for (int f = 0; f < kF; ++f)
         v[u][f] = __builtin_bit_cast(
             f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       rsrc_p, slot(f),
+                       rsrc_p, slot(f) | (q0 + u < g.slices ? 0u : kOobOffset),
                        (uint32_t)min(q0 + u, g.slices - 1) * stride, 0));
-    // As in gemm_skinny_body: +0 for slices past the last, not a branch.
+    // As in gemm_skinny_body: slices past the last load +0 out of range.
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const bool live = q0 + u < g.slices;
+    for (int u = 0; u < kBatch; ++u)
 #pragma unroll
-      for (int f = 0; f < kF; ++f) sum[f] += live ? v[u][f] : f32x4{};
-    }
+      for (int f = 0; f < kF; ++f) sum[f] += v[u][f];
   }
   const int es = kExt ? out_bytes(scl.ev.out) : 2;  // bytes per C element
   const __amdgpu_buffer_rsrc_t rsrc_c =

@@ -260,7 +260,7 @@ __device__ __forceinline__ void gemm_strip_body(const StripArgs& g, lds_u8* lds)
     if (!last) return;
     // Every slice's partial, in slice order (the workgroup's own included,
     // read back, so that the order is the same whoever arrives last); slices
-    // past the last re-read it and add +0.
+    // past the last load +0 out of range (no memory request) and add it.
 #pragma unroll
     for (int u = 0; u < kMine; ++u) sum[u] = f32x4{};
     constexpr int kBatch = 8;
@@ -273,15 +273,15 @@ __device__ __forceinline__ void gemm_strip_body(const StripArgs& g, lds_u8* lds)
           const int b = min(wave + 4 * u, kBlocks - 1);
           v[t][u] = __builtin_bit_cast(
               f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                         rsrc_p, (uint32_t)(b * 1024 + lane * 16),
+                         rsrc_p,
+                         (uint32_t)(b * 1024 + lane * 16) |
+                             (s0 + t < g.slices ? 0u : kOobOffset),
                          (uint32_t)(min(s0 + t, g.slices - 1) * part), kCoherent));
         }
 #pragma unroll
-      for (int t = 0; t < kBatch; ++t) {
-        const bool live = s0 + t < g.slices;
+      for (int t = 0; t < kBatch; ++t)
 #pragma unroll
-        for (int u = 0; u < kMine; ++u) sum[u] += live ? v[t][u] : f32x4{};
-      }
+        for (int u = 0; u < kMine; ++u) sum[u] += v[t][u];
     }
   }
 
