@@ -22,7 +22,8 @@ const void* four_wave_plain(int mf, const Key& k) {
     return k.vec ? (const void*)&k_fp8_gemm_4wave<true, 32, 0>
                  : (const void*)&k_fp8_gemm_4wave<false, 32, 0>;
   }
-  return sel4(k.fmt, [&](auto F) {
+  // The 8-bit pairs and fp4 x fp4 (kFmtPairFp4).
+  return sel_fmt(k.fmt, [&](auto F) {
     return sel2(k.vec, [&](auto V) {
       return (const void*)&k_fp8_gemm_4wave<decltype(V)::value == 1, 16, decltype(F)::value>;
     });

@@ -255,6 +255,13 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   static_assert(kMf == 32 || kMf == 16, "MFMA shape");
   static_assert(!kExt || kMf == 16, "extended epilogue: 16x16x128 only");
   static_assert(!kMx || (kMf == 16 && !kExt), "MX: 16x16x128, plain epilogue");
+  // fp4 x fp4: a 128-byte step holds 256 elements, so each 16x16 block takes
+  // two MFMA per step, on the low and the high 16 bytes of its fragments
+  // (the instruction reads four registers of each operand).  A and B_T share
+  // the K order, which is all a product needs.  Per-tensor epilogue.
+  constexpr bool k4 = is_fp4(kFmt);
+  static_assert(!k4 || (kMf == 16 && !kMx), "fp4: 16x16x128, no MX");
+  constexpr int kMfmaPerBlock = k4 ? 2 : 1;
   constexpr bool k16 = kMf == 16;
   constexpr int kDmaPerGroup = 4;  // per wave
   constexpr int kWaitSteady = 4 * kDmaPerGroup;
@@ -452,13 +459,21 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
 #pragma unroll
       for (int n = from; n < to; ++n) {
         const int i = 4 * qi + n / 4, j = 4 * qj + n % 4;
-        if constexpr (kMx)
+        if constexpr (kMx) {
           acc16[i][j] = mfma_16x16x128_mx<fmt_b(kFmt), fmt_a(kFmt)>(
               fb16[j], fa16[i], acc16[i][j], w[2 + j / 4], w[i / 4], j % 4,
               i % 4);
-        else
+        } else if constexpr (k4) {
+          const i32x8& x = fb16[j];
+          const i32x8& y = fa16[i];
+          acc16[i][j] = mfma_16x16x128<kFmtFp4, kFmtFp4>(x, y, acc16[i][j]);
+          acc16[i][j] = mfma_16x16x128<kFmtFp4, kFmtFp4>(
+              __builtin_shufflevector(x, x, 4, 5, 6, 7, 0, 1, 2, 3),
+              __builtin_shufflevector(y, y, 4, 5, 6, 7, 0, 1, 2, 3), acc16[i][j]);
+        } else {
           acc16[i][j] = mfma_16x16x128<fmt_b(kFmt), fmt_a(kFmt)>(
               fb16[j], fa16[i], acc16[i][j]);
+        }
       }
       return;
     }
@@ -531,7 +546,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       for (int n = 0; n < 8; ++n) {
         quarter_mfma(qi, qj, n, n + 1, w);
         rd[n] = read16_one(rop, rhi, rst, n);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kMfmaPerBlock, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         sched_fence();
       }
@@ -539,7 +554,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       for (int n = 0; n < 4; ++n) {
         quarter_mfma(qi, qj, 8 + n, 9 + n, w);
         dma_one(d, dst, dop, dhi, n);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kMfmaPerBlock, 0);
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         sched_fence();
       }

@@ -217,14 +217,17 @@ def test_gemm_desc_entry_validation():
 
 def test_fp4_entry_validation():
     """fp4 operands: both fp4, K (elements) a multiple of 32, lda / ldb in
-    bytes >= K / 2, AUTO or the 128 x 128 schedule (MX scales too, with the
-    per-tensor epilogue); the descriptor's
-    workspace query plans the 128 x 128 schedule on K / 2 bytes."""
+    bytes >= K / 2; AUTO, the 128 x 128 schedule (MX scales too, with the
+    per-tensor epilogue) or, with the per-tensor epilogue and no MX, the
+    4-wave 16x16x128 one.  The descriptor's workspace query plans the
+    128 x 128 schedule on K / 2 bytes, and nothing where AUTO takes the
+    4-wave schedule."""
     base = dict(A=FAKE, B_T=FAKE, C=FAKE, M=300, N=300, K=256, lda=128,
                 ldb=128, ldc=300, a_format=4, b_format=4)
     assert hg.gemm_desc_raw(hg.GemmDesc(**dict(base, M=0))) == 0
     for bad in (dict(b_format=0), dict(a_format=1), dict(K=240), dict(lda=112),
-                dict(variant=2), dict(variant=3), dict(variant=4),
+                dict(variant=1), dict(variant=3), dict(variant=4),
+                dict(variant=2, bias=FAKE), dict(variant=2, out_dtype=1),
                 dict(mx_scale_a=FAKE, mx_scale_b=FAKE, variant=2),
                 dict(mx_scale_a=FAKE, mx_scale_b=FAKE, bias=FAKE)):
         assert hg.gemm_desc_raw(hg.GemmDesc(**dict(base, **bad))) == INVALID, bad
@@ -238,6 +241,10 @@ def test_fp4_entry_validation():
     d8 = hg.GemmDesc(**dict(base, a_format=0, b_format=0, M=256, N=4096,
                             K=14336, lda=14336, ldb=14336, ldc=4096))
     assert L.hipgemm_gemm_workspace_size(ctypes.byref(d8)) == 16384 + 64 * 4 * 65536
+    # 8192^3 elements: AUTO takes the 4-wave schedule, which needs none
+    big = hg.GemmDesc(**dict(base, M=8192, N=8192, K=8192, lda=4096, ldb=4096,
+                             ldc=8192))
+    assert L.hipgemm_gemm_workspace_size(ctypes.byref(big)) == 0
 
 
 def test_fp6_entry_validation():

@@ -1,5 +1,5 @@
-"""GPU parity of fp4 (OCP E2M1) operands on the 128 x 128 schedule against
-the oracle's hg_gemm_ex.
+"""GPU parity of fp4 (OCP E2M1) operands on the 128 x 128 schedule and the
+4-wave 16x16x128 one (per-tensor epilogue) against the oracle's hg_gemm_ex.
 
 Every product of two fp4 values is a multiple of 1/4 below 36 and every
 partial sum over K <= 8192 stays below 2^19, so fp32 sums are exact in any
@@ -57,10 +57,13 @@ def rand_fp4(shape, seed):
     return np.random.default_rng(seed).integers(0, 256, shape).astype(np.uint8)
 
 
-@pytest.mark.parametrize("variant", [0, 5], ids=["auto", "tile128"])
+@pytest.mark.parametrize("variant", [0, 2, 5], ids=["auto", "4wave", "tile128"])
 @pytest.mark.parametrize("M,N,K", [(300, 260, 224), (512, 512, 1024),
                                    (129, 1000, 96), (1100, 700, 4128),
-                                   (200, 300, 8192)])
+                                   (200, 300, 8192),
+                                   # 81 tiles of 256, K 2176 bytes: AUTO's
+                                   # 4-wave schedule
+                                   (2304, 2304, 4352)])
 def test_fp4_bit_exact(gpu, oracle, M, N, K, variant):
     say(f"case [v{variant}] fp4 M={M} N={N} K={K} seed=111")
     A, B = rand_fp4((M, K // 2), 111), rand_fp4((N, K // 2), 112)
