@@ -46,7 +46,8 @@ __global__ __launch_bounds__(256) void k_mx_pack(const uint8_t* src, int rows,
 }  // namespace
 
 const void* four_wave_mx(const Key& k) {
-  return sel4(k.fmt, [&](auto F) {
+  // The 8-bit pairs and fp4 x fp4 (MXFP4).
+  return sel_fmt(k.fmt, [&](auto F) {
     return sel2(k.vec, [&](auto V) {
       return (const void*)&k_fp8_gemm_4wave_mx<decltype(V)::value == 1,
                                                decltype(F)::value>;

@@ -258,10 +258,20 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // fp4 x fp4: a 128-byte step holds 256 elements, so each 16x16 block takes
   // two MFMA per step, on the low and the high 16 bytes of its fragments
   // (the instruction reads four registers of each operand).  A and B_T share
-  // the K order, which is all a product needs.  Per-tensor epilogue.
+  // the K order, which is all a plain product needs; kMx stores the
+  // instruction K order (the fragment halves are then K-chunks g and g + 4,
+  // the two halves of one MX scale pair).  Per-tensor epilogue.
   constexpr bool k4 = is_fp4(kFmt);
-  static_assert(!k4 || (kMf == 16 && !kMx), "fp4: 16x16x128, no MX");
+  static_assert(!k4 || kMf == 16, "fp4: 16x16x128");
   constexpr int kMfmaPerBlock = k4 ? 2 : 1;
+  // kMx scale words per step and MFMA: 8-bit steps take words 2s, 2s + 1 of
+  // their pair's load; an fp4 step is a whole pair (its halves h take words
+  // 2h, 2h + 1), so it loads its own words one step ahead and passes eight
+  // per step.  Those loads are waited for by the next step's first barrier,
+  // which must then retire everything but the 16 newest DMAs: the relaxed
+  // waits past a tile's epilogue stores are not used.
+  constexpr bool k4Mx = k4 && kMx;
+  constexpr int kMxW = k4Mx ? 8 : 4;  // scale words per step
   constexpr bool k16 = kMf == 16;
   constexpr int kDmaPerGroup = 4;  // per wave
   constexpr int kWaitSteady = 4 * kDmaPerGroup;
@@ -459,7 +469,16 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
 #pragma unroll
       for (int n = from; n < to; ++n) {
         const int i = 4 * qi + n / 4, j = 4 * qj + n % 4;
-        if constexpr (kMx) {
+        if constexpr (k4Mx) {
+          const i32x8& x = fb16[j];
+          const i32x8& y = fa16[i];
+          acc16[i][j] = mfma_16x16x128_mx<kFmtFp4, kFmtFp4>(
+              x, y, acc16[i][j], w[2 + j / 4], w[i / 4], j % 4, i % 4);
+          acc16[i][j] = mfma_16x16x128_mx<kFmtFp4, kFmtFp4>(
+              __builtin_shufflevector(x, x, 4, 5, 6, 7, 0, 1, 2, 3),
+              __builtin_shufflevector(y, y, 4, 5, 6, 7, 0, 1, 2, 3), acc16[i][j],
+              w[6 + j / 4], w[4 + i / 4], j % 4, i % 4);
+        } else if constexpr (kMx) {
           acc16[i][j] = mfma_16x16x128_mx<fmt_b(kFmt), fmt_a(kFmt)>(
               fb16[j], fa16[i], acc16[i][j], w[2 + j / 4], w[i / 4], j % 4,
               i % 4);
@@ -488,24 +507,26 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // kMx: scale words of the current step pair (mxc: A words 0-3, B words
   // 4-7, as loaded), of the next pair (mxn, in flight), and of the previous
   // step (mxp, for the tail MFMA that crosses into the next step).
-  uint32_t mxc[8] = {}, mxn[8] = {}, mxp[4] = {};
-  // Loads the scale words of the step pair starting at step kb2 (steps
-  // kb2 >= kt_pad: the next tile's) into dst: two 16-byte loads per lane,
+  uint32_t mxc[8] = {}, mxn[8] = {}, mxp[kMxW] = {};
+  // Loads the scale words of the step pair starting at step kb2 (fp4: of
+  // step kb2, a pair by itself; steps kb2 >= kt_pad: the next tile's) into
+  // dst: two 16-byte loads per lane,
   // counted in vmcnt.  The whole offset is in the range-checked VGPR
   // offset: tiles past the last, 128-row groups past M / N and the padding
   // steps past the last pair read zero (scale 2^-127 on zero data).
   auto mx_load = [&](int kb2, uint32_t (&dst)[8]) {
     const bool next = kb2 >= kt_pad;
     const int tt = next ? t + walk.stride : t;
-    const int p = (next ? kb2 - kt_pad : kb2) / 2;
+    const int p = (next ? kb2 - kt_pad : kb2) / (k4 ? 1 : 2);
     const MxArgs mx = kernel_mx();
-    const int P = mx_pairs(K);
+    const int kel = k4 ? 2 * K : K;  // K in elements (K counts bytes of a row)
+    const int P = mx_pairs(kel);
     const bool live = tt < walk.end && p < P;
     const TileCoord c = grouped_tile(live ? tt : t, tiles_m, tiles_n, g.group_m);
     const __amdgpu_buffer_rsrc_t ra =
-        make_rsrc(mx.a, live ? (uint32_t)mx_packed_bytes(M, K) : 0u);
+        make_rsrc(mx.a, live ? (uint32_t)mx_packed_bytes(M, kel) : 0u);
     const __amdgpu_buffer_rsrc_t rb =
-        make_rsrc(mx.b, live ? (uint32_t)mx_packed_bytes(N, K) : 0u);
+        make_rsrc(mx.b, live ? (uint32_t)mx_packed_bytes(N, kel) : 0u);
     const uint32_t vo = (uint32_t)lane * 16u;
     const i32x4 va = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
         ra, vo + (uint32_t)(((c.m * 2 + wm) * P + p) * 1024), 0, 0));
@@ -598,7 +619,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       const int kt = kt0 + s;
       const bool tail = !(kFirst && s == 0);
       wait_lgkmcnt<0>();
-      if (kFirst && stores_in_flight) wait_vmcnt<kWaitAfterStores>();
+      if (kFirst && stores_in_flight && !k4Mx) wait_vmcnt<kWaitAfterStores>();
       else wait_vmcnt<kWaitSteady>();
       // After the wait (which counts only older operations): the six loads
       // at most make the tile's next two waits retire six more stores.
@@ -607,15 +628,28 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       barrier();  // Q00
       // kMx: this step's scale words; the next pair's are loaded here (after
       // the wait, like scale_dma: at most two more stores retired early).
-      uint32_t w[4] = {mxc[2 * s], mxc[2 * s + 1], mxc[4 + 2 * s],
-                       mxc[4 + 2 * s + 1]};
-      if constexpr (kMx)
-        if (s == 0) mx_load(kt0 + 2, mxn);
+      uint32_t w[kMxW];
+      if constexpr (k4Mx) {
+        // halves 0 and 1 of this step: A words 0-1, B words 0-1, then A
+        // words 2-3, B words 2-3 of its load; the next step's words now.
+        const uint32_t ws[8] = {mxc[0], mxc[1], mxc[4], mxc[5],
+                                mxc[2], mxc[3], mxc[6], mxc[7]};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) w[q] = ws[q];
+        mx_load(kt + 1, mxn);
+      } else {
+        w[0] = mxc[2 * s];
+        w[1] = mxc[2 * s + 1];
+        w[2] = mxc[4 + 2 * s];
+        w[3] = mxc[4 + 2 * s + 1];
+        if constexpr (kMx)
+          if (s == 0) mx_load(kt0 + 2, mxn);
+      }
       quarter(tail, 1, 1, 0, 0, 1, 1, s, kt + 2, s, 0, 0, w, mxp);
       wait_lgkmcnt<0>();  // Q01
       quarter(true, 0, 0, 0, 1, 0, 1, s, kt + 2, s, 1, 0, w, w);
       wait_lgkmcnt<0>();
-      if (kFirst && s == 0 && stores_in_flight) wait_vmcnt<kWaitAfterStores>();
+      if (kFirst && s == 0 && stores_in_flight && !k4Mx) wait_vmcnt<kWaitAfterStores>();
       else wait_vmcnt<kWaitSteady>();
       barrier();  // Q10
       quarter(true, 0, 1, 1, 0, 0, 0, s ^ 1, kt + 2, s, 1, 1, w, w);
@@ -623,9 +657,12 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       quarter(true, 1, 0, 1, 1, 1, 0, s ^ 1, kt + 2, s, 0, 1, w, w);
       if constexpr (kMx)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) mxp[q] = w[q];
+        for (int q = 0; q < kMxW; ++q) mxp[q] = w[q];
+      if constexpr (k4Mx)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) mxc[q] = mxn[q];
     }
-    if constexpr (kMx)
+    if constexpr (kMx && !k4Mx)
 #pragma unroll
       for (int q = 0; q < 8; ++q) mxc[q] = mxn[q];
   };

@@ -150,14 +150,18 @@ def test_mx_unit_scales_equal_plain(gpu, oracle):
     assert compare(C, oracle.gemm(A, B))[0] <= REL_TOL
 
 
-@pytest.mark.parametrize("variant", [0, 5], ids=["auto", "tile128"])
+@pytest.mark.parametrize("variant", [0, 2, 5], ids=["auto", "4wave", "tile128"])
 @pytest.mark.parametrize("M,N,K", [(300, 260, 256), (129, 1000, 96),
-                                   (1100, 700, 4128), (200, 300, 4096)])
+                                   (1100, 700, 4128), (200, 300, 4096),
+                                   # 81 tiles of 256, K 2176 bytes: AUTO's
+                                   # 4-wave schedule
+                                   (2304, 2304, 4352)])
 def test_mxfp4_bit_exact(gpu, oracle, M, N, K, variant):
     """MXFP4: fp4 operands (random bytes) with block scales 2^-1 .. 2^1 on
-    the 128 x 128 schedule (whole K and K-slices): products are multiples of
-    2^-4 below 144, sums below 2^20 for K <= 4128, exact in fp32 in any
-    order -- bit-exact against hg_gemm_mx."""
+    the 128 x 128 schedule (whole K and K-slices) and the 4-wave one:
+    products are multiples of 2^-4 below 144, sums below 2^20 for
+    K <= 7000, exact in fp32 in any order -- bit-exact against
+    hg_gemm_mx."""
     say(f"case [v{variant}] mxfp4 M={M} N={N} K={K} seed=121")
     rng = np.random.default_rng(121)
     A = rng.integers(0, 256, (M, K // 2)).astype(np.uint8)
