@@ -422,8 +422,8 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   int M = d.M, N = d.N, K = d.K, lda = d.lda, ldb = d.ldb, variant = d.variant;
   if (!valid_code(d.out_dtype, 4)) return hipErrorInvalidValue;
   // fp4 operands: both, K a multiple of 32 elements, the 128 x 128
-  // schedule, or with the per-tensor epilogue (MX scales or not) the 4-wave
-  // 16x16x128 one (fp4_variant); from here on K counts bytes of a row
+  // schedule or the 4-wave 16x16x128 one (fp4_variant); from here on K
+  // counts bytes of a row
   // (K / 2).  fp6 operands:
   // both (either variant each), K a multiple of 64 elements (48 bytes), the
   // 128 x 128 schedule; K counts bytes (3 K / 4).
@@ -483,8 +483,6 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   // MX block scales: the 4-wave 16x16x128 and 128 x 128 schedules,
   // per-tensor epilogue (K in elements a multiple of 32: bytes of 16 for fp4).
   const bool mx = d.mx_scale_a || d.mx_scale_b;
-  if (fp4 && variant == HIPGEMM_VARIANT_4WAVE_MFMA16 && ext)
-    return hipErrorInvalidValue;
   if (mx && (fp6 || !d.mx_scale_a || !d.mx_scale_b || K % (fp4 ? 16 : 32) != 0 || ext ||
              !aligned(d.mx_scale_a, 16) || !aligned(d.mx_scale_b, 16) ||
              (variant != HIPGEMM_VARIANT_AUTO &&
@@ -494,10 +492,9 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   const int n1 = (variant == HIPGEMM_VARIANT_AUTO && !mx && !fp4 && !fp6 && K > 0)
                      ? split_columns(M, N, cu_count())
                      : 0;
-  variant = fp6          ? HIPGEMM_VARIANT_TILE128
-            : fp4 && ext       ? HIPGEMM_VARIANT_TILE128
-            : fp4              ? fp4_variant(variant, M, N, K)
-                               : resolve_variant(variant, M, N, K);
+  variant = fp6   ? HIPGEMM_VARIANT_TILE128
+            : fp4 ? fp4_variant(variant, M, N, K)
+                  : resolve_variant(variant, M, N, K);
   // MX: the 128 x 128 schedule where AUTO picks it, else the 4-wave one.
   if (mx && variant != HIPGEMM_VARIANT_TILE128) variant = HIPGEMM_VARIANT_4WAVE_MFMA16;
   if (variant == HIPGEMM_VARIANT_8WAVE && d.out_dtype >= HIPGEMM_OUT_F32)
@@ -621,8 +618,7 @@ int resolve_variant(int variant, int M, int N, int K) {
                                          : variant;
 }
 
-// fp4 x fp4 with the per-tensor epilogue, with or without MX scales (Kb:
-// bytes of a row).  AUTO: the
+// fp4 x fp4 (Kb: bytes of a row).  AUTO: the
 // 4-wave 16x16x128 schedule where it picks that one for 8-bit operands of
 // the same byte shape (a 128-byte step is one MFMA's worth for 8-bit
 // operands, two for fp4: the same LDS bytes per step, twice the flops);
@@ -740,11 +736,7 @@ size_t hipgemm_gemm_workspace_size(const hipgemm_gemm_desc* d) {
   const bool fp4 = d->a_format == HIPGEMM_FMT_FP4_E2M1 ||
                    d->b_format == HIPGEMM_FMT_FP4_E2M1;
   if (fp4) {
-    const bool ext = d->scale_rows || d->scale_cols || d->bias ||
-                     d->activation != HIPGEMM_ACT_NONE ||
-                     d->out_dtype != HIPGEMM_OUT_BF16;
-    if (!ext &&
-        fp4_variant(d->variant, d->M, d->N, d->K / 2) == HIPGEMM_VARIANT_4WAVE_MFMA16)
+    if (fp4_variant(d->variant, d->M, d->N, d->K / 2) == HIPGEMM_VARIANT_4WAVE_MFMA16)
       return 0;
     return plan_t128(d->M, d->N, d->K / 2, cu_count()).ws_bytes;
   }

@@ -97,9 +97,9 @@ enum {
  * mantissa bit -- 0, 0.5, 1, 1.5, 2, 3, 4, 6 and their negatives -- two per
  * byte, element 2i in the low nibble of byte i of a row; A and B_T both
  * FP4_E2M1 (not mixed with the other formats), K (in elements) a multiple
- * of 32, lda / ldb in bytes (>= K / 2); schedules AUTO, TILE128 and, with
- * the per-tensor epilogue (MX scales or not), 4WAVE_MFMA16 (AUTO's choice
- * where it takes that schedule for 8-bit operands of the same byte shape).
+ * of 32, lda / ldb in bytes (>= K / 2); schedules AUTO, TILE128 and
+ * 4WAVE_MFMA16 (AUTO's choice where it takes that schedule for 8-bit
+ * operands of the same byte shape).
  * FP6_E2M3 (1 sign, 2 exponent bits, bias 1, 3 mantissa bits; largest 7.5)
  * and FP6_E3M2 (1 sign, 3 exponent bits, bias 3, 2 mantissa bits; largest
  * 28), no inf or NaN: four per three bytes, packed LSB first -- element k

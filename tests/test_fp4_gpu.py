@@ -73,19 +73,20 @@ def test_fp4_bit_exact(gpu, oracle, M, N, K, variant):
     assert np.array_equal(C, want), f"{int((C != want).sum())} of {C.size} differ"
 
 
+@pytest.mark.parametrize("variant", [2, 5], ids=["4wave", "tile128"])
 @pytest.mark.parametrize("out", [0, 1, 2, 3], ids=["bf16", "f16", "f32", "e4m3"])
 @pytest.mark.parametrize("shape", [(384, 520, 512), (200, 300, 8192)],
                          ids=["plain", "ksplit"])
-def test_fp4_epilogue(gpu, oracle, out, shape):
+def test_fp4_epilogue(gpu, oracle, out, shape, variant):
     M, N, K = shape
-    say(f"case [v5] fp4-epilogue out={out} M={M} N={N} K={K} seed=113")
+    say(f"case [v{variant}] fp4-epilogue out={out} M={M} N={N} K={K} seed=113")
     rng = np.random.default_rng(113)
     A, B = rand_fp4((M, K // 2), 113), rand_fp4((N, K // 2), 114)
     sr = np.exp2(rng.integers(-3, 4, M)).astype(np.float32)
     sc = np.exp2(rng.integers(-6, -1, N)).astype(np.float32)
     bias = rng.uniform(-4, 4, N).astype(np.float32)
     C, guard = run(gpu, A, B, K, out=out, act=1, sa=[0.25], sr=sr, sc=sc,
-                   bias=bias, variant=5)
+                   bias=bias, variant=variant)
     assert guard
     want = oracle.gemm_ex(A, B, a_fmt=4, b_fmt=4, out=out, act=1, scale_a=0.25,
                           scale_rows=sr, scale_cols=sc, bias=bias)
