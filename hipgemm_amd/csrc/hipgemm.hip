@@ -153,10 +153,10 @@ hipError_t launch_tiled(int variant, GemmArgs g, hk::Key key,
   return hipLaunchKernel(fn, dim3(grid), dim3(threads), args, 0, stream);
 }
 
-// Split-K plan of the skinny schedule: 16-row blocks of M, K-slices per
-// column tile of CfgSkinny::bn(kmb) columns (enough workgroups to give every
-// CU one), and the workspace it needs (arrival counters, then the partial
-// tiles).
+// Split-K plan of the skinny schedule: 16-row blocks of M, column tiles of
+// 64 kf columns (kf B_T fragments per wave), K-slices per column tile
+// (enough workgroups to give every CU one, or two, below), and the
+// workspace it needs (arrival counters, then the partial tiles).
 //
 // Workspace layout, shared by every schedule so that calls of different
 // schedules may share one workspace: bytes [0, HIPGEMM_WS_COUNTER_BYTES)
@@ -167,38 +167,57 @@ constexpr size_t kWsCounterBytes = HIPGEMM_WS_COUNTER_BYTES;
 constexpr int kWsMaxCounters = (int)(kWsCounterBytes / sizeof(int));
 
 struct SkinnyPlan {
-  int kmb, bn, tiles_n, slices, slice_steps;
+  int kmb, kf, bn, tiles_n, slices, slice_steps;
   size_t counter_bytes, ws_bytes;
 };
 
+// Long slices: as many workgroups as two per CU hold (the kernel's LDS and
+// registers allow two), when each slice keeps at least 12 steps to amortise
+// its partial tile.  The second workgroup on a CU doubles the loads in
+// flight there, and the per-CU miss path is this kernel's bound.  Same
+// process against one workgroup per CU: 128 x 8192 x 16384 +27 %, x 28672
+// +29 %, x 12288 +7 %, 128 x 4096 x 28672 +8 %; with 8 steps per slice
+// (128 x 8192 x 8192) -2 %, with 4 (x 4096) -25 %.  The grid stays within
+// 2 x CUs workgroups, so the workspace within 512 partial tiles.
+//
+// From 65 rows the column tile is 64 instead of 128 columns when only the
+// narrower tile reaches two workgroups per CU: 128 x 8192 x 8192 +8 %,
+// 96 x 8192 x 8192 +9 %, 128 x 4096 x 14336 +7 % (each workgroup reads all
+// of A for its K-slice, so a narrower tile costs A traffic, and where the
+// 128-column tile already has two workgroups per CU, or neither has,
+// 64 columns measured 3-11 % slower).
 SkinnyPlan plan_skinny(int M, int N, int K) {
-  SkinnyPlan p{};
-  p.kmb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
-  p.bn = CfgSkinny::bn(p.kmb);
-  p.tiles_n = (N + p.bn - 1) / p.bn;
+  const int kmb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
   const int steps = (K + CfgSkinny::kBK - 1) / CfgSkinny::kBK;
   const int cus = cu_count();
-  int slices = (cus + p.tiles_n - 1) / p.tiles_n;
-  // Long slices: as many workgroups as two per CU hold (the kernel's LDS and
-  // registers allow two), when each slice keeps at least 12 steps to
-  // amortise its partial tile.  The second workgroup on a CU doubles the
-  // loads in flight there, and the per-CU miss path is this kernel's bound.
-  // Same process against one workgroup per CU: 128 x 8192 x 16384 +27 %,
-  // x 28672 +29 %, x 12288 +7 %, 128 x 4096 x 28672 +8 %; with 8 steps per
-  // slice (128 x 8192 x 8192) -2 %, with 4 (x 4096) -25 %.  The grid stays
-  // within 2 x CUs workgroups, so the workspace within 512 partial tiles.
-  const int slices2 = 2 * cus / p.tiles_n;
-  if (slices2 > slices && steps >= 12 * slices2) slices = slices2;
-  if (slices > steps) slices = steps;
-  // One counter per column tile: more tiles than the counter region holds
-  // (never with slices > 1 on a GPU of at most 4096 CUs) run unsplit.
-  if (slices < 1 || p.tiles_n > kWsMaxCounters) slices = 1;
-  p.slice_steps = steps > 0 ? (steps + slices - 1) / slices : 0;
-  p.slices = p.slice_steps > 0 ? (steps + p.slice_steps - 1) / p.slice_steps : 1;
-  if (p.slices > 1) {
-    p.counter_bytes = kWsCounterBytes;
-    p.ws_bytes = p.counter_bytes + (size_t)p.tiles_n * p.slices * p.kmb * 16 *
-                                       p.bn * sizeof(float);
+  auto plan = [&](int kf, bool* two) {
+    SkinnyPlan p{};
+    p.kmb = kmb;
+    p.kf = kf;
+    p.bn = CfgSkinny::bn_of(kf);
+    p.tiles_n = (N + p.bn - 1) / p.bn;
+    int slices = (cus + p.tiles_n - 1) / p.tiles_n;
+    const int slices2 = 2 * cus / p.tiles_n;
+    *two = slices2 > slices && steps >= 12 * slices2;
+    if (*two) slices = slices2;
+    if (slices > steps) slices = steps;
+    // One counter per column tile: more tiles than the counter region holds
+    // (never with slices > 1 on a GPU of at most 4096 CUs) run unsplit.
+    if (slices < 1 || p.tiles_n > kWsMaxCounters) slices = 1;
+    p.slice_steps = steps > 0 ? (steps + slices - 1) / slices : 0;
+    p.slices = p.slice_steps > 0 ? (steps + p.slice_steps - 1) / p.slice_steps : 1;
+    if (p.slices > 1) {
+      p.counter_bytes = kWsCounterBytes;
+      p.ws_bytes = p.counter_bytes + (size_t)p.tiles_n * p.slices * p.kmb * 16 *
+                                         p.bn * sizeof(float);
+    }
+    return p;
+  };
+  bool two = false, two1 = false;
+  const SkinnyPlan p = plan(CfgSkinny::frags(kmb), &two);
+  if (kmb == 8 && !two) {
+    const SkinnyPlan p1 = plan(1, &two1);
+    if (two1) return p1;
   }
   return p;
 }
@@ -219,7 +238,8 @@ hipError_t launch_skinny(const GemmArgs& a, const SkinnyPlan& p, void* ws,
   // One store per lane of 4 columns that never straddle N.
   key.vec = vec_ok(key.out, a.N, a.ldc, a.C, 4);
   const int grid = p.tiles_n * p.slices;
-  const void* fn = key.ext ? hk::skinny_ext(p.kmb, key) : hk::skinny_plain(p.kmb, key);
+  const void* fn = key.ext ? hk::skinny_ext(p.kmb, p.kf, key)
+                           : hk::skinny_plain(p.kmb, p.kf, key);
   if (!fn) return hipErrorInvalidValue;
   void* args1[] = {&g};
   hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(CfgSkinny::kThreads),
@@ -227,7 +247,7 @@ hipError_t launch_skinny(const GemmArgs& a, const SkinnyPlan& p, void* ws,
   if (e != hipSuccess || !reduce_pass) return e;
   int kmb = p.kmb;
   void* args[] = {&g, &kmb};
-  return hipLaunchKernel(hk::skinny_reduce(CfgSkinny::frags(p.kmb), key),
+  return hipLaunchKernel(hk::skinny_reduce(p.kf, key),
                          dim3(p.tiles_n * p.kmb),
                          dim3(CfgSkinny::kThreads), args, 0, stream);
 }

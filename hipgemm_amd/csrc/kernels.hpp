@@ -35,8 +35,8 @@ const void* four_wave_ext_wide(const Key& k);       // k4wave_ext_wide.hip
 const void* eight_wave_plain(const Key& k);         // k8wave_plain.hip
 const void* eight_wave_ext_bf16(const Key& k);      // k8wave_ext_bf16.hip
 const void* eight_wave_ext_f16(const Key& k);       // k8wave_ext_f16.hip
-const void* skinny_plain(int kmb, const Key& k);    // kskinny_plain.hip
-const void* skinny_ext(int kmb, const Key& k);      // kskinny_ext.hip
+const void* skinny_plain(int kmb, int kf, const Key& k);  // kskinny_plain.hip
+const void* skinny_ext(int kmb, int kf, const Key& k);    // kskinny_ext.hip
 const void* skinny_reduce(int kf, const Key& k);    // kskinny_plain.hip
 const void* strip_plain(int kmb, int knb, const Key& k);  // kstrip_plain.hip
 const void* strip_ext(int kmb, int knb, const Key& k);    // kstrip_ext.hip

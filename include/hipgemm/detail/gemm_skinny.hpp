@@ -61,13 +61,12 @@ struct CfgSkinny {
   // B_T fragments (16 columns each) per wave, 4 waves per workgroup: 4 up to
   // 32 rows; 2 above, which halves the workgroup's column tile and so the
   // K-slices and the partial-tile traffic per output (128 x 8192 x 8192:
-  // 16 instead of 32 MiB written and read back).
+  // 16 instead of 32 MiB written and read back).  From 65 rows the plan
+  // may take 1 instead (hipgemm.hip, plan_skinny), for two workgroups per
+  // CU.
   static constexpr int frags(int kmb) { return kmb >= 4 ? 2 : 4; }
-  static constexpr int bn(int kmb) { return 4 * 16 * frags(kmb); }
+  static constexpr int bn_of(int kf) { return 4 * 16 * kf; }
   static constexpr int kMaxM = 128;
-  // Floats of one slice's partial tile.
-  template <int kMB>
-  static constexpr int partial_floats() { return kMB * 16 * bn(kMB); }
 };
 
 // Epilogue of the C elements one lane writes: rows 16 (m0 + m) + l % 16
@@ -96,12 +95,12 @@ struct SkinnyEpi {
 
 // kMB: 16-row blocks of M (M <= 16 kMB).  kVec8: C rows allow 8-byte stores
 // (N % 4 == 0, ldc % 4 == 0, C 8-byte aligned).  kExt: the extended
-// epilogue (SkinnyEpi).
-template <int kMB, bool kVec8, bool kExt = false, int kFmt = 0>
+// epilogue (SkinnyEpi).  kF: B_T fragments per wave.
+template <int kMB, bool kVec8, bool kExt = false, int kFmt = 0,
+          int kF = CfgSkinny::frags(kMB)>
 __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   using Cfg = CfgSkinny;
-  constexpr int kF = Cfg::frags(kMB);  // B_T fragments per wave
-  constexpr int kBN = Cfg::bn(kMB);    // columns per workgroup
+  constexpr int kBN = Cfg::bn_of(kF);  // columns per workgroup
   // A (at most 128 rows) is shared by the four waves: up to 32 rows each
   // wave loads its own copy into registers; above, the workgroup stages it
   // through LDS once (DMA, one barrier per step) so A costs no more HBM or
@@ -255,7 +254,7 @@ __device__ __forceinline__ void gemm_skinny_body(const SkinnyArgs& g) {
   // from waiting for the stores' completion (vmcnt 0) in every wave before
   // the workgroup barrier that precedes the increment.
   constexpr int kCoherent = 16;  // cache policy: sc1
-  const int tile_floats = Cfg::partial_floats<kMB>();
+  const int tile_floats = kMB * 16 * kBN;  // floats of one slice's partial
   const __amdgpu_buffer_rsrc_t rsrc_p = make_rsrc(
       g.partial + (size_t)nt * g.slices * tile_floats,
       (uint32_t)(g.slices * tile_floats * sizeof(float)));
