@@ -225,9 +225,17 @@ SkinnyPlan plan_skinny(int M, int N, int K) {
 hipError_t launch_skinny(const GemmArgs& a, const SkinnyPlan& p, void* ws,
                          hk::Key key, hipStream_t stream) {
   // From 4 row blocks up, one workgroup per column tile summing every slice
-  // (1 MiB of partials per tile at M = 128) is the long pole: a second
-  // kernel sums them over tiles_n x kmb workgroups instead.
-  const int reduce_pass = p.slices > 1 && p.kmb >= 4;
+  // is the long pole when the tile's partials are large (1 MiB at M = 128
+  // with 16 slices): a second kernel sums them over tiles_n x kmb
+  // workgroups instead.  With small partials (at most 32 KiB per slice and
+  // 96 KiB for the last arrival to read) the last arrival sums them itself:
+  // one launch fewer.  Same process: 128 x 8192 x 8192 (64-column tiles, 4
+  // slices) +3.8 %, 64 x 28672 x 4096 (2 slices of 32 KiB) +4.7 %; with 8
+  // slices (128 x 4096 x 14336) or 64 KiB per slice (128 x 28672 x 8192) it
+  // measured equal or 3 % slower, so those keep the second kernel.
+  const size_t partial = (size_t)p.kmb * 16 * p.bn * sizeof(float);
+  const bool small = partial <= (32u << 10) && (size_t)(p.slices - 1) * partial <= (96u << 10);
+  const int reduce_pass = p.slices > 1 && p.kmb >= 4 && !small;
   SkinnyArgs g{a.A, a.B, a.C, a.scale_a, a.scale_b, a.M, a.N, a.K,
                a.lda, a.ldb, a.ldc, p.slices, p.slice_steps, nullptr, nullptr,
                reduce_pass, a.epi};
