@@ -463,7 +463,7 @@ def gemm(a, b_t, *, a_format: int = FMT_E4M3, b_format: int = FMT_E4M3,
                  mx_scale_b=_mx_ptr(mx_scale_b, N, K, "mx_scale_b"),
                  scale_out=_scale_ptr(scale_out, "scale_out"))
     need = int(lib().hipgemm_gemm_workspace_size(ctypes.byref(d)))
-    if need != nbytes:  # the formats decide the schedule (fp4: 128 x 128)
+    if need != nbytes:  # the formats and MX scales decide the schedule
         w = _workspace(a.device, stream, need) if need else None
         d.workspace = w.data_ptr() if w is not None else None
         d.workspace_bytes = need
