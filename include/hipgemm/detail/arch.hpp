@@ -50,10 +50,22 @@ constexpr int kStoreC = 2;
 // build (num_records is always < 2^31): such a lane reads zero.
 constexpr uint32_t kOobOffset = 0x80000000u;
 
+// A buffer resource over [base, base + bytes).  Both must be wave-uniform
+// (every caller builds them from kernel arguments, tile coordinates, the
+// workgroup index or the scalar wave index); they are read from lane 0 into
+// scalar registers.  Where part of the address came out of VALU code (integer
+// division has no scalar form) the compiler would otherwise treat the
+// resource as divergent and wrap every buffer instruction that takes it in a
+// readfirstlane loop.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
                                                            uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
-                                           (int)bytes, kBufferWord3);
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(lo | (hi << 32)),
+                                           (short)0,
+                                           __builtin_amdgcn_readfirstlane((int)bytes),
+                                           kBufferWord3);
 }
 
 // 16 bytes per lane, global (rsrc + voffset + soffset) -> LDS

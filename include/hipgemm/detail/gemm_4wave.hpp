@@ -183,38 +183,26 @@ struct QuarterShape {
   static constexpr int kHead = kMfma - kTail;
 };
 
-// sched_group_barrier pattern of one quarter-step region: the previous
-// quarter's tail MFMA (0x008) first, then this quarter's head MFMA with its
-// 8 LDS reads (0x100) in the first half and its 4 DMA (0x020) after.
-// 32x32x64: [M R R] x 4, [M D] x 2, [M D D].  16x16x128: [M R] x 8,
-// [M D] x 4, [M] x 3 (spreading the DMAs between the reads, or issuing them
-// first, measured 9-10 % slower).
-template <int kMf>
-__device__ __forceinline__ void quarter_schedule(bool tail) {
+// Order of one quarter-step: the previous quarter's tail MFMA first, then
+// this quarter's head MFMA with its LDS reads in the first half and its 4
+// DMA after.  16x16x128: [M R] x 8, [M D] x 4, [M] x 3 (spreading the DMAs
+// between the reads, or issuing them first, measured 9-10 % slower), written
+// out in `quarter`.  32x32x64: [M R R] x 4, [M D] x 2, [M D D], as a
+// sched_group_barrier pattern (0x008 MFMA, 0x100 LDS read, 0x020 DMA) over
+// the whole quarter.
+__device__ __forceinline__ void quarter_schedule_32(bool tail) {
   if (tail)
-    __builtin_amdgcn_sched_group_barrier(0x008, QuarterShape<kMf>::kTail, 0);
-  if constexpr (kMf == 16) {
-    for (int x = 0; x < 8; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    for (int x = 0; x < 4; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-  } else {
-    for (int x = 0; x < 4; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    }
-    for (int x = 0; x < 2; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    }
+    __builtin_amdgcn_sched_group_barrier(0x008, QuarterShape<32>::kTail, 0);
+  for (int x = 0; x < 4; ++x) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
   }
+  for (int x = 0; x < 2; ++x) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
 }
 
 // Operand windows of one output tile: buffer resources over the tile's valid
@@ -228,7 +216,7 @@ __device__ __forceinline__ TileSrc tile_src(const GemmArgs& g, int t,
                                             int end, int tiles_m,
                                             int tiles_n) {
   if (t >= end) return TileSrc{make_rsrc(g.A, 0), make_rsrc(g.B, 0)};
-  const TileCoord tc = grouped_tile(t, tiles_m, tiles_n, g.group_m);
+  const TileCoord tc = grouped_tile_u(t, tiles_m, tiles_n, g.group_m);
   const int rows_a = min(Cfg4w::kBM, g.M - tc.m * Cfg4w::kBM);
   const int rows_b = min(Cfg4w::kBN, g.N - tc.n * Cfg4w::kBN);
   return TileSrc{make_rsrc(g.A + (size_t)tc.m * Cfg4w::kBM * g.lda,
@@ -393,7 +381,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // index goes through an opaque copy, so that nothing here is hoisted out
   // of the tile loop.
   auto scale_dma = [&](int tile) {
-    const TileCoord sc = grouped_tile(tile, tiles_m, tiles_n, g.group_m);
+    const TileCoord sc = grouped_tile_u(tile, tiles_m, tiles_n, g.group_m);
     const EpiArgs ea = kernel_epi();
     const float* pr = ea.row_scale;
     const float* pc = ea.col_scale;
@@ -522,7 +510,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     const int kel = k4 ? 2 * K : K;  // K in elements (K counts bytes of a row)
     const int P = mx_pairs(kel);
     const bool live = tt < walk.end && p < P;
-    const TileCoord c = grouped_tile(live ? tt : t, tiles_m, tiles_n, g.group_m);
+    const TileCoord c = grouped_tile_u(live ? tt : t, tiles_m, tiles_n, g.group_m);
     const __amdgpu_buffer_rsrc_t ra =
         make_rsrc(mx.a, live ? (uint32_t)mx_packed_bytes(M, kel) : 0u);
     const __amdgpu_buffer_rsrc_t rb =
@@ -546,19 +534,19 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // One quarter-step: the previous quarter's tail MFMA (quarter tq) if
   // `tail`, the head MFMA of quarter q, the LDS reads of register tile
   // (rop, rhi) of stage rst, and DMA group (dop, dhi) of step kb into stage
-  // dst, in the order of quarter_schedule.  The scheduler follows that
-  // pattern for the default instantiation (e4m3, per-tensor epilogue), but
-  // for the extended-epilogue ones and other formats it clustered the DMAs
-  // and the reads instead (4 % slower): there the order is written out, one
-  // scheduling region per pair.  (Written out for the default instantiation
-  // too, it measured 0.6 % slower than the scheduler's own placement of the
-  // address arithmetic.)
+  // dst, in the order of quarter_schedule_32.  For 16x16x128 the order is
+  // written out, one scheduling region per pair: given only the
+  // sched_group_barrier pattern, the scheduler clustered the DMAs (DDDD) and
+  // the reads in some quarters of some instantiations, and which ones moved
+  // with unrelated changes elsewhere in the kernel (3-7 % slower when it
+  // hit the default instantiation; tests/test_isa_schedule.py checks the
+  // built loops).
   // kMx: w / wt are the scale words of this quarter's step and of the
   // tail's.
   auto quarter = [&](bool tail, int tqi, int tqj, int qi, int qj, int rop,
                      int rhi, int rst, int kb, int dst, int dop, int dhi,
                      const uint32_t* w = nullptr, const uint32_t* wt = nullptr) {
-    if constexpr (k16 && (kExt || kFmt != 0 || kMx)) {
+    if constexpr (k16) {
       if (tail) quarter_mfma(tqi, tqj, QS::kHead, QS::kMfma, wt);
       const DmaSrc d = dma_src(kb, dop);
       sched_fence();
@@ -592,7 +580,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       quarter_mfma(qi, qj, 0, QS::kHead);
       read_tile(rop, rhi, rst);
       dma_group(kb, dst, dop, dhi);
-      quarter_schedule<kMf>(tail);
+      quarter_schedule_32(tail);
     }
   };
 
@@ -747,7 +735,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     };
     int elane = lane;
     asm volatile("" : "+v"(elane));
-    const TileCoord tc = grouped_tile(t, tiles_m, tiles_n, g.group_m);
+    const TileCoord tc = grouped_tile_u(t, tiles_m, tiles_n, g.group_m);
     const int rows_c = min(Cfg::kBM, M - tc.m * Cfg::kBM);
     // Every store is a buffer store over this tile's window of C; a lane
     // whose row or columns fall outside M x N gets an out-of-range offset and

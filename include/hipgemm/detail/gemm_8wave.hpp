@@ -229,7 +229,7 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
     // ---- epilogue: 32 rows at a time through the wave's own 4 KiB --------
     int elane = lane;
     asm volatile("" : "+v"(elane));
-    const TileCoord tc = grouped_tile(t, tiles_m, tiles_n, g.group_m);
+    const TileCoord tc = grouped_tile_u(t, tiles_m, tiles_n, g.group_m);
     const int rows_c = min(Cfg::kBM, M - tc.m * Cfg::kBM);
     const __amdgpu_buffer_rsrc_t rsrc_c = make_rsrc(
         g.C + (size_t)tc.m * Cfg::kBM * g.ldc + (size_t)tc.n * Cfg::kBN,

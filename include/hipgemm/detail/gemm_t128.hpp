@@ -149,7 +149,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
       return Src{make_rsrc(g.A, 0u), make_rsrc(g.B, 0u), 0u, 0, -1, 0};
     const int tile = kSplit ? unit % tiles : unit;
     const int slice = kSplit ? unit / tiles : 0;
-    const TileCoord c = grouped_tile(tile, tiles_m, tiles_n, g.group_m);
+    const TileCoord c = grouped_tile_u(tile, tiles_m, tiles_n, g.group_m);
     const int ra = min(Cfg::kBM, M - c.m * Cfg::kBM);
     const int rb = min(Cfg::kBN, N - c.n * Cfg::kBN);
     const int k0 = slice * steps * kStepBytes;
@@ -379,7 +379,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   // lane; zero past M / N.
   lds_u8* stg = lds + Cfg::kStoreBase + wave * Cfg::kStoreStage;
   auto scale_dma = [&](int tile) {
-    const TileCoord c = grouped_tile(tile, tiles_m, tiles_n, g.group_m);
+    const TileCoord c = grouped_tile_u(tile, tiles_m, tiles_n, g.group_m);
     const EpiArgs ea = kernel_epi();
     int ln = lane;
     asm volatile("" : "+v"(ln));
@@ -456,7 +456,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
               __builtin_bit_cast(i32x4, acc[i][j]), rp,
               (uint32_t)((4 * i + j) * 1024 + lane * 16), 0);
     } else {
-    const TileCoord tc = grouped_tile(t, tiles_m, tiles_n, g.group_m);
+    const TileCoord tc = grouped_tile_u(t, tiles_m, tiles_n, g.group_m);
     const int rows_left = M - tc.m * Cfg::kBM - wm * 64;  // from wave row 0
     const int cols_left = N - tc.n * Cfg::kBN - wn * 64;  // from wave col 0
     auto oob_unless = [](int x, int limit) -> uint32_t {
@@ -599,7 +599,7 @@ __device__ __forceinline__ void gemm_t128_reduce_body(const GemmArgs& g) {
   const int w = blockIdx.x & 3, t = blockIdx.x >> 2;
   if (t >= tiles) return;
   const int wm = w >> 1, wn = w & 1;
-  const TileCoord tc = grouped_tile(t, tiles_m, tiles_n, g.group_m);
+  const TileCoord tc = grouped_tile_u(t, tiles_m, tiles_n, g.group_m);
   const int row0 = tc.m * Cfg::kBM + wm * 64, col0 = tc.n * Cfg::kBN + wn * 64;
   const float s = (g.scale_a ? *g.scale_a : 1.0f) * (g.scale_b ? *g.scale_b : 1.0f);
   EpiVec<4, 4> ev;

@@ -87,5 +87,18 @@ __host__ __device__ inline TileCoord grouped_tile(int t, int tiles_m,
   return TileCoord{m0 + r % rows, r / rows};
 }
 
+// grouped_tile in device code, for a wave-uniform t, with both coordinates
+// moved to scalar registers.  Integer division has no scalar instruction, so
+// the quotients are computed by VALU; left in VGPRs, a buffer resource built
+// from them counts as divergent, and every buffer instruction that takes it
+// is wrapped in a readfirstlane loop (12 extra instructions and a branch per
+// store in the 4-wave epilogue).
+__device__ __forceinline__ TileCoord grouped_tile_u(int t, int tiles_m,
+                                                    int tiles_n, int group_m) {
+  const TileCoord c = grouped_tile(t, tiles_m, tiles_n, group_m);
+  return TileCoord{__builtin_amdgcn_readfirstlane(c.m),
+                   __builtin_amdgcn_readfirstlane(c.n)};
+}
+
 }  // namespace detail
 }  // namespace hipgemm
