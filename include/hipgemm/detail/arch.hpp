@@ -56,7 +56,9 @@ constexpr uint32_t kOobOffset = 0x80000000u;
 // scalar registers.  Where part of the address came out of VALU code (integer
 // division has no scalar form) the compiler would otherwise treat the
 // resource as divergent and wrap every buffer instruction that takes it in a
-// readfirstlane loop.
+// readfirstlane loop.  readfirstlane is convergent: a select between such a
+// resource and another is not speculated (in a loop it becomes a branch), so
+// the resources of the K loops are built once per tile, outside them.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
                                                            uint32_t bytes) {
   const uint64_t p = reinterpret_cast<uint64_t>(base);

@@ -275,6 +275,12 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   const int tiles = tiles_m * tiles_n;
   const int kt_real = (K + Cfg::kBK - 1) / Cfg::kBK;
   const int kt_pad = max(4, (kt_real + 1) & ~1);
+  // Pair kt0 fetches steps kt0 + 2 and kt0 + 3.  The first pair whose DMAs
+  // can reach a step that is not a whole step of the tile (index kt_full
+  // and up: the step K ends inside, padding, the next tile's steps): the
+  // smallest even kt0 >= kt_full - 3.
+  const int kt_full = K / Cfg::kBK;
+  const int kt_edge = max(2, (kt_full - 2) & ~1);
   const int workers = g.workers > 0 ? min((int)gridDim.x, g.workers)
                                     : (int)gridDim.x;
   if ((int)blockIdx.x >= workers) return;
@@ -338,13 +344,21 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // DMA of one sub-buffer group of pipeline step kb into `stage`: operand op
   // (0 = A, 1 = B), half hi (0 = lo group, 1 = hi group).  Steps kb >= kt_pad
   // are steps kb - kt_pad of the next tile.  4 instructions per wave.
+  // `edge` (std::true_type) DMAs may fetch the next tile's steps, a padding
+  // step, or the step K ends inside (K not a multiple of 128): lanes whose
+  // chunk lies at or past K get an out-of-range offset and read zero, one
+  // VALU select per instruction.  The other DMAs (steady pairs, kt_edge)
+  // fetch whole steps of the current tile and take the lane offsets as they
+  // are: a select on every DMA was 24 VALU per wave-step and cost 2-4 % at
+  // 4096^3 .. 8192x8192x28672.
   struct DmaSrc {
     __amdgpu_buffer_rsrc_t src;
     uint32_t k0;
-    bool ok;
+    bool ok;  // this lane's chunk is below K (read by edge DMAs only)
   };
-  auto dma_src = [&](int kb, int op) {
-    const bool next = kb >= kt_pad;  // wave-uniform
+  auto dma_src = [&](int kb, int op, auto edge) {
+    constexpr bool kEdge = decltype(edge)::value;
+    const bool next = kEdge && kb >= kt_pad;  // wave-uniform
     uint32_t k0 = (uint32_t)(next ? kb - kt_pad : kb) * Cfg::kBK;
     // Opaque to the optimiser: keeps the per-step lane masks from being
     // hoisted out of the tile loop (they would pin VGPRs and spill).
@@ -353,19 +367,23 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                   (int)(k0 + dchunk * 16) < K};
   };
   // Instruction qq (0..3) of the group.
-  auto dma_one = [&](const DmaSrc& d, int stage, int op, int hi, int qq) {
+  auto dma_one = [&](const DmaSrc& d, int stage, int op, int hi, int qq,
+                     auto edge) {
+    constexpr bool kEdge = decltype(edge)::value;
     const int q = (qq & 1) + 4 * (qq >> 1) + 2 * hi;
+    const uint32_t va = kEdge ? (d.ok ? voff_a[q] : kOobOffset) : voff_a[q];
+    const uint32_t vb = kEdge ? (d.ok ? voff_b[q] : kOobOffset) : voff_b[q];
     if (op == 0)
       dma16(d.src, lds + Cfg::kABase + stage * Cfg::kAStage + (4 * q + wave) * 1024,
-            d.ok ? voff_a[q] : kOobOffset, d.k0);
+            va, d.k0);
     else
       dma16(d.src, lds + Cfg::kBBase + stage * Cfg::kBStage + (4 * q + wave) * 1024,
-            d.ok ? voff_b[q] : kOobOffset, d.k0);
+            vb, d.k0);
   };
-  auto dma_group = [&](int kb, int stage, int op, int hi) {
-    const DmaSrc d = dma_src(kb, op);
+  auto dma_group = [&](int kb, int stage, int op, int hi, auto edge) {
+    const DmaSrc d = dma_src(kb, op, edge);
 #pragma unroll
-    for (int qq = 0; qq < kDmaPerGroup; ++qq) dma_one(d, stage, op, hi, qq);
+    for (int qq = 0; qq < kDmaPerGroup; ++qq) dma_one(d, stage, op, hi, qq, edge);
   };
 
   // kExt: the wave's 128 row scales, 128 column scales and 128 biases of
@@ -543,12 +561,12 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // built loops).
   // kMx: w / wt are the scale words of this quarter's step and of the
   // tail's.
-  auto quarter = [&](bool tail, int tqi, int tqj, int qi, int qj, int rop,
-                     int rhi, int rst, int kb, int dst, int dop, int dhi,
+  auto quarter = [&](auto edge, bool tail, int tqi, int tqj, int qi, int qj,
+                     int rop, int rhi, int rst, int kb, int dst, int dop, int dhi,
                      const uint32_t* w = nullptr, const uint32_t* wt = nullptr) {
     if constexpr (k16) {
       if (tail) quarter_mfma(tqi, tqj, QS::kHead, QS::kMfma, wt);
-      const DmaSrc d = dma_src(kb, dop);
+      const DmaSrc d = dma_src(kb, dop, edge);
       sched_fence();
       i32x4 rd[8];
 #pragma unroll
@@ -562,7 +580,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         quarter_mfma(qi, qj, 8 + n, 9 + n, w);
-        dma_one(d, dst, dop, dhi, n);
+        dma_one(d, dst, dop, dhi, n, edge);
         __builtin_amdgcn_sched_group_barrier(0x008, kMfmaPerBlock, 0);
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         sched_fence();
@@ -579,7 +597,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       if (tail) quarter_mfma(tqi, tqj, QS::kHead, QS::kMfma);
       quarter_mfma(qi, qj, 0, QS::kHead);
       read_tile(rop, rhi, rst);
-      dma_group(kb, dst, dop, dhi);
+      dma_group(kb, dst, dop, dhi, edge);
       quarter_schedule_32(tail);
     }
   };
@@ -590,7 +608,9 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // Two pipeline steps kt0, kt0 + 1 (stages 0, 1).  kFirst: the tile's first
   // two steps, whose first three barriers wait past the previous tile's
   // epilogue stores.
-  auto step_pair = [&](int kt0, auto first) {
+  // edge: std::true_type when one of the pair's DMAs may fetch a step that
+  // K ends inside (see dma_src).
+  auto step_pair = [&](int kt0, auto first, auto edge) {
     constexpr bool kFirst = decltype(first)::value;
     // One barrier per half step (before quarters 00 and 10).  Quarter q
     // refills, for step kt + 2, the LDS group whose last read was at least
@@ -633,16 +653,16 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
         if constexpr (kMx)
           if (s == 0) mx_load(kt0 + 2, mxn);
       }
-      quarter(tail, 1, 1, 0, 0, 1, 1, s, kt + 2, s, 0, 0, w, mxp);
+      quarter(edge, tail, 1, 1, 0, 0, 1, 1, s, kt + 2, s, 0, 0, w, mxp);
       wait_lgkmcnt<0>();  // Q01
-      quarter(true, 0, 0, 0, 1, 0, 1, s, kt + 2, s, 1, 0, w, w);
+      quarter(edge, true, 0, 0, 0, 1, 0, 1, s, kt + 2, s, 1, 0, w, w);
       wait_lgkmcnt<0>();
       if (kFirst && s == 0 && stores_in_flight && !k4Mx) wait_vmcnt<kWaitAfterStores>();
       else wait_vmcnt<kWaitSteady>();
       barrier();  // Q10
-      quarter(true, 0, 1, 1, 0, 0, 0, s ^ 1, kt + 2, s, 1, 1, w, w);
+      quarter(edge, true, 0, 1, 1, 0, 0, 0, s ^ 1, kt + 2, s, 1, 1, w, w);
       wait_lgkmcnt<0>();  // Q11
-      quarter(true, 1, 0, 1, 1, 1, 0, s ^ 1, kt + 2, s, 0, 1, w, w);
+      quarter(edge, true, 1, 0, 1, 1, 1, 0, s ^ 1, kt + 2, s, 0, 1, w, w);
       if constexpr (kMx)
 #pragma unroll
         for (int q = 0; q < kMxW; ++q) mxp[q] = w[q];
@@ -665,10 +685,10 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // waits for everything: its scale loads follow the DMAs.
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
-    dma_group(st, st, 0, 0);
-    dma_group(st, st, 1, 0);
-    dma_group(st, st, 1, 1);
-    dma_group(st, st, 0, 1);
+    dma_group(st, st, 0, 0, std::true_type{});
+    dma_group(st, st, 1, 0, std::true_type{});
+    dma_group(st, st, 1, 1, std::true_type{});
+    dma_group(st, st, 0, 1, std::true_type{});
   }
   if constexpr (kMx) {
     mx_load(0, mxc);
@@ -696,8 +716,13 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
     }
 
-    step_pair(0, std::true_type{});
-    for (int kt0 = 2; kt0 < kt_pad; kt0 += 2) step_pair(kt0, std::false_type{});
+    // Edge DMAs for the first pair (one per tile) and from kt_edge on.
+    step_pair(0, std::true_type{}, std::true_type{});
+    int kt0 = 2;
+    for (; kt0 < kt_edge; kt0 += 2)
+      step_pair(kt0, std::false_type{}, std::false_type{});
+    for (; kt0 < kt_pad; kt0 += 2)
+      step_pair(kt0, std::false_type{}, std::true_type{});
 
     last_tail();
     // The tail's accumulator is read only by the epilogue's explicit

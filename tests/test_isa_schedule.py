@@ -7,9 +7,10 @@
    v_readfirstlane, two compares, an exec save and a branch per store.  The
    resources here are wave-uniform by construction (make_rsrc in
    include/hipgemm/detail/arch.hpp reads them from lane 0).
-2. The steady K loop of every 16x16x128 4-wave kernel issues its LDS reads
-   and its DMAs one per MFMA block: never two DMAs or two reads back to
-   back.  Given only a sched_group_barrier pattern, the scheduler clustered
+2. The K loops of every 16x16x128 4-wave kernel issue their LDS reads
+   and DMAs one per MFMA block: never two DMAs or two reads back to back;
+   and the steady loop (whole steps of the tile) has no VALU besides the
+   MFMA (a per-lane K-tail select on each DMA there cost 2-4 %).  Given only a sched_group_barrier pattern, the scheduler clustered
    them in some quarters, and an unrelated change elsewhere in the kernel
    moved the clustering into the default instantiation (3-7 % slower); the
    order is now written out (`quarter` in gemm_4wave.hpp), and this checks
@@ -72,25 +73,27 @@ def readfirstlane_loops(insns, func_addr_of):
     return hits
 
 
-def k_loop_pattern(insns, func_addr_of):
-    """M / R / D string of the innermost loop with >= 64 MFMA, or None."""
-    best = None
+def k_loops(insns, func_addr_of):
+    """The K loops: loops of one step pair, 64-256 MFMA (the tile loop that
+    holds them has more).  Each as (M / R / D pattern, non-MFMA VALU count)."""
+    out = []
     for s, e in loops(insns, func_addr_of):
         body = insns[s:e + 1]
         n = sum(op.startswith("v_mfma") for _, op, _ in body)
-        if n >= 64 and (best is None or n < best[0]):
-            best = (n, body)
-    if best is None:
-        return None
-    pat = ""
-    for _, op, rest in best[1]:
-        if op.startswith("v_mfma"):
-            pat += "M"
-        elif op.startswith("ds_read"):
-            pat += "R"
-        elif op.startswith("buffer_load") and rest.split("//")[0].rstrip().endswith("lds"):
-            pat += "D"
-    return pat
+        if not 64 <= n <= 256:
+            continue
+        pat, valu = "", 0
+        for _, op, rest in body:
+            if op.startswith("v_mfma"):
+                pat += "M"
+            elif op.startswith("ds_read"):
+                pat += "R"
+            elif op.startswith("buffer_load") and rest.split("//")[0].rstrip().endswith("lds"):
+                pat += "D"
+            elif op.startswith("v_"):
+                valu += 1
+        out.append((pat, valu))
+    return out
 
 
 def disassemble(tmp_path):
@@ -138,23 +141,33 @@ def test_no_readfirstlane_loops(tmp_path):
 @needs_lib[0]
 @needs_lib[1]
 def test_4wave_16x16x128_loops_interleave(tmp_path):
-    checked, bad = 0, []
+    """Every K loop interleaves; each kernel without MX scales has a steady
+    loop (the pairs that fetch whole steps of the tile) with no VALU besides
+    the MFMA."""
+    checked, bad, valu = 0, [], []
     for asm in disassemble(tmp_path):
         fa = addr_map(asm)
         for name, insns in functions(asm).items():
             if "4wave" not in name or not any(
                     "16x16x128" in op for _, op, _ in insns):
                 continue
-            pat = k_loop_pattern(insns, fa)
-            if pat is None:
+            ks = k_loops(insns, fa)
+            if not ks:
                 continue
             checked += 1
-            assert pat.count("D") >= 16 and pat.count("R") >= 32, (name, pat)
-            if "DD" in pat or "RR" in pat:
-                bad.append(f"{name}: {pat}")
+            # steady and edge (an edge loop may show two back edges)
+            assert len(ks) >= 2, (name, len(ks))
+            for pat, _ in ks:
+                assert pat.count("D") >= 16 and pat.count("R") >= 32, (name, pat)
+                if "DD" in pat or "RR" in pat:
+                    bad.append(f"{name}: {pat}")
+            # MX kernels load their block scales with VALU address work
+            if "_mx" not in name and min(v for _, v in ks) != 0:
+                valu.append(f"{name}: {[v for _, v in ks]}")
     # plain, MX and extended-epilogue units, every format
-    assert checked >= 100, f"only {checked} 16x16x128 4-wave loops found"
+    assert checked >= 100, f"only {checked} 16x16x128 4-wave kernels found"
     assert not bad, f"{len(bad)} clustered loops, e.g.:\n" + "\n".join(bad[:3])
+    assert not valu, f"{len(valu)} kernels with VALU in the steady loop:\n" + "\n".join(valu[:3])
 
 
 def test_pattern_scanner():
@@ -173,7 +186,8 @@ def test_pattern_scanner():
                              ("ds_read_b128", " v[0:3], v1")] * 64 +
         [("v_mfma_f32_16x16x128_f8f6f4", ""),
          ("buffer_load_dwordx4", " v1, s[4:7], s8 offen lds")] * 32)]
+    body.append((4 * len(body), "v_cndmask_b32_e32", " v1, v2, v3, vcc"))
     body.append((4 * len(body), "s_cbranch_scc0", " 1 " + f % 0))
-    pat = k_loop_pattern(body, lambda n: 0)
-    assert pat == "MR" * 64 + "MD" * 32
+    (pat, valu), = k_loops(body, lambda n: 0)
+    assert pat == "MR" * 64 + "MD" * 32 and valu == 1
     assert "DD" not in pat and "RR" not in pat
