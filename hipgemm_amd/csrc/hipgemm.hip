@@ -525,8 +525,6 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
                   : resolve_variant(variant, M, N, K);
   // MX: the 128 x 128 schedule where AUTO picks it, else the 4-wave one.
   if (mx && variant != HIPGEMM_VARIANT_TILE128) variant = HIPGEMM_VARIANT_4WAVE_MFMA16;
-  if (variant == HIPGEMM_VARIANT_8WAVE && d.out_dtype >= HIPGEMM_OUT_F32)
-    variant = HIPGEMM_VARIANT_4WAVE_MFMA16;  // AUTO's 8-wave choice
   if (K == 0) lda = ldb = 16;  // nothing is read; keep the offset math inert
   const int tiles_m = (M + Cfg4w::kBM - 1) / Cfg4w::kBM;
   const int tiles_n = (N + Cfg4w::kBN - 1) / Cfg4w::kBN;
@@ -669,23 +667,23 @@ int hipgemm_select_variant(int M, int N, int K) {
   // split-K schedule, 32 rows 15.1 against 21.6, 64 rows 21.0 against 24.9.
   // From 65 to 128 rows the split-K schedule, whose 128-column tiles read A
   // a quarter as often as a 32-column strip (128 x 8192 x 8192: 30.8 us
-  // against 37.3 with 32 columns, 31.4 with 64).  Above, the 4-wave 16x16x128 schedule (1-2 %
-  // ahead of the 8-wave one from 4096^3 up, and at 4000 x 5000 x 3584),
-  // except for short K on few tiles (a fraction of one round over the CUs),
-  // where the 8-wave one is 3-12 % ahead (2048^3, 512^3).  Measured on
-  // MI355X, schedules compared in one process.
-  //
-  // When the 128 x 128 tiles fit in one round over the CUs (the 256 x 256
-  // ones then fill at most a quarter of them), the 128 x 128 schedule
-  // (2048^3: 1.69x the 8-wave one).  AUTO also splits C between the 4-wave
-  // and 128 x 128 schedules for a short last round (hipgemm_split_columns);
-  // this returns the 4-wave one then.
-  (void)K;
+  // against 37.3 with 32 columns, 31.4 with 64).  Above, the 4-wave
+  // 16x16x128 schedule (3-7 % ahead of the 8-wave one from 2048 x 4096 up),
+  // except where the 128 x 128 tiles fit in one round over the CUs (the
+  // 256 x 256 ones then fill at most a quarter of them; 2048^3: 1.69x the
+  // 8-wave one), and for short K on at most 128 tiles of 256 x 256 (half a
+  // round), where the 128 x 128 schedule is level or ahead (3072 x 2048 x
+  // 2048 +12 %, 2048 x 4096 x 512 +8 %, 2048 x 4096 x 2048 +1.4 %,
+  // 2048 x 4096 x 1024 -0.6 %; from K = 3072, or above 128 tiles, the 4-wave
+  // one leads by 3-48 %).  Measured on MI355X, schedules compared in one
+  // process.  AUTO also splits C between the 4-wave and 128 x 128 schedules
+  // for a short last round (hipgemm_split_columns); this returns the 4-wave
+  // one then.
   if (M <= 64) return HIPGEMM_VARIANT_STRIP;
   if (M <= CfgSkinny::kMaxM) return HIPGEMM_VARIANT_SKINNY;
   if (ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN) <= cu_count())
     return HIPGEMM_VARIANT_TILE128;
-  if (K <= 2048 && tiles_of(M, N) <= 128) return HIPGEMM_VARIANT_8WAVE;
+  if (K <= 2048 && tiles_of(M, N) <= 128) return HIPGEMM_VARIANT_TILE128;
   return HIPGEMM_VARIANT_4WAVE_MFMA16;
 }
 

@@ -59,8 +59,8 @@ enum {
    * persistent grid, v_mfma_f32_32x32x64_f8f6f4. */
   HIPGEMM_VARIANT_4WAVE = 1,
   /* The same schedule on v_mfma_f32_16x16x128_f8f6f4: AUTO's choice for
-   * M > 128 when the 256 x 256 tiles fill the CUs (but see 8WAVE, TILE128
-   * and hipgemm_split_columns), and the schedule behind the drop-in
+   * M > 128 when the 256 x 256 tiles fill the CUs (but see TILE128 and
+   * hipgemm_split_columns), and the schedule behind the drop-in
    * template. */
   HIPGEMM_VARIANT_4WAVE_MFMA16 = 2,
   /* M <= 128 only: split-K over every CU for the HBM-bound skinny shapes,
@@ -70,17 +70,18 @@ enum {
   HIPGEMM_VARIANT_SKINNY = 3,
   /* 512 threads (8 waves, two per SIMD, in two groups that alternate
    * between LDS/DMA work and MFMAs), 256 x 256 tile, each wave 128 x 64 of
-   * it, persistent grid, v_mfma_f32_16x16x128_f8f6f4.  AUTO's choice for
-   * M > 128 with K <= 2048 on at most 128 tiles of 256 x 256 when the
-   * 128 x 128 tiles take more than one round.  The reference's kernels are
-   * 4-wave only; no reference counterpart. */
+   * it, persistent grid, v_mfma_f32_16x16x128_f8f6f4.  Never AUTO's
+   * choice (3-7 % behind the 4-wave one from 2048 x 4096 up, behind the
+   * 128 x 128 one below).  The reference's kernels are 4-wave only; no
+   * reference counterpart. */
   HIPGEMM_VARIANT_8WAVE = 4,
   /* 256 threads (4 waves, one per SIMD), 128 x 128 tile, each wave 64 x 64
    * of it, 4 LDS stages, persistent grid, v_mfma_f32_16x16x128_f8f6f4: four
    * times as many tiles as the 256 x 256 schedules, for shapes whose 256 x
    * 256 tiles underfill the CUs: AUTO's choice for M > 128 when its tiles
-   * fit in one round over the CUs.  No reference counterpart (the reference
-   * has 256 x 256 tiles only). */
+   * fit in one round over the CUs, or for K <= 2048 on at most 128 tiles of
+   * 256 x 256.  No reference counterpart (the reference has 256 x 256
+   * tiles only). */
   HIPGEMM_VARIANT_TILE128 = 5,
   /* M <= 128 only: 256 threads, each workgroup a strip of 32 columns of C
    * (64 above 32 rows) over all of K (over a K-slice, with a workspace,

@@ -43,7 +43,8 @@ def test_version_and_variants():
     # 128 x 128 tiles in one round over the (256, without a device) CUs
     assert hg.select_variant(2048, 2048, 2048) == 5
     assert hg.select_variant(512, 512, 512) == 5
-    assert hg.select_variant(2048, 4096, 2048) == 4
+    assert hg.select_variant(2048, 4096, 2048) == 5   # short K, 128 tiles
+    assert hg.select_variant(2048, 4096, 4096) == 2
     assert hg.select_variant(128, 8192, 8192) == 3
     assert hg.select_variant(64, 8192, 8192) == 6
     assert hg.select_variant(16, 8192, 8192) == 6
