@@ -38,6 +38,8 @@
 // fp8_4wave.hpp:334-567 and :594-708).
 #pragma once
 
+#include <type_traits>
+
 #include "arch.hpp"
 #include "gemm_4wave.hpp"
 #include "layout.hpp"
@@ -154,7 +156,16 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
     if (grp == 1) barrier();  // group 1 starts half a step later
 
     int bs = 0;  // B stage of step j (j % 3)
-    for (int j = 0; j < kt; ++j) {
+    // Step j's memory phase fetches steps j + 1 and j + 2.  Up to j_edge
+    // those are whole steps of the tile (below kt_full = K / 128) and the
+    // DMAs take the lane offsets as they are; from there (the step K ends
+    // inside, steps past the end) each lane's chunk is checked against K
+    // (a VALU select per DMA, which in every step cost the 4-wave schedule
+    // 2-4 %).
+    const int kt_full = K / Cfg::kBK;
+    const int j_edge = min(kt, max(0, kt_full - 2));
+    auto step = [&](int j, auto edge) {
+      constexpr bool kEdge = decltype(edge)::value;
       // ---- memory phase of step j: LDS -> registers and 8 DMAs ------------
       // Group 0: A rows 128-255 of step j + 1 (into the stage of step j - 1,
       // last read by group 1 in phase 2j - 1) and B rows 128-255 of step
@@ -168,7 +179,7 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
       const uint32_t pa = off_a + (j & 1) * Cfg::kAStage;
       const uint32_t pb = off_b + bs * Cfg::kBStage;
       const int kba = grp == 0 ? j + 1 : j + 2, kbb = j + 2;
-      const bool oka = k_ok(kba), okb = k_ok(kbb);
+      const bool oka = !kEdge || k_ok(kba), okb = !kEdge || k_ok(kbb);
       const uint32_t dsta = grp == 0 ? a_stage(j + 1) : a_stage(j);
       const uint32_t dstb = Cfg::kBBase + (bs == 0 ? 2 : bs - 1) * Cfg::kBStage;
       const int q0 = (grp == 0 ? 16 : 0) + wn;
@@ -222,7 +233,10 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
         wait_vmcnt<Cfg::kDmaPhase>();
       barrier();
       bs = bs == 2 ? 0 : bs + 1;
-    }
+    };
+    int j = 0;
+    for (; j < j_edge; ++j) step(j, std::false_type{});
+    for (; j < kt; ++j) step(j, std::true_type{});
     if (grp == 0) barrier();  // group 1's last compute phase
     mfma_drain();
 
