@@ -206,23 +206,26 @@ __device__ __forceinline__ void quarter_schedule_32(bool tail) {
 }
 
 // Operand windows of one output tile: buffer resources over the tile's valid
-// rows of A and B_T (none at all past the last tile, so every read is zero).
+// rows of A and B_T (none at all past the last tile, so every read is zero),
+// and its coordinates (0 past the last tile).
 struct TileSrc {
   __amdgpu_buffer_rsrc_t a, b;
+  int tm, tn;
 };
 
 // `end`: one past the last tile index the caller may visit.
 __device__ __forceinline__ TileSrc tile_src(const GemmArgs& g, int t,
                                             int end, int tiles_m,
                                             int tiles_n) {
-  if (t >= end) return TileSrc{make_rsrc(g.A, 0), make_rsrc(g.B, 0)};
+  if (t >= end) return TileSrc{make_rsrc(g.A, 0), make_rsrc(g.B, 0), 0, 0};
   const TileCoord tc = grouped_tile_u(t, tiles_m, tiles_n, g.group_m);
   const int rows_a = min(Cfg4w::kBM, g.M - tc.m * Cfg4w::kBM);
   const int rows_b = min(Cfg4w::kBN, g.N - tc.n * Cfg4w::kBN);
   return TileSrc{make_rsrc(g.A + (size_t)tc.m * Cfg4w::kBM * g.lda,
                            (uint32_t)rows_a * (uint32_t)g.lda),
                  make_rsrc(g.B + (size_t)tc.n * Cfg4w::kBN * g.ldb,
-                           (uint32_t)rows_b * (uint32_t)g.ldb)};
+                           (uint32_t)rows_b * (uint32_t)g.ldb),
+                 tc.m, tc.n};
 }
 
 // kMf selects the MFMA: 32 = v_mfma_f32_32x32x64_f8f6f4 (4 x 4 blocks of
@@ -528,7 +531,9 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     const int kel = k4 ? 2 * K : K;  // K in elements (K counts bytes of a row)
     const int P = mx_pairs(kel);
     const bool live = tt < walk.end && p < P;
-    const TileCoord c = grouped_tile_u(live ? tt : t, tiles_m, tiles_n, g.group_m);
+    // Tile coordinates from the tile's operand windows (no integer division
+    // in the K loop).
+    const TileCoord c{next ? nxt.tm : cur.tm, next ? nxt.tn : cur.tn};
     const __amdgpu_buffer_rsrc_t ra =
         make_rsrc(mx.a, live ? (uint32_t)mx_packed_bytes(M, kel) : 0u);
     const __amdgpu_buffer_rsrc_t rb =
