@@ -1,5 +1,5 @@
 // The 4-wave schedule with the per-tensor epilogue: 16x16x128 for every
-// operand-format pair, 32x32x64 for e4m3 x e4m3.
+// operand-format pair (fp6 included), 32x32x64 for e4m3 x e4m3.
 #include "kernels.hpp"
 
 namespace hipgemm {
@@ -22,8 +22,9 @@ const void* four_wave_plain(int mf, const Key& k) {
     return k.vec ? (const void*)&k_fp8_gemm_4wave<true, 32, 0>
                  : (const void*)&k_fp8_gemm_4wave<false, 32, 0>;
   }
-  // The 8-bit pairs and fp4 x fp4 (kFmtPairFp4).
-  return sel_fmt(k.fmt, [&](auto F) {
+  // The 8-bit pairs, fp4 x fp4 (kFmtPairFp4) and fp6 x fp6
+  // (kFmtPairFp6 + 0..3).
+  return sel_fmt_t128(k.fmt, [&](auto F) {
     return sel2(k.vec, [&](auto V) {
       return (const void*)&k_fp8_gemm_4wave<decltype(V)::value == 1, 16, decltype(F)::value>;
     });

@@ -74,8 +74,8 @@ const void* sel_fmt(int v, F&& f) {
     default: return nullptr;
   }
 }
-// The 128 x 128 schedule's pairs: those of sel_fmt and fp6 x fp6
-// (kFmtPairFp6 + 0..3).
+// The pairs of sel_fmt and fp6 x fp6 (kFmtPairFp6 + 0..3): the 128 x 128
+// schedule's, and the 4-wave schedule's with the per-tensor epilogue.
 template <class F>
 const void* sel_fmt_t128(int v, F&& f) {
   switch (v) {

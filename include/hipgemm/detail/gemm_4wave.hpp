@@ -254,6 +254,13 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // the two halves of one MX scale pair).  Per-tensor epilogue.
   constexpr bool k4 = is_fp4(kFmt);
   static_assert(!k4 || kMf == 16, "fp4: 16x16x128");
+  // fp6 (four elements per three bytes): a step is 128 elements, 96 bytes of
+  // a row -- one MFMA per block, whose operands are six registers.  The
+  // 96 bytes sit in slots 0-5 of the 128-byte LDS row (slots 6 and 7 stay
+  // zero); each lane group reads its 24 bytes as three 8-byte pieces.
+  constexpr bool k6 = is_fp6(kFmt);
+  static_assert(!k6 || (kMf == 16 && !kMx), "fp6: 16x16x128, no MX");
+  constexpr int kStep = k6 ? 96 : Cfg::kBK;  // bytes of a row per step
   constexpr int kMfmaPerBlock = k4 ? 2 : 1;
   // kMx scale words per step and MFMA: 8-bit steps take words 2s, 2s + 1 of
   // their pair's load; an fp4 step is a whole pair (its halves h take words
@@ -276,13 +283,13 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   const int tiles_m = (M + Cfg::kBM - 1) / Cfg::kBM;
   const int tiles_n = (N + Cfg::kBN - 1) / Cfg::kBN;
   const int tiles = tiles_m * tiles_n;
-  const int kt_real = (K + Cfg::kBK - 1) / Cfg::kBK;
+  const int kt_real = (K + kStep - 1) / kStep;
   const int kt_pad = max(4, (kt_real + 1) & ~1);
   // Pair kt0 fetches steps kt0 + 2 and kt0 + 3.  The first pair whose DMAs
   // can reach a step that is not a whole step of the tile (index kt_full
   // and up: the step K ends inside, padding, the next tile's steps): the
   // smallest even kt0 >= kt_full - 3.
-  const int kt_full = K / Cfg::kBK;
+  const int kt_full = K / kStep;
   const int kt_edge = max(2, (kt_full - 2) & ~1);
   const int workers = g.workers > 0 ? min((int)gridDim.x, g.workers)
                                     : (int)gridDim.x;
@@ -304,12 +311,14 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   const int drow = lane >> 3;
   const int dslot = (lane & 7) ^ slot_xor(8 * (wave & 1) + drow);
   const int dchunk = kMx ? kpair_chunk(dslot) : dslot;
+  // fp6: the lanes of slots 6 and 7 always read zero.
+  const uint32_t pad6 = k6 && dchunk >= 6 ? kOobOffset : 0u;
   uint32_t voff_a[8], voff_b[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
     const int row = (4 * q + wave) * 8 + drow;
-    voff_a[q] = (uint32_t)row * (uint32_t)g.lda + dchunk * 16;
-    voff_b[q] = (uint32_t)row * (uint32_t)g.ldb + dchunk * 16;
+    voff_a[q] = ((uint32_t)row * (uint32_t)g.lda + dchunk * 16) | pad6;
+    voff_b[q] = ((uint32_t)row * (uint32_t)g.ldb + dchunk * 16) | pad6;
   }
 
   // ---- ds_read lane geometry: fragment row lane%32; K-half kh, lane group
@@ -340,6 +349,19 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       Cfg::kBBase + (wn * 128 + rrow16) * Cfg::kBK + rslot16 * 16;
   const lds_u8* pa16[2] = {lds + off16_a, lds + (off16_a ^ kHalf16)};
   const lds_u8* pb16[2] = {lds + off16_b, lds + (off16_b ^ kHalf16)};
+  // fp6: lane group g = lane/16 holds bytes 24g .. 24g + 23 of the step
+  // (element boundaries fall on 3-byte multiples), read as three 8-byte
+  // pieces: piece p (byte b = 24g + 8p) of row r sits in slot
+  // (b / 16) ^ slot_xor(r), half (b / 8) % 2.  Each 32-lane half of a read
+  // covers 32 distinct 8-byte bank pairs.
+  uint32_t p6[3];
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    const int b = 24 * (lane >> 4) + 8 * q;
+    p6[q] = (uint32_t)((((b >> 4) ^ slot_xor(rrow16)) << 4) + (((b >> 3) & 1) << 3));
+  }
+  const uint32_t row6_a = Cfg::kABase + (wm * 128 + rrow16) * Cfg::kBK;
+  const uint32_t row6_b = Cfg::kBBase + (wn * 128 + rrow16) * Cfg::kBK;
 
   TileSrc cur = tile_src(g, t, walk.end, tiles_m, tiles_n);
   TileSrc nxt = tile_src(g, t + walk.stride, walk.end, tiles_m, tiles_n);
@@ -362,7 +384,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   auto dma_src = [&](int kb, int op, auto edge) {
     constexpr bool kEdge = decltype(edge)::value;
     const bool next = kEdge && kb >= kt_pad;  // wave-uniform
-    uint32_t k0 = (uint32_t)(next ? kb - kt_pad : kb) * Cfg::kBK;
+    uint32_t k0 = (uint32_t)(next ? kb - kt_pad : kb) * kStep;
     // Opaque to the optimiser: keeps the per-step lane masks from being
     // hoisted out of the tile loop (they would pin VGPRs and spill).
     asm volatile("" : "+s"(k0));
@@ -436,7 +458,30 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       return lds_read16(pa16[n % 2] + stage * Cfg::kAStage + f * 16 * Cfg::kBK);
     return lds_read16(pb16[n % 2] + stage * Cfg::kBStage + f * 16 * Cfg::kBK);
   };
+  // fp6: read n (0..11) of register tile (op, hi): fragment 4 hi + n / 3,
+  // piece n % 3.
+  auto read6_one = [&](int op, int hi, int stage, int n) -> u32x2 {
+    const int f = 4 * hi + n / 3;
+    if (op == 0)
+      return lds_read8(lds + row6_a + stage * Cfg::kAStage + f * 16 * Cfg::kBK + p6[n % 3]);
+    return lds_read8(lds + row6_b + stage * Cfg::kBStage + f * 16 * Cfg::kBK + p6[n % 3]);
+  };
+  // The six registers of an fp6 operand (the MFMA reads no more).
+  auto join6 = [](u32x2 a, u32x2 b, u32x2 c) {
+    return i32x8{(int)a.x, (int)a.y, (int)b.x, (int)b.y, (int)c.x, (int)c.y, 0, 0};
+  };
   auto read_tile = [&](int op, int hi, int stage) {
+    if constexpr (k6) {
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const i32x8 v = join6(read6_one(op, hi, stage, 3 * f),
+                              read6_one(op, hi, stage, 3 * f + 1),
+                              read6_one(op, hi, stage, 3 * f + 2));
+        if (op == 0) fa16[4 * hi + f] = v;
+        else fb16[4 * hi + f] = v;
+      }
+      return;
+    }
     if constexpr (k16) {
 #pragma unroll
       for (int f = 4 * hi; f < 4 * hi + 4; ++f) {
@@ -573,6 +618,36 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       if (tail) quarter_mfma(tqi, tqj, QS::kHead, QS::kMfma, wt);
       const DmaSrc d = dma_src(kb, dop, edge);
       sched_fence();
+      if constexpr (k6) {
+        // 12 eight-byte reads: [M R] x 8, [M D R] x 4, [M] x 3.
+        u32x2 rd6[12];
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+          quarter_mfma(qi, qj, n, n + 1, w);
+          rd6[n] = read6_one(rop, rhi, rst, n);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          sched_fence();
+        }
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          quarter_mfma(qi, qj, 8 + n, 9 + n, w);
+          dma_one(d, dst, dop, dhi, n, edge);
+          rd6[8 + n] = read6_one(rop, rhi, rst, 8 + n);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          sched_fence();
+        }
+        quarter_mfma(qi, qj, 12, QS::kHead, w);
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          const i32x8 v = join6(rd6[3 * f], rd6[3 * f + 1], rd6[3 * f + 2]);
+          if (rop == 0) fa16[4 * rhi + f] = v;
+          else fb16[4 * rhi + f] = v;
+        }
+        return;
+      }
       i32x4 rd[8];
 #pragma unroll
       for (int n = 0; n < 8; ++n) {

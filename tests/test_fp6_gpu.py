@@ -1,5 +1,5 @@
-"""GPU parity of fp6 (OCP E2M3 / E3M2) operands on the 128 x 128 schedule
-against the oracle's hg_gemm_ex.
+"""GPU parity of fp6 (OCP E2M3 / E3M2) operands on the 128 x 128 and 4-wave
+16x16x128 schedules against the oracle's hg_gemm_ex.
 
 Operands are packed LSB first, element k of a row at bits [6k, 6k + 6) of
 its little-endian bit string (include/hipgemm.h).  The inputs keep every
@@ -83,12 +83,15 @@ PAIRS = [(E2M3, E2M3), (E3M2, E3M2), (E2M3, E3M2), (E3M2, E2M3)]
 
 
 @pytest.mark.parametrize("fa,fb", PAIRS, ids=["e2m3", "e3m2", "mixed", "mixed2"])
-@pytest.mark.parametrize("variant", [0, 5], ids=["auto", "tile128"])
+@pytest.mark.parametrize("variant", [0, 2, 5], ids=["auto", "4wave16", "tile128"])
 @pytest.mark.parametrize("M,N,K", [(300, 260, 192), (512, 512, 1024),
                                    (129, 1000, 64), (1100, 700, 4096),
-                                   (200, 300, 4032), (256, 2048, 3072)])
+                                   (200, 300, 4032), (256, 2048, 3072),
+                                   (2304, 3840, 256)])
 def test_fp6_bit_exact(gpu, oracle, M, N, K, fa, fb, variant):
+    # 2304 x 3840: 135 tiles of 256 x 256, so AUTO takes the 4-wave schedule
     say(f"case [v{variant}] fp6 a={fa} b={fb} M={M} N={N} K={K} seed=121 "
+        f"auto={hg.select_variant(M, N, K // 4 * 3)} "
         f"ws={hg.lib().hipgemm_workspace_size(M, N, K // 4 * 3, 5)}")
     A = pack6(rand_codes(fa, (M, K), 121))
     B = pack6(rand_codes(fb, (N, K), 122))
