@@ -255,6 +255,35 @@ def test_k_tails(gpu, oracle, K, variant):
     check_full(oracle, C, A, B, 1.5, 0.5)
 
 
+@pytest.mark.parametrize("K", [128, 256, 384, 512, 640, 768, 1024, 1088, 1152,
+                               1216, 1280, 2112])
+def test_k_loop_edges(gpu, oracle, K, variant):
+    """K around the split of the K loops into steady pairs (DMAs of whole
+    steps, plain lane offsets) and edge pairs (per-lane masks): K a multiple
+    of the 128-byte step with an even or odd step count (a zero padding
+    step), K ending inside a step, and step counts that make the steady
+    loop empty, one pair long or longer.  Ternary inputs: bit-exact."""
+    M, N = 520, 300
+    say(f"case [v{variant}] k-loop-edges M={M} N={N} K={K} seed=17")
+    A, B = gen_ternary(M, N, K, 17)
+    C = run_gpu(gpu, A, B, 2.0, 0.25, variant=variant)
+    check_full(oracle, C, A, B, 2.0, 0.25, exact=True)
+
+
+@pytest.mark.parametrize("K", [1152, 1216])
+@pytest.mark.parametrize("v", [pytest.param(2, id="mfma16"),
+                               pytest.param(4, id="8wave")])
+def test_k_loop_edges_multi_tile(gpu, oracle, K, v):
+    """The same with 17 x 17 = 289 tiles, so that the edge pairs' DMAs also
+    fetch the workgroups' next tiles (K = 1216: the step K ends inside comes
+    right before them).  Ternary inputs: bit-exact."""
+    M = N = 4352
+    say(f"case [v{v}] k-loop-edges-multi M={M} N={N} K={K} seed=19")
+    A, B = gen_ternary(M, N, K, 19)
+    C = run_gpu(gpu, A, B, 1.0, 1.0, variant=v)
+    check_full(oracle, C, A, B, 1.0, 1.0, exact=True)
+
+
 @pytest.mark.parametrize("N,K", [(4352, 272), (4350, 144), (4352, 1040),
                                  (4350, 16)])
 def test_persistent_multi_tile(gpu, oracle, N, K, variant):
