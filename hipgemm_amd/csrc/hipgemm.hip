@@ -153,6 +153,39 @@ hipError_t launch_tiled(int variant, GemmArgs g, hk::Key key,
   return hipLaunchKernel(fn, dim3(grid), dim3(threads), args, 0, stream);
 }
 
+// AUTO's column split (hipgemm_split_columns): g4 columns [0, n1) on the
+// 4-wave 16x16x128 schedule, g1 columns [n1, N) on the 128 x 128 one.  One
+// persistent launch (ksplit_plain.hip) where both take the per-tensor
+// epilogue with 16-byte stores and 8-bit operands: each workgroup runs its
+// 4-wave tiles, then its 128 x 128 ones, so the second part starts on every
+// CU as the first finishes there, without a launch between them.  Else the
+// two schedules one after the other.
+hipError_t launch_split(GemmArgs g4, GemmArgs g1, hk::Key key,
+                        hipStream_t stream) {
+  if (!key.ext && key.fmt < 4 && !g4.mx.a &&
+      vec_ok(key.out, g4.N, g4.ldc, g4.C, 8) &&
+      vec_ok(key.out, g1.N, g1.ldc, g1.C, 8)) {
+    const int cus = cu_count();
+    auto prep = [&](GemmArgs& g, int bm, int bn) {
+      const int tm = (g.M + bm - 1) / bm, tn = (g.N + bn - 1) / bn;
+      g.group_m = default_group_m(tm, tn);
+      g.workers = tm * tn < cus ? tm * tn : cus;
+    };
+    prep(g4, Cfg4w::kBM, Cfg4w::kBN);
+    prep(g1, CfgT128::kBM, CfgT128::kBN);
+    key.vec = true;
+    if (const void* fn = hk::split_plain(key)) {
+      void* args[] = {&g4, &g1};
+      const int grid = g4.workers > g1.workers ? g4.workers : g1.workers;
+      return hipLaunchKernel(fn, dim3(grid), dim3(Cfg4w::kThreads), args, 0,
+                             stream);
+    }
+  }
+  hipError_t e = launch_tiled(HIPGEMM_VARIANT_4WAVE_MFMA16, g4, key, stream);
+  if (e != hipSuccess) return e;
+  return launch_tiled(HIPGEMM_VARIANT_TILE128, g1, key, stream);
+}
+
 // Split-K plan of the skinny schedule: 16-row blocks of M, column tiles of
 // 64 kf columns (kf B_T fragments per wave), K-slices per column tile
 // (enough workgroups to give every CU one, or two, below), and the
@@ -617,9 +650,7 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
                                            (size_t)n1 * es);
         if (g2.epi.col_scale) g2.epi.col_scale += n1;
         if (g2.epi.bias) g2.epi.bias += n1;
-        e = launch_tiled(HIPGEMM_VARIANT_4WAVE_MFMA16, g, key, stream);
-        if (e != hipSuccess) return e;
-        return launch_tiled(HIPGEMM_VARIANT_TILE128, g2, key, stream);
+        return launch_split(g, g2, key, stream);
       }
       return launch_tiled(variant, g, key, stream);
   }

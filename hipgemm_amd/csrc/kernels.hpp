@@ -51,6 +51,7 @@ inline const void* tile128_ext(const Key& k) {
 }
 const void* tile128_split(const Key& k);            // kt128_plain.hip
 const void* tile128_reduce(const Key& k);           // kt128_plain.hip
+const void* split_plain(const Key& k);              // ksplit_plain.hip
 // Packs [rows][ceil(K/32)] E8M0 scales (row stride ld) into MxArgs' layout.
 hipError_t mx_pack(const uint8_t* src, int rows, int K, int ld, uint8_t* dst,
                    hipStream_t stream);

@@ -215,6 +215,21 @@ def test_config5c_auto_split(gpu, oracle):
                exact=True)
 
 
+def test_auto_split_ragged(gpu, oracle):
+    """AUTO's column split with parts of different sizes, run as one
+    launch: 4200 x 4496 x 2048 splits at n1 = 3840 into 17 x 15 = 255 tiles
+    of 256 x 256 (one workgroup without a 4-wave tile) and 33 x 6 = 198 of
+    128 x 128, both with ragged rows and the last 128-column tile ragged
+    too.  Ternary inputs: bit-exact."""
+    M, N, K = 4200, 4496, 2048
+    n1 = hg.split_columns(M, N, K)
+    say(f"case [auto] split-ragged M={M} N={N} K={K} n1={n1} seed=57")
+    assert n1 in (0, 3840)  # 0 only on a device with another CU count
+    A, B = gen_ternary(M, N, K, 57)
+    C = run_gpu(gpu, A, B, 0.5, 1.5, variant=0)
+    check_full(oracle, C, A, B, 0.5, 1.5, exact=True)
+
+
 # ----------------------------------------------------------- edges ---------
 
 @pytest.mark.parametrize("M,N,K", [(300, 260, 208), (1, 1, 16), (257, 255, 80),
