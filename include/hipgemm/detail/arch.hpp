@@ -45,6 +45,12 @@ constexpr int kBufferWord3 = 0x00020000;
 // written in one burst; marked non-temporal it displaces less of the A/B
 // panels the next tiles read from L2 (8192^3: +1.2 %, measured).
 constexpr int kStoreC = 2;
+// Cache policy of the C stores that write part of a line per instruction
+// (straight from the accumulators: fp32 and e4m3 outputs, and the 8-, 2- and
+// 1-byte stores for N or ldc that rule out 16-byte ones): cached, so the L2
+// merges a line before it goes to memory.  Non-temporal, such stores
+// measured 4x slower than cached (8192 x 8192 x 128).
+constexpr int kStoreCPart = 0;
 
 // Any per-lane offset at or above this is out of range for every buffer we
 // build (num_records is always < 2^31): such a lane reads zero.

@@ -936,7 +936,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                                                    i, j);
           if constexpr (kOut == kOutF32) {
             if constexpr (kVecStore) {
-              store_b128<kStoreC>(
+              store_b128<kStoreCPart>(
                   __builtin_bit_cast(i32x4, v), rsrc_c,
                   (vrow | oob_unless(c, cols_left)) + 16 * j * es, srow);
             } else {
@@ -945,21 +945,21 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                 __builtin_amdgcn_raw_buffer_store_b32(
                     (uint32_t)__builtin_bit_cast(i32x4, v)[e], rsrc_c,
                     (vrow | oob_unless(c + e, cols_left)) + (16 * j + e) * es,
-                    srow, kStoreC);
+                    srow, kStoreCPart);
             }
           } else {
             const uint32_t w = ev.e4m3x4(v);
             if constexpr (kVecStore) {
               __builtin_amdgcn_raw_buffer_store_b32(
                   w, rsrc_c, (vrow | oob_unless(c, cols_left)) + 16 * j * es, srow,
-                  kStoreC);
+                  kStoreCPart);
             } else {
 #pragma unroll
               for (int e = 0; e < 4; ++e)
                 __builtin_amdgcn_raw_buffer_store_b8(
                     (uint8_t)(w >> (8 * e)), rsrc_c,
                     (vrow | oob_unless(c + e, cols_left)) + (16 * j + e) * es,
-                    srow, kStoreC);
+                    srow, kStoreCPart);
             }
           }
           sched_fence();  // bound the live range: one block at a time
@@ -1111,7 +1111,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
             if (four) {
               __builtin_amdgcn_raw_buffer_store_b64(
                   v, rsrc_c, (vrow | oob_unless(c, cols_left)) + 16 * j * 2, srow,
-                  kStoreC);
+                  kStoreCPart);
             } else {
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
@@ -1119,7 +1119,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                 __builtin_amdgcn_raw_buffer_store_b16(
                     (unsigned short)w, rsrc_c,
                     (vrow | oob_unless(c + r, cols_left)) + (16 * j + r) * 2,
-                    srow, kStoreC);
+                    srow, kStoreCPart);
               }
             }
             sched_fence();  // bound the live range: one block at a time
@@ -1146,7 +1146,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                     (unsigned short)w, rsrc_c,
                     (vrow | oob_unless(c + r, cols_left)) +
                         (32 * j + 8 * q + r) * 2,
-                    srow, kStoreC);
+                    srow, kStoreCPart);
               }
             }
             sched_fence();  // bound the live range: one block at a time

@@ -330,7 +330,7 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
             const uint32_t w = (q < 2 ? v.x : v.y) >> (16 * (q & 1));
             __builtin_amdgcn_raw_buffer_store_b16(
                 (unsigned short)w, rsrc_c,
-                (vrow | oob_unless(col + q, cols_left)) + (16 * j + q) * 2, srow, kStoreC);
+                (vrow | oob_unless(col + q, cols_left)) + (16 * j + q) * 2, srow, kStoreCPart);
           }
           sched_fence();
         }

@@ -499,7 +499,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
           const f32x4 v = ev.template value4<kAct>(a[0], a[1], a[2], a[3], i, j);
           if constexpr (kOut == kOutF32) {
             if constexpr (kVec) {
-              store_b128<kStoreC>(
+              store_b128<kStoreCPart>(
                   __builtin_bit_cast(i32x4, v), rsrc_c,
                   off | oob_unless(col, cols_left), 0);
             } else {
@@ -507,19 +507,19 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
               for (int e = 0; e < 4; ++e)
                 __builtin_amdgcn_raw_buffer_store_b32(
                     (uint32_t)__builtin_bit_cast(i32x4, v)[e], rsrc_c,
-                    (off | oob_unless(col + e, cols_left)) + 4 * e, 0, kStoreC);
+                    (off | oob_unless(col + e, cols_left)) + 4 * e, 0, kStoreCPart);
             }
           } else {
             const uint32_t w = ev.e4m3x4(v);
             if constexpr (kVec) {
               __builtin_amdgcn_raw_buffer_store_b32(
-                  w, rsrc_c, off | oob_unless(col, cols_left), 0, kStoreC);
+                  w, rsrc_c, off | oob_unless(col, cols_left), 0, kStoreCPart);
             } else {
 #pragma unroll
               for (int e = 0; e < 4; ++e)
                 __builtin_amdgcn_raw_buffer_store_b8(
                     (uint8_t)(w >> (8 * e)), rsrc_c,
-                    (off | oob_unless(col + e, cols_left)) + e, 0, kStoreC);
+                    (off | oob_unless(col + e, cols_left)) + e, 0, kStoreCPart);
             }
           }
         }
@@ -559,7 +559,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
             const uint32_t w = (e < 2 ? pk.x : pk.y) >> (16 * (e & 1));
             __builtin_amdgcn_raw_buffer_store_b16(
                 (unsigned short)w, rsrc_c,
-                (rb | oob_unless(col + e, cols_left)) + 2 * e, 0, kStoreC);
+                (rb | oob_unless(col + e, cols_left)) + 2 * e, 0, kStoreCPart);
           }
         }
     }
