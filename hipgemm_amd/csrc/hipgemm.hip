@@ -353,7 +353,6 @@ hipError_t launch_strip(const GemmArgs& a, const StripPlan& p, void* ws,
 
 int resolve_variant(int variant, int M, int N, int K);
 int fp4_variant(int variant, int M, int N, int Kb);
-int fp6_variant(int variant, int M, int N, int Kb, bool ext);
 
 // K-split plan of the 128 x 128 schedule: when its tiles fill at most a
 // quarter of the CUs and K has at least 16 steps of 128, K-slices of at
@@ -486,9 +485,8 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   // fp4 operands: both, K a multiple of 32 elements, the 128 x 128
   // schedule or the 4-wave 16x16x128 one (fp4_variant); from here on K
   // counts bytes of a row (K / 2).  fp6 operands: both (either variant
-  // each), K a multiple of 64 elements (48 bytes), the 128 x 128 schedule
-  // or, with the per-tensor epilogue, the 4-wave 16x16x128 one; K counts
-  // bytes (3 K / 4).
+  // each), K a multiple of 64 elements (48 bytes), the same schedules as
+  // fp4 (fp4_variant on the byte shape); K counts bytes (3 K / 4).
   const bool fp4 = d.a_format == HIPGEMM_FMT_FP4_E2M1 ||
                    d.b_format == HIPGEMM_FMT_FP4_E2M1;
   auto is6 = [](int f) {
@@ -540,10 +538,8 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
                               2 * (d.b_format == HIPGEMM_FMT_FP6_E3M2)
                         : d.a_format | (d.b_format << 1);
   // The 32x32x64 schedule is built for e4m3 x e4m3 with the per-tensor
-  // epilogue only; fp6 on the 4-wave schedule with the per-tensor one only.
+  // epilogue only.
   if (variant == HIPGEMM_VARIANT_4WAVE && (ext || fmt != 0))
-    return hipErrorInvalidValue;
-  if (fp6 && ext && variant == HIPGEMM_VARIANT_4WAVE_MFMA16)
     return hipErrorInvalidValue;
   // MX block scales: the 4-wave 16x16x128 and 128 x 128 schedules,
   // per-tensor epilogue (K in elements a multiple of 32: bytes of 16 for fp4).
@@ -557,7 +553,7 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   const int n1 = (variant == HIPGEMM_VARIANT_AUTO && !mx && !fp4 && !fp6 && K > 0)
                      ? split_columns(M, N, cu_count())
                      : 0;
-  variant = fp6   ? fp6_variant(variant, M, N, K, ext)
+  variant = fp6   ? fp4_variant(variant, M, N, K)
             : fp4 ? fp4_variant(variant, M, N, K)
                   : resolve_variant(variant, M, N, K);
   // MX: the 128 x 128 schedule where AUTO picks it, else the 4-wave one.
@@ -679,11 +675,11 @@ int resolve_variant(int variant, int M, int N, int K) {
                                          : variant;
 }
 
-// fp4 x fp4 (Kb: bytes of a row).  AUTO: the
-// 4-wave 16x16x128 schedule where it picks that one for 8-bit operands of
-// the same byte shape (a 128-byte step is one MFMA's worth for 8-bit
-// operands, two for fp4: the same LDS bytes per step, twice the flops);
-// else the 128 x 128 one.
+// fp4 x fp4 and fp6 x fp6 (Kb: bytes of a row).  AUTO: the 4-wave 16x16x128
+// schedule where it picks that one for 8-bit operands of the same byte
+// shape (a 128-byte step is one MFMA's worth for 8-bit operands, two for
+// fp4: the same LDS bytes per step, twice the flops; a 96-byte fp6 step is
+// one MFMA of 128 elements); else the 128 x 128 one.
 int fp4_variant(int variant, int M, int N, int Kb) {
   if (variant != HIPGEMM_VARIANT_AUTO) return variant;
   return hipgemm_select_variant(M, N, Kb) == HIPGEMM_VARIANT_4WAVE_MFMA16
@@ -691,13 +687,6 @@ int fp4_variant(int variant, int M, int N, int Kb) {
              : HIPGEMM_VARIANT_TILE128;
 }
 
-// fp6 x fp6 (Kb: bytes of a row).  AUTO: as for fp4, with the per-tensor
-// epilogue (the 4-wave schedule's fp6 kernels have no other); else the
-// 128 x 128 schedule.
-int fp6_variant(int variant, int M, int N, int Kb, bool ext) {
-  if (variant != HIPGEMM_VARIANT_AUTO) return variant;
-  return ext ? HIPGEMM_VARIANT_TILE128 : fp4_variant(variant, M, N, Kb);
-}
 
 }  // namespace
 
@@ -812,10 +801,7 @@ size_t hipgemm_gemm_workspace_size(const hipgemm_gemm_desc* d) {
   const bool fp6 = d->a_format == HIPGEMM_FMT_FP6_E2M3 ||
                    d->a_format == HIPGEMM_FMT_FP6_E3M2;
   if (fp6) {
-    const bool ext = d->scale_rows || d->scale_cols || d->bias ||
-                     d->activation != HIPGEMM_ACT_NONE ||
-                     d->out_dtype != HIPGEMM_OUT_BF16;
-    if (fp6_variant(d->variant, d->M, d->N, d->K / 4 * 3, ext) ==
+    if (fp4_variant(d->variant, d->M, d->N, d->K / 4 * 3) ==
         HIPGEMM_VARIANT_4WAVE_MFMA16)
       return 0;
     return plan_t128(d->M, d->N, d->K / 4 * 3, cu_count(), 96).ws_bytes;

@@ -17,7 +17,7 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm_4wave_ext(GemmArgs g) {
 }  // namespace
 
 const void* four_wave_ext_bf16(const Key& k) {
-  return sel_fmt(k.fmt, [&](auto F) {  // 8-bit pairs and fp4 x fp4
+  return sel_fmt_t128(k.fmt, [&](auto F) {  // 8-bit pairs, fp4 x fp4, fp6 x fp6
     return sel4(k.act, [&](auto A) {
       return sel2(k.vec, [&](auto V) {
         return (const void*)&k_fp8_gemm_4wave_ext<decltype(V)::value == 1,

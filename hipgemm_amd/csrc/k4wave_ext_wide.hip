@@ -18,7 +18,7 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm_4wave_ext_wide(GemmArgs g) 
 
 const void* four_wave_ext_wide(const Key& k) {
   if (k.out != kOutF32 && k.out != kOutF8) return nullptr;
-  return sel_fmt(k.fmt, [&](auto F) {  // 8-bit pairs and fp4 x fp4
+  return sel_fmt_t128(k.fmt, [&](auto F) {  // 8-bit pairs, fp4 x fp4, fp6 x fp6
     return sel4(k.act, [&](auto A) {
       return sel2(k.vec, [&](auto V) {
         if (k.out == kOutF32)

@@ -107,9 +107,9 @@ enum {
  * of a row is bits [6k, 6k + 6) of the row read as one little-endian bit
  * string; A and B_T both fp6 (either variant each), K (in elements) a
  * multiple of 64, lda / ldb in bytes (>= 3K / 4, multiples of 16),
- * schedules AUTO, TILE128 and, with the per-tensor epilogue only,
- * 4WAVE_MFMA16 (AUTO's choice there where it takes that schedule for 8-bit
- * operands of the same byte shape), no MX block scales. */
+ * schedules AUTO, TILE128 and 4WAVE_MFMA16 (AUTO's choice where it takes
+ * that schedule for 8-bit operands of the same byte shape), no MX block
+ * scales. */
 enum {
   HIPGEMM_FMT_E4M3 = 0,     /* E4M3FN: bias 7, max 448, NaN 0x7F/0xFF, no inf */
   HIPGEMM_FMT_E5M2 = 1,     /* E5M2: bias 15, max 57344, IEEE inf and NaN     */

@@ -250,7 +250,7 @@ def test_fp4_entry_validation():
 def test_fp6_entry_validation():
     """fp6 operands: both fp6 (either variant each), K (elements) a multiple
     of 64, lda / ldb in bytes >= 3K / 4, AUTO, the 128 x 128 schedule or
-    (per-tensor epilogue only) the 4-wave 16x16x128 one, no MX scales; the
+    the 4-wave 16x16x128 one, no MX scales; the
     descriptor's workspace query plans the 128 x 128 schedule on 96-byte
     steps of 3K / 4 bytes where it runs, and the 4-wave one needs none."""
     base = dict(A=FAKE, B_T=FAKE, C=FAKE, M=300, N=300, K=256, lda=192,
@@ -259,7 +259,6 @@ def test_fp6_entry_validation():
     for bad in (dict(b_format=0), dict(a_format=1), dict(a_format=4),
                 dict(K=224), dict(lda=176), dict(variant=1), dict(variant=3),
                 dict(variant=4), dict(variant=6),
-                dict(variant=2, out_dtype=2), dict(variant=2, bias=FAKE),
                 dict(mx_scale_a=FAKE, mx_scale_b=FAKE)):
         assert hg.gemm_desc_raw(hg.GemmDesc(**dict(base, **bad))) == INVALID, bad
     L = hg.lib()
@@ -269,12 +268,14 @@ def test_fp6_entry_validation():
                            ldc=2048))
     assert L.hipgemm_gemm_workspace_size(ctypes.byref(d)) == 16384 + 32 * 3 * 65536
     # AUTO takes the 4-wave schedule (no workspace) where it does for 8-bit
-    # operands of the byte shape, with the per-tensor epilogue
+    # operands of the byte shape, with either epilogue
     big = dict(base, M=4096, N=4096, K=4096, lda=3072, ldb=3072, ldc=4096)
     assert hg.select_variant(4096, 4096, 3072) == 2
     assert L.hipgemm_gemm_workspace_size(ctypes.byref(hg.GemmDesc(**big))) == 0
     assert L.hipgemm_gemm_workspace_size(
         ctypes.byref(hg.GemmDesc(**dict(big, variant=2)))) == 0
+    assert L.hipgemm_gemm_workspace_size(
+        ctypes.byref(hg.GemmDesc(**dict(big, out_dtype=2, bias=FAKE)))) == 0
 
 
 def test_mx_entry_validation():

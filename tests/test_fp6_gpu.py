@@ -8,7 +8,8 @@ for bit: E2M3 products are multiples of 2^-6 below 56.25 and K <= 4096
 keeps sums below 2^18; E3M2 codes are drawn with magnitudes <= 3.5
 (products multiples of 2^-8 below 12.25, sums below 2^16).  Covered: the
 four format pairs, K tails (half a 96-byte step), ragged M / N, the K-split
-path, every output type with row / column scales, bias and relu, canaries.
+path, every output type with row / column scales, bias and relu on both
+schedules, canaries.
 Every case prints its name before it touches the GPU.
 """
 import ctypes
@@ -102,11 +103,12 @@ def test_fp6_bit_exact(gpu, oracle, M, N, K, fa, fb, variant):
 
 
 @pytest.mark.parametrize("out", [0, 1, 2, 3], ids=["bf16", "f16", "f32", "e4m3"])
-@pytest.mark.parametrize("shape", [(384, 520, 512), (256, 2048, 3072)],
-                         ids=["plain", "ksplit"])
-def test_fp6_epilogue(gpu, oracle, out, shape):
+@pytest.mark.parametrize("shape,variant", [((384, 520, 512), 5), ((256, 2048, 3072), 5),
+                                           ((384, 520, 512), 2), ((300, 1040, 1088), 2)],
+                         ids=["plain", "ksplit", "4wave16", "4wave16-ragged"])
+def test_fp6_epilogue(gpu, oracle, out, shape, variant):
     M, N, K = shape
-    say(f"case [v5] fp6-epilogue out={out} M={M} N={N} K={K} seed=123")
+    say(f"case [v{variant}] fp6-epilogue out={out} M={M} N={N} K={K} seed=123")
     rng = np.random.default_rng(123)
     A = pack6(rand_codes(E2M3, (M, K), 123))
     B = pack6(rand_codes(E3M2, (N, K), 124))
@@ -114,7 +116,7 @@ def test_fp6_epilogue(gpu, oracle, out, shape):
     sc = np.exp2(rng.integers(-6, -1, N)).astype(np.float32)
     bias = rng.uniform(-4, 4, N).astype(np.float32)
     C, guard = run(gpu, A, B, K, E2M3, E3M2, out=out, act=1, sa=[0.25], sr=sr,
-                   sc=sc, bias=bias, variant=5)
+                   sc=sc, bias=bias, variant=variant)
     assert guard
     want = oracle.gemm_ex(A, B, a_fmt=E2M3, b_fmt=E3M2, out=out, act=1,
                           scale_a=0.25, scale_rows=sr, scale_cols=sc, bias=bias)
