@@ -374,12 +374,15 @@ def test_nan_and_saturation(gpu, oracle, variant):
     B = np.full((300, K), 0xFE, np.uint8)  # -448
     A[5, 17] = 0x7F
     B[299, 0] = 0xFF
-    C = run_gpu(torch, A, B, variant=variant)
-    want = oracle.gemm(A, B)
-    nan = np.isnan(bf16_to_f32(C))
-    assert np.array_equal(nan, np.isnan(bf16_to_f32(want)))
-    assert nan[5].all() and nan[:, 299].all()
-    assert np.array_equal(C[~nan], want[~nan])
+    # no scales and a product of exactly 1.0 (the unit-scale epilogue), and
+    # a scaled one
+    for sa, sb in ((None, None), (2.0, 0.5), (0.5, 0.75)):
+        C = run_gpu(torch, A, B, sa, sb, variant=variant)
+        want = oracle.gemm(A, B, 1.0 if sa is None else sa, 1.0 if sb is None else sb)
+        nan = np.isnan(bf16_to_f32(C))
+        assert np.array_equal(nan, np.isnan(bf16_to_f32(want))), (sa, sb)
+        assert nan[5].all() and nan[:, 299].all()
+        assert np.array_equal(C[~nan], want[~nan]), (sa, sb)
 
 
 def test_scales_bit_exact_on_exact_sums(gpu, oracle, variant):
@@ -387,7 +390,7 @@ def test_scales_bit_exact_on_exact_sums(gpu, oracle, variant):
     M, N, K = 512, 512, 256
     say(f"case [v{variant}] scales-exact")
     A, B = gen_ternary(M, N, K, 10)
-    for sa, sb in ((2.0, 0.25), (0.75, 1.3), (-1.0, 3.0), (1.0, None)):
+    for sa, sb in ((2.0, 0.25), (0.75, 1.3), (-1.0, 3.0), (1.0, None), (2.0, 0.5)):
         C = run_gpu(torch, A, B, sa, sb, variant=variant)
         want = oracle.gemm(A, B, sa, 1.0 if sb is None else sb)
         assert np.array_equal(C, want), (sa, sb)
