@@ -1,0 +1,197 @@
+"""Seeded random sweep of hipgemm_gemm against the oracle's hg_gemm_ex.
+
+Each case draws a shape, a schedule, the operand formats (e4m3 / e5m2 per
+operand), the output type (bf16 / fp16), per-tensor, per-row and per-column
+scales, a bias, relu, and the leading dimensions of A, B_T and C.  Inputs
+are ternary, so every sum is exact in any order and the epilogue is exact
+arithmetic (per-tensor scales, power-of-two row / column scales, one
+rounding of the bias fma, relu, one rounding to the output type): every
+case is bit-exact.  The padding columns of A and B_T hold NaN bytes, so a
+read past K turns outputs into NaN; canaries around C catch writes outside
+M x N.  The cases come from a fixed seed and each prints its parameters
+before it touches the GPU.
+"""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+import hipgemm_amd as hg
+from oracle import pyoracle as po
+from util import say
+
+pytestmark = pytest.mark.gpu
+
+CANARY = 0x7FA5
+TERN = {0: np.array([0xB8, 0x00, 0x38], np.uint8),   # e4m3 -1, 0, +1
+        1: np.array([0xBC, 0x00, 0x3C], np.uint8)}   # e5m2
+NAN_BYTE = 0x7F  # NaN in both e4m3 and e5m2
+SEED = 20261202
+N_CASES = 128
+MAX_MACS = 2e10  # the CPU oracle: about 0.4 s per case at most
+
+
+def draw(rng):
+    """One case's parameters (plain Python values)."""
+    v = int(rng.choice([0, 0, 0, 1, 2, 2, 3, 4, 5, 5, 6]))
+    skinny = v in (3, 6)
+    M = int(rng.integers(1, 129)) if skinny else int(math.exp(rng.uniform(0, math.log(5000))))
+    N = int(math.exp(rng.uniform(0, math.log(5000))))
+    K = 16 * int(math.exp(rng.uniform(0, math.log(512))))
+    while M * N * K > MAX_MACS:
+        K = max(16, K // 2 // 16 * 16)
+    c = dict(variant=v, M=M, N=N, K=K,
+             lda=K + 16 * int(rng.integers(0, 3)),
+             ldb=K + 16 * int(rng.integers(0, 3)),
+             guard=int(rng.integers(0, 41)),
+             seed=int(rng.integers(0, 1 << 30)))
+    if v == 1:  # 32x32x64: e4m3 x e4m3, per-tensor epilogue only
+        c.update(fa=0, fb=0, out=0, act=0, sr=False, sc=False, bias=False)
+    else:
+        c.update(fa=int(rng.integers(0, 2)), fb=int(rng.integers(0, 2)),
+                 out=int(rng.integers(0, 2)), act=int(rng.integers(0, 2)),
+                 sr=bool(rng.integers(0, 2)), sc=bool(rng.integers(0, 2)),
+                 bias=bool(rng.integers(0, 2)))
+    scales = [None, None, 0.5, 1.25, 2.0, 3.0, -1.0]
+    c["sa"] = scales[int(rng.integers(0, len(scales)))]
+    c["sb"] = scales[int(rng.integers(0, len(scales)))]
+    return c
+
+
+CASES = [draw(np.random.default_rng([SEED, i])) for i in range(N_CASES)]
+
+
+def case_id(i, c):
+    return f"{i:02d}-v{c['variant']}-{c['M']}x{c['N']}x{c['K']}"
+
+
+def operand(rng, fmt, rows, K, ld):
+    """rows x ld bytes: ternary in the first K columns, NaN bytes after."""
+    full = np.full((rows, ld), NAN_BYTE, np.uint8)
+    full[:, :K] = TERN[fmt][rng.integers(0, 3, (rows, K))]
+    return full
+
+
+@pytest.mark.parametrize("c", CASES, ids=[case_id(i, c) for i, c in enumerate(CASES)])
+def test_random_case(gpu, oracle, c):
+    torch = gpu
+    say(f"case random {c}")
+    M, N, K = c["M"], c["N"], c["K"]
+    rng = np.random.default_rng(c["seed"])
+    A = operand(rng, c["fa"], M, K, c["lda"])
+    B = operand(rng, c["fb"], N, K, c["ldb"])
+    sr = np.exp2(rng.integers(-3, 4, M)).astype(np.float32) if c["sr"] else None
+    sc = np.exp2(rng.integers(-3, 4, N)).astype(np.float32) if c["sc"] else None
+    bias = rng.uniform(-4, 4, N).astype(np.float32) if c["bias"] else None
+
+    def dev(x):
+        return None if x is None else torch.from_numpy(
+            np.ascontiguousarray(np.atleast_1d(np.float32(x)) if np.isscalar(x) else x,
+                                 np.float32).reshape(-1)).to("cuda")
+
+    t = dict(sa=dev(c["sa"]), sb=dev(c["sb"]), sr=dev(sr), sc=dev(sc), bias=dev(bias))
+    ptr = (lambda x: x.data_ptr() if x is not None else 0)
+    a = torch.from_numpy(A).to("cuda")
+    b = torch.from_numpy(B).to("cuda")
+    ldc = N + c["guard"]
+    buf = torch.full((M + 4, ldc), CANARY, dtype=torch.int16, device="cuda")
+    d = hg.GemmDesc(A=a.data_ptr(), B_T=b.data_ptr(), C=buf.data_ptr() + 2 * ldc * 2,
+                    M=M, N=N, K=K, lda=c["lda"], ldb=c["ldb"], ldc=ldc,
+                    a_format=c["fa"], b_format=c["fb"], out_dtype=c["out"],
+                    activation=c["act"], scale_a=ptr(t["sa"]), scale_b=ptr(t["sb"]),
+                    scale_rows=ptr(t["sr"]), scale_cols=ptr(t["sc"]),
+                    bias=ptr(t["bias"]), variant=c["variant"])
+    need = int(hg.lib().hipgemm_gemm_workspace_size(ctypes.byref(d)))
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device="cuda")
+    d.workspace, d.workspace_bytes = (ws.data_ptr(), need) if need else (0, 0)
+    code = hg.gemm_desc_raw(d, torch.cuda.current_stream().cuda_stream)
+    assert code == 0, code
+    torch.cuda.synchronize()
+    got = buf.cpu().numpy().view(np.uint16)
+    assert np.all(got[:2] == CANARY) and np.all(got[M + 2:] == CANARY)
+    assert np.all(got[2:M + 2, N:] == CANARY)
+    C = np.ascontiguousarray(got[2:M + 2, :N])
+    want = oracle.gemm_ex(np.ascontiguousarray(A[:, :K]), np.ascontiguousarray(B[:, :K]),
+                          a_fmt=c["fa"], b_fmt=c["fb"], out=c["out"], act=c["act"],
+                          scale_a=1.0 if c["sa"] is None else c["sa"],
+                          scale_b=1.0 if c["sb"] is None else c["sb"],
+                          scale_rows=sr, scale_cols=sc, bias=bias)
+    bad = int((C != want).sum())
+    assert bad == 0, f"{bad} of {M * N} outputs differ"
+
+
+# ---- fp4, fp6 and MX block scales ------------------------------------------
+# Exact sums (so bit-exact in any order): fp4 products are multiples of 2^-2
+# below 36, at most 2^18.2 in magnitude for K <= 8192; fp6 E2M3 x E2M3
+# multiples of 2^-6 below 57 (K <= 2048: below 2^17), E3M2 codes kept to
+# magnitudes <= 3.5 (multiples of 2^-8 below 13); MX ternary operands with
+# E8M0 scales 2^-2 .. 2^2 and MXFP4 with 2^-1 .. 2^1 stay within 2^20.
+
+def draw_narrow(rng):
+    kind = str(rng.choice(["fp4", "fp6", "mx8", "mxfp4"]))
+    v = int(rng.choice([0, 2, 5]))
+    M = int(math.exp(rng.uniform(0, math.log(3000))))
+    N = int(math.exp(rng.uniform(0, math.log(3000))))
+    kmax, kq = {"fp4": (8192, 32), "fp6": (2048, 64), "mx8": (4096, 32),
+                "mxfp4": (6144, 32)}[kind]
+    K = kq * max(1, int(math.exp(rng.uniform(0, math.log(kmax // kq)))))
+    c = dict(kind=kind, variant=v, M=M, N=N, K=K, guard=int(rng.integers(0, 41)),
+             seed=int(rng.integers(0, 1 << 30)),
+             sa=[None, 0.5, 1.25, 2.0, -1.0][int(rng.integers(0, 5))])
+    if kind == "fp6":
+        c.update(fa=int(rng.integers(0, 2)) + po.FMT_FP6_E2M3,
+                 fb=int(rng.integers(0, 2)) + po.FMT_FP6_E2M3)
+    elif kind == "mx8":
+        c.update(fa=int(rng.integers(0, 2)), fb=int(rng.integers(0, 2)))
+    else:
+        c.update(fa=4, fb=4)
+    if kind in ("fp4", "fp6"):
+        c.update(out=int(rng.integers(0, 4)), act=int(rng.integers(0, 2)),
+                 sr=bool(rng.integers(0, 2)), sc=bool(rng.integers(0, 2)),
+                 bias=bool(rng.integers(0, 2)))
+    return c
+
+
+NARROW = [draw_narrow(np.random.default_rng([SEED, 1, i])) for i in range(48)]
+
+
+@pytest.mark.parametrize("c", NARROW, ids=[f"{i:02d}-{c['kind']}-v{c['variant']}-"
+                                           f"{c['M']}x{c['N']}x{c['K']}"
+                                           for i, c in enumerate(NARROW)])
+def test_random_narrow_case(gpu, oracle, c):
+    import test_fp6_gpu as t6
+    import test_mx_gpu as tmx
+    say(f"case random-narrow {c}")
+    M, N, K, kind = c["M"], c["N"], c["K"], c["kind"]
+    rng = np.random.default_rng(c["seed"])
+    if kind == "fp4" or kind == "mxfp4":
+        A = rng.integers(0, 256, (M, K // 2)).astype(np.uint8)
+        B = rng.integers(0, 256, (N, K // 2)).astype(np.uint8)
+    elif kind == "fp6":
+        A = t6.pack6(t6.rand_codes(c["fa"], (M, K), c["seed"]))
+        B = t6.pack6(t6.rand_codes(c["fb"], (N, K), c["seed"] + 1))
+    else:
+        A = TERN[c["fa"]][rng.integers(0, 3, (M, K))]
+        B = TERN[c["fb"]][rng.integers(0, 3, (N, K))]
+    sa = None if c["sa"] is None else [c["sa"]]
+    if kind in ("mx8", "mxfp4"):
+        lo, hi = (125, 130) if kind == "mx8" else (126, 129)
+        xa, xb = tmx.scales(rng, M, K, lo, hi), tmx.scales(rng, N, K, lo, hi)
+        C, guard = tmx.run(gpu, A, B, xa, xb, c["fa"], c["fb"], s_a=c["sa"],
+                           variant=c["variant"], ldc_pad=c["guard"], K=K)
+        want = oracle.gemm_mx(A, B, xa, xb, c["fa"], c["fb"],
+                              scale_a=1.0 if c["sa"] is None else c["sa"])
+    else:
+        sr = np.exp2(rng.integers(-3, 4, M)).astype(np.float32) if c["sr"] else None
+        sc = np.exp2(rng.integers(-6, -1, N)).astype(np.float32) if c["sc"] else None
+        bias = rng.uniform(-4, 4, N).astype(np.float32) if c["bias"] else None
+        C, guard = t6.run(gpu, A, B, K, c["fa"], c["fb"], out=c["out"], act=c["act"],
+                          sa=sa, sr=sr, sc=sc, bias=bias, variant=c["variant"],
+                          guard_cols=c["guard"])
+        want = oracle.gemm_ex(A, B, a_fmt=c["fa"], b_fmt=c["fb"], out=c["out"],
+                              act=c["act"], scale_a=1.0 if c["sa"] is None else c["sa"],
+                              scale_rows=sr, scale_cols=sc, bias=bias)
+    assert guard, "write outside the M x N window"
+    bad = int((C != want).sum())
+    assert bad == 0, f"{bad} of {M * N} outputs differ"
