@@ -64,6 +64,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-ceiling", action="store_true",
+                    help="skip the MFMA ceiling probe")
+    ap.add_argument("--ceiling-seconds", type=float, default=2.0,
+                    help="pre-warm of the MFMA ceiling probe")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="before the GEMMs, run one elementwise copy kernel "
                          "over this many MiB (reads N, writes N bytes) as the "
@@ -139,6 +143,54 @@ def cpu_baseline(A_host, B_host, M, N, K, target_s):
                    f"slab, which equals the full-size rate (cost is linear "
                    f"in M)"),
     }
+
+
+def mfma_ceiling(dev, stream, prewarm_s, steps=100, iters=256):
+    """Sustained v_mfma_f32_16x16x128_f8f6f4 rate with register-resident
+    normal(0,1) e4m3 operands and no memory traffic
+    (hipgemm_amd/probe/mfma_ceiling.hip): the rate this GPU holds under its
+    power limit when the matrix unit alone draws power.  One workgroup of 4
+    waves per CU, each wave issuing the 64 MFMA of one K-step of the 4-wave
+    schedule `iters` times per launch (iters 256: the flop of one 8192^3
+    GEMM).  Timed like the GEMM: pre-warm, then `steps` launches between one
+    event pair."""
+    import torch
+    path = os.path.join(ROOT, "hipgemm_amd", "libhipgemm_probe.so")
+    if not os.path.exists(path):
+        raise SystemExit(f"{path} is missing: build first "
+                         "(python -c 'import __graft_entry__ as g; g.build()')")
+    L = ctypes.CDLL(path)
+    L.hipgemm_probe_ops_bytes.restype = ctypes.c_size_t
+    L.hipgemm_probe_mfma_ceiling.argtypes = [ctypes.c_void_p, ctypes.c_void_p,
+                                            ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_void_p]
+    L.hipgemm_probe_mfma_ceiling.restype = ctypes.c_int
+    nbytes = int(L.hipgemm_probe_ops_bytes())
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4242)
+    ops = (torch.randn(nbytes, generator=gen, device=dev)
+           .clamp_(-448, 448).to(torch.float8_e4m3fn))
+    grid = torch.cuda.get_device_properties(dev).multi_processor_count
+    out = torch.empty(grid * 256, dtype=torch.float32, device=dev)
+    sptr = stream.cuda_stream
+
+    def launch(_i):
+        code = L.hipgemm_probe_mfma_ceiling(ops.data_ptr(), out.data_ptr(),
+                                            grid, iters, sptr)
+        if code != 0:
+            raise RuntimeError(f"hipgemm_probe_mfma_ceiling returned {code}")
+
+    res = time_kernel(launch, 20, steps, stream, prewarm_s)
+    flop = grid * 4 * iters * 64 * 2.0 * 16 * 16 * 128
+    tflops = flop / (res["event_ms"] * 1e-3) / 1e12
+    return {"achieved": round(tflops, 1), "unit": "TFLOP/s",
+            "kernel_ms_avg": round(res["event_ms"], 5),
+            "kernel": "mfma_ceiling_16x16x128 (hipgemm_amd/probe/"
+                      "mfma_ceiling.hip)",
+            "what": (f"{grid} workgroups x 4 waves, {iters} x 64 "
+                     "register-resident 16x16x128 e4m3 MFMA per wave, "
+                     "normal(0,1) operands, no memory traffic; "
+                     f"{res['prewarm_launches']} pre-warm launches")}
 
 
 def prewarm(launch, seconds):
@@ -342,6 +394,13 @@ def main():
                          kernel_ms_best=round(res["best_ms"], 5)),
         "cpu_baseline": None,
     }
+    if not args.no_ceiling and roofline["bound"] == "mfma":
+        # After the GEMM, so that its timed loop ran first on a GPU in the
+        # state bench.py always leaves it in.
+        ceil = mfma_ceiling(dev, stream, args.ceiling_seconds)
+        ceil["frac"] = round(achieved / ceil["achieved"], 4)
+        result["roofline"]["mfma_ceiling"] = ceil
+        log(f"bench: MFMA ceiling {ceil}")
     if not args.no_cpu_baseline:
         A_host = As[0].view(torch.uint8).cpu().numpy()
         B_host = Bs[0].view(torch.uint8).cpu().numpy()

@@ -3,7 +3,9 @@
 ``python -m hipgemm_amd.build`` compiles every hipgemm_amd/csrc/*.hip with
 hipcc for gfx950 (in parallel, one object per file under
 hipgemm_amd/_build/), then links them into hipgemm_amd/libhipgemm.so,
-in-tree, so the library travels with the source tree.  No GPU is needed to
+in-tree, so the library travels with the source tree.  It also builds
+hipgemm_amd/libhipgemm_probe.so from probe/mfma_ceiling.hip, the MFMA ceiling
+probe that bench.py reports beside the GEMM.  No GPU is needed to
 build.
 """
 from __future__ import annotations
@@ -22,6 +24,10 @@ CSRC = os.path.join(PKG, "csrc")
 SRCS = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 OBJDIR = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libhipgemm.so")
+# Measurement-only probe (bench.py's MFMA ceiling), a library of its own so
+# that nothing of it is linked into libhipgemm.so.
+PROBE_SRC = os.path.join(PKG, "probe", "mfma_ceiling.hip")
+PROBE_LIB = os.path.join(PKG, "libhipgemm_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -66,6 +72,10 @@ def build(verbose: bool = False, jobs: int = 0) -> str:
     tmp = LIB + ".tmp"
     _run(link_cmd(objs, tmp), verbose)
     os.replace(tmp, LIB)
+    tmp = PROBE_LIB + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, "-shared", f"-I{INCLUDE}", PROBE_SRC, "-o", tmp],
+         verbose)
+    os.replace(tmp, PROBE_LIB)
     return LIB
 
 
