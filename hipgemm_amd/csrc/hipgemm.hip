@@ -409,7 +409,7 @@ hipError_t launch_t128_split(GemmArgs g, const T128Plan& p, void* ws,
   key.vec = vec_ok(key.out, g.N, g.ldc, g.C, 4);
   fn = hk::tile128_reduce(key);
   if (!fn) return hipErrorInvalidValue;
-  return hipLaunchKernel(fn, dim3(tiles * 4), dim3(64), args, 0, stream);
+  return hipLaunchKernel(fn, dim3(tiles * 16), dim3(64), args, 0, stream);
 }
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
@@ -697,9 +697,17 @@ int hipgemm_select_variant(int M, int N, int K) {
   // column-strip schedule (whole-line DMA of B_T, no split-K partials when
   // N / 32 fills the CUs): 16 x 8192 x 8192 12.9 us against 17.8 on the
   // split-K schedule, 32 rows 15.1 against 21.6, 64 rows 21.0 against 24.9.
-  // From 65 to 128 rows the split-K schedule, whose 128-column tiles read A
-  // a quarter as often as a 32-column strip (128 x 8192 x 8192: 30.8 us
-  // against 37.3 with 32 columns, 31.4 with 64).  Above, the 4-wave
+  // From 65 to 128 rows the 128 x 128 schedule (K-sliced where its tiles
+  // fill at most a quarter of the CUs, plan_t128), which DMAs whole lines of
+  // A and B_T and reads A once per 128 columns: 128 x 8192 x 8192 22.6 us
+  // against 28.0 on the split-K schedule, 80 x 8192 x 8192 21.8 / 26.3,
+  // 128 x 28672 x 8192 52.7 / 74.3, 128 x 4096 x 28672 32.9 / 43.6,
+  // 128 x 8192 x 1024 7.9 / 12.8, 128 x 512 x 8192 11.8 / 17.2.  Except
+  // where its K-split stops at 8-step slices short of the CUs (at most
+  // half of them busy) over a B_T of 12 MiB or more, where the split-K
+  // schedule, which fills every CU, stays ahead: 128 x 4096 x 4096 14.0 us
+  // against 16.1, 128 x 2048 x 8192 14.5 / 16.1, 128 x 8192 x 2048
+  // 14.2 / 16.2 (80 rows alike).  Above, the 4-wave
   // 16x16x128 schedule (3-7 % ahead of the 8-wave one from 2048 x 4096 up),
   // except where the 128 x 128 tiles fit in one round over the CUs (the
   // 256 x 256 ones then fill at most a quarter of them; 2048^3: 1.69x the
@@ -712,7 +720,14 @@ int hipgemm_select_variant(int M, int N, int K) {
   // for a short last round (hipgemm_split_columns); this returns the 4-wave
   // one then.
   if (M <= 64) return HIPGEMM_VARIANT_STRIP;
-  if (M <= CfgSkinny::kMaxM) return HIPGEMM_VARIANT_SKINNY;
+  if (M <= CfgSkinny::kMaxM) {
+    const int cus = cu_count();
+    const T128Plan p = plan_t128(M, N, K, cus);
+    const int units = ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN) * p.slices;
+    const bool half_filled = p.slices > 1 && 2 * units <= cus;
+    return half_filled && (long long)N * K >= (12ll << 20) ? HIPGEMM_VARIANT_SKINNY
+                                                          : HIPGEMM_VARIANT_TILE128;
+  }
   if (ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN) <= cu_count())
     return HIPGEMM_VARIANT_TILE128;
   if (K <= 2048 && tiles_of(M, N) <= 128) return HIPGEMM_VARIANT_TILE128;

@@ -65,7 +65,9 @@ enum {
   HIPGEMM_VARIANT_4WAVE_MFMA16 = 2,
   /* M <= 128 only: split-K over every CU for the HBM-bound skinny shapes,
    * operands streamed straight into registers, a deterministic in-kernel
-   * reduction of the K-slices.  AUTO's choice for 64 < M <= 128.  Needs a
+   * reduction of the K-slices.  AUTO's choice for 64 < M <= 128 only where
+   * the 128 x 128 schedule's K-split would leave at least half the CUs idle
+   * over a B_T of 12 MiB or more (e.g. 128 x 4096 x 4096).  Needs a
    * workspace (hipgemm_workspace_size) when it splits K. */
   HIPGEMM_VARIANT_SKINNY = 3,
   /* 512 threads (8 waves, two per SIMD, in two groups that alternate
@@ -80,8 +82,10 @@ enum {
    * times as many tiles as the 256 x 256 schedules, for shapes whose 256 x
    * 256 tiles underfill the CUs: AUTO's choice for M > 128 when its tiles
    * fit in one round over the CUs, or for K <= 2048 on at most 128 tiles of
-   * 256 x 256.  No reference counterpart (the reference has 256 x 256
-   * tiles only). */
+   * 256 x 256, and for 64 < M <= 128 (except as under SKINNY).  Splits K
+   * into slices, summed by a second kernel, when its tiles fill at most a
+   * quarter of the CUs (a workspace then: hipgemm_workspace_size).  No
+   * reference counterpart (the reference has 256 x 256 tiles only). */
   HIPGEMM_VARIANT_TILE128 = 5,
   /* M <= 128 only: 256 threads, each workgroup a strip of 32 columns of C
    * (64 above 32 rows) over all of K (over a K-slice, with a workspace,

@@ -45,7 +45,10 @@ def test_version_and_variants():
     assert hg.select_variant(512, 512, 512) == 5
     assert hg.select_variant(2048, 4096, 2048) == 5   # short K, 128 tiles
     assert hg.select_variant(2048, 4096, 4096) == 2
-    assert hg.select_variant(128, 8192, 8192) == 3
+    assert hg.select_variant(128, 8192, 8192) == 5   # 64 tiles x 4 K-slices
+    assert hg.select_variant(80, 8192, 1024) == 5    # short K, no K-slices
+    assert hg.select_variant(128, 4096, 4096) == 3   # half-filled K-split
+    assert hg.select_variant(65, 2048, 8192) == 3
     assert hg.select_variant(64, 8192, 8192) == 6
     assert hg.select_variant(16, 8192, 8192) == 6
     assert hg.select_variant(129, 8192, 8192) == 5   # 2 x 64 tiles of 128
@@ -132,11 +135,11 @@ def test_workspace_size_and_validation():
     before launching anything."""
     skinny = hg.VARIANTS["skinny"]
     strip = hg.VARIANTS["strip"]
-    assert hg.select_variant(100, 8192, 8192) == skinny
+    assert hg.select_variant(100, 4096, 4096) == skinny
     assert hg.select_variant(129, 8192, 8192) != skinny
-    need = hg.workspace_size(100, 8192, 8192, 0)
+    need = hg.workspace_size(100, 4096, 4096, 0)
     assert need > 0 and need % 256 == 0
-    assert hg.workspace_size(100, 8192, 8192, skinny) == need
+    assert hg.workspace_size(100, 4096, 4096, skinny) == need
     # The strip schedule needs none when N / 32 fills the (256) CUs, and
     # counters plus 2 slices x 128 strips x 16 x 32 fp32 at N = 4096.
     assert hg.workspace_size(16, 8192, 8192, 0) == 0
@@ -144,7 +147,7 @@ def test_workspace_size_and_validation():
     assert hg.workspace_size(512, 8192, 8192, 0) == 0   # 4-wave: none
     assert hg.workspace_size(16, 300, 64, 0) == 0       # one K-step: no split
     assert hg.workspace_size(0, 8192, 8192, 0) == 0
-    args = (FAKE, FAKE, FAKE, 100, 8192, 8192, 8192, 8192, 8192, 0, 0)
+    args = (FAKE, FAKE, FAKE, 100, 4096, 4096, 4096, 4096, 4096, 0, 0)
     assert hg.gemm_raw_ws(*args, 0, 0, need) == INVALID          # no workspace
     assert hg.gemm_raw_ws(*args, 0, FAKE, need - 256) == INVALID  # too small
     assert hg.gemm_raw_ws(*args, 0, FAKE + 64, need) == INVALID   # misaligned

@@ -186,6 +186,24 @@ def test_tile128_k_split(gpu, oracle, out, act):
     assert np.array_equal(C, want), f"{int((C != want).sum())} differ"
 
 
+@pytest.mark.parametrize("M,N,K", [(100, 500, 12272), (128, 256, 20480)])
+def test_tile128_k_split_many_slices(gpu, oracle, M, N, K):
+    """The reduce kernel loads 8 slices per batch: 12 slices (one full batch
+    and a part, ragged M and N, a K tail) and 20 (two full batches and a
+    part), bit-exact on ternary sums, canaries around C."""
+    say(f"case [v5] k-split many slices M={M} N={N} K={K}")
+    ws = hg.workspace_size(M, N, K, 5)
+    tiles = -(-M // 128) * -(-N // 128)
+    slices = (ws - 16384) // (tiles * 65536)  # HIPGEMM_WS_COUNTER_BYTES first
+    say(f"    tiles={tiles} slices={slices}")
+    assert slices > 8 and slices % 8, slices
+    A, B = ternary(0, (M, K), 91), ternary(0, (N, K), 92)
+    C, guard = run(gpu, A, B, sa=[0.25], sb=[4.0], variant=5)
+    assert guard
+    want = oracle.gemm_ex(A, B, scale_a=0.25, scale_b=4.0)
+    assert np.array_equal(C, want), f"{int((C != want).sum())} differ"
+
+
 def test_auto_split_epilogue(gpu, oracle):
     """AUTO's column split with every column-indexed option: the column
     scales and the bias of the 128 x 128 half are offset by the split
