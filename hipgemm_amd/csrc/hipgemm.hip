@@ -356,13 +356,14 @@ int fp4_variant(int variant, int M, int N, int Kb);
 
 // K-split plan of the 128 x 128 schedule: when its tiles fill at most a
 // quarter of the CUs and K has at least 16 steps of 128, K-slices of at
-// least 8 (even) steps so that tiles x slices approaches the CU count; the
-// workspace holds one 64 KiB fp32 partial tile per (tile, slice).  Measured
-// against no split in one process: 256 x 4096 x 14336 (64 tiles, 4 slices)
-// 1.39x; at 128 tiles (2 slices) 3-8 % slower (256 x 8192 x 8192,
-// 512 x 4096 x 8192), so half-filled grids are not split.  Below 129 rows
-// the skinny schedule stays ahead (128 x 8192 x 8192: 555 against 466
-// TFLOP/s split 4 ways).
+// least 8 (even) steps so that tiles x slices approaches the CU count; when
+// they fill at most half of them and K has at least 64 steps, 2 slices of at
+// least 32 steps.  The workspace holds one 64 KiB fp32 partial tile per
+// (tile, slice).  Measured against no split in one process:
+// 256 x 4096 x 14336 (64 tiles, 4 slices) 1.39x; 128 tiles, 2 slices, with
+// the reduce kernel's batched loads: 256 x 8192 x 8192 1.18x,
+// 512 x 4096 x 8192 1.18x, 384 x 4096 x 8192 (96 tiles) 1.19x,
+// 256 x 8192 x 28672 1.66x, but 256 x 8192 x 4096 (16-step slices) 0.89x.
 struct T128Plan {
   int slices = 1, slice_steps = 0;
   size_t ws_bytes = 0;
@@ -375,7 +376,8 @@ T128Plan plan_t128(int M, int N, int K, int cus, int step_bytes = CfgT128::kBK) 
                     ((N + CfgT128::kBN - 1) / CfgT128::kBN);
   const int steps = (K + step_bytes - 1) / step_bytes;
   p.slice_steps = steps;
-  if (tiles <= 0 || 4 * tiles > cus || steps < 16) return p;
+  if (tiles <= 0 || 2 * tiles > cus || steps < 16) return p;
+  if (4 * tiles > cus && steps < 64) return p;
   int sl = cus / tiles < steps / 8 ? cus / tiles : steps / 8;
   if (sl < 2) return p;
   int ss = (steps + sl - 1) / sl;

@@ -58,11 +58,15 @@ def test_tile128_k_split_workspace():
     """The 128 x 128 schedule splits K when its tiles fill at most a quarter
     of the (256) CUs and K has 16+ steps: 256 x 4096 x 14336 is 2 x 32 tiles,
     4 slices of 28 steps, one 64 KiB partial per (tile, slice), after the
-    counter region every workspace starts with (HIPGEMM_WS_COUNTER_BYTES)."""
+    counter region every workspace starts with (HIPGEMM_WS_COUNTER_BYTES).
+    At most half of them and 64+ steps: 2 slices."""
     ctr = 16384
     assert hg.workspace_size(256, 4096, 14336, 5) == ctr + 64 * 4 * 65536
     assert hg.workspace_size(256, 4096, 14336, 0) == ctr + 64 * 4 * 65536  # AUTO
-    assert hg.workspace_size(256, 8192, 8192, 5) == 0    # 128 tiles: no split
+    assert hg.workspace_size(256, 8192, 8192, 5) == ctr + 128 * 2 * 65536
+    assert hg.workspace_size(256, 8192, 4096, 5) == 0    # 128 tiles, 32 steps
+    assert hg.workspace_size(384, 4096, 8192, 5) == ctr + 96 * 2 * 65536
+    assert hg.workspace_size(512, 8192, 8192, 5) == 0    # 256 tiles
     assert hg.workspace_size(256, 4096, 1920, 5) == 0    # 15 steps: no split
     # 300 x 1000 x 4112: 3 x 8 tiles, 33 steps -> 4 slices of 10 steps
     assert hg.workspace_size(300, 1000, 4112, 5) == ctr + 24 * 4 * 65536

@@ -204,6 +204,22 @@ def test_tile128_k_split_many_slices(gpu, oracle, M, N, K):
     assert np.array_equal(C, want), f"{int((C != want).sum())} differ"
 
 
+def test_tile128_k_split_half_filled(gpu, oracle):
+    """Tiles that fill between a quarter and half of the CUs split K in two
+    when K has 64+ steps: 3 x 40 tiles (ragged M and N), 65 steps (a K
+    tail), 2 slices; AUTO takes it; bit-exact on ternary sums, canaries."""
+    M, N, K = 300, 5000, 8272
+    say(f"case [auto] k-split half-filled M={M} N={N} K={K}")
+    assert hg.select_variant(M, N, K) == 5
+    ws = hg.workspace_size(M, N, K, 0)
+    assert ws == 16384 + 3 * 40 * 2 * 65536, ws
+    A, B = ternary(0, (M, K), 95), ternary(1, (N, K), 96)
+    C, guard = run(gpu, A, B, fb=1, sa=[2.0], sb=[0.125], variant=0)
+    assert guard
+    want = oracle.gemm_ex(A, B, b_fmt=1, scale_a=2.0, scale_b=0.125)
+    assert np.array_equal(C, want), f"{int((C != want).sum())} differ"
+
+
 def test_auto_split_epilogue(gpu, oracle):
     """AUTO's column split with every column-indexed option: the column
     scales and the bias of the 128 x 128 half are offset by the split
