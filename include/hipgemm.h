@@ -246,8 +246,9 @@ hipError_t hipgemm_fp8_gemm_bf16_ws(const void *A, const void *B_T, void *C,
  * be NULL for all ones.  The product of the two scales is formed in fp32 and
  * applied to the fp32 accumulator before rounding, as in
  * hipgemm_fp8_gemm_bf16 (which is this call with constant vectors).  Both
- * vectors must be 4-byte aligned.  Accepts AUTO, SKINNY, 4WAVE_MFMA16 and
- * 8WAVE; HIPGEMM_VARIANT_4WAVE returns hipErrorInvalidValue.  Workspace as in
+ * vectors must be 4-byte aligned.  Accepts every schedule but
+ * HIPGEMM_VARIANT_4WAVE, which returns hipErrorInvalidValue (SKINNY and
+ * STRIP for M <= 128 only).  Workspace as in
  * hipgemm_fp8_gemm_bf16_ws, except that workspace == NULL with
  * workspace_bytes == 0 takes a stream-ordered allocation when one is needed,
  * as hipgemm_fp8_gemm_bf16 does.
