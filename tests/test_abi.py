@@ -345,3 +345,23 @@ def test_product_does_not_import_oracle():
     for dirpath, _, files in os.walk(os.path.join(root, "include")):
         for f in files:
             assert "oracle" not in open(os.path.join(dirpath, f)).read(), f
+
+
+def test_mfma_ceiling_probe_library():
+    """bench.py's MFMA ceiling probe is its own library (nothing of it is in
+    libhipgemm.so): it loads, exports its two entry points, reads 2 MiB of
+    operands (64 sets x 16 fragments x 64 lanes x 32 bytes) and rejects bad
+    arguments before launching."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    path = os.path.join(root, "hipgemm_amd", "libhipgemm_probe.so")
+    L = ctypes.CDLL(path)
+    L.hipgemm_probe_ops_bytes.restype = ctypes.c_size_t
+    assert L.hipgemm_probe_ops_bytes() == 64 * 16 * 64 * 32
+    f = L.hipgemm_probe_mfma_ceiling
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                  ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    assert f(None, None, 256, 256, None) == INVALID
+    assert f(FAKE, FAKE, 0, 256, None) == INVALID
+    assert f(FAKE, FAKE, 256, 0, None) == INVALID
+    assert not hasattr(hg.lib(), "hipgemm_probe_mfma_ceiling")
