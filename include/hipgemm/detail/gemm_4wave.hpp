@@ -1001,11 +1001,13 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       };
       if constexpr (k16) {
         // Blocks (2i + ii, j): lane l holds row 16 ii + l%16, 8-byte piece
-        // 4j + l/16; piece x of row r at 8-byte slot x ^ 2(r % 16).  A
-        // 16-byte chunk keeps its two halves in order (the XOR is even), so
-        // each lane reads its chunk k of row r with one ds_read_b128 at
-        // chunk k ^ (r % 16).  Writes: each half-wave covers 32 distinct
-        // slots; reads: each row's 16 lanes cover 16 distinct chunks.
+        // 4j + l/16; piece x of row r at 8-byte slot x ^ (r % 16).  Each
+        // write instruction's 16 lanes of one piece index (16 rows) then
+        // cover 16 distinct slots modulo 16, which rocprof reads as no bank
+        // conflict (the slot x ^ 2(r % 16) used before cost 4 conflict
+        // cycles per write, 1024 per tile).  Chunk k of row r (pieces 2k,
+        // 2k + 1) is the 16-byte unit k ^ ((r % 16) / 2), its halves swapped
+        // on odd rows; each row's 16 lanes read 16 distinct units.
         //
         // Software-pipelined over the four 32-row chunks: chunk i is read
         // back, then chunk i + 1 is converted and written into the same
@@ -1017,7 +1019,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
         auto write_blk = [&](int i, int ii, int j) {
           const int bi = 2 * i + ii;
           const f32x4& a = acc16[bi][j];
-          lds_write8(stg + (16 * ii + wr) * 256 + (((4 * j + wg) ^ (2 * wr)) * 8),
+          lds_write8(stg + (16 * ii + wr) * 256 + (((4 * j + wg) ^ wr) * 8),
                      pack16(a, bi, j));
         };
         auto store_one = [&](int i, int p, const i32x4& v) {
@@ -1042,7 +1044,8 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
 #pragma unroll
           for (int p = 0; p < 8; ++p) {
             const int r = 4 * p + rsub;
-            v[p] = lds_read16(stg + r * 256 + ((chunk ^ (r & 15)) * 16));
+            v[p] = lds_read16(stg + r * 256 + ((chunk ^ ((r & 15) >> 1)) * 16));
+            if (r & 1) v[p] = i32x4{v[p][2], v[p][3], v[p][0], v[p][1]};
           }
           compiler_fence();
 #pragma unroll

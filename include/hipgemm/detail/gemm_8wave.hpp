@@ -273,10 +273,11 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
     };
     if constexpr (kVecStore) {
       // Staging: row r (0..31) at 128 r; 8-byte piece x (0..15) at slot
-      // x ^ 2((r / 2) % 8).  Writes (b64, 32 lanes a pass: rows 0-15, pieces
-      // 4j, 4j + 1) cover all 32 eight-byte bank pairs; reads (b128, 16
-      // lanes a pass: two rows of opposite parity, 8 chunks each) likewise.
-      // The XOR is even, so a 16-byte chunk keeps its halves in order.
+      // x ^ (r % 16), so that the 16 lanes of one piece index (16 rows) in
+      // a write instruction cover 16 distinct slots: rocprof reads no bank
+      // conflict (x ^ 2((r / 2) % 8), used before, cost 4 conflict cycles
+      // per write).  Chunk c of row r (pieces 2c, 2c + 1) is the 16-byte
+      // unit ((2c) ^ (r % 16)) / 2, its halves swapped on odd rows.
       lds_u8* stg = lds + Cfg::kStoreBase + wave * Cfg::kStoreStage;
       const int wr = elane & 15, wg = elane >> 4;
       const int rsub = elane >> 3, chunk = elane & 7;  // store: 8 rows x 128 B
@@ -289,7 +290,7 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
           const int r = 16 * ii + wr;
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            lds_write8(stg + r * 128 + (((4 * j + wg) ^ (r & 14)) * 8),
+            lds_write8(stg + r * 128 + (((4 * j + wg) ^ (r & 15)) * 8),
                        cvt(2 * c + ii, j));
           sched_fence();
         }
@@ -298,7 +299,8 @@ __device__ __forceinline__ void gemm_8wave_body(const GemmArgs& g, lds_u8* lds) 
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
           const int r = 8 * p + rsub;
-          v[p] = lds_read16(stg + r * 128 + (((2 * chunk) ^ (r & 14)) * 8));
+          v[p] = lds_read16(stg + r * 128 + ((((2 * chunk) ^ (r & 15)) >> 1) * 16));
+          if (r & 1) v[p] = i32x4{v[p][2], v[p][3], v[p][0], v[p][1]};
         }
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
