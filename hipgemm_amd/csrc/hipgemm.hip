@@ -99,6 +99,12 @@ bool vec_ok(int out, int N, int ldc, const void* C, int group) {
   return N % group == 0 && ldc % group == 0 && aligned(C, (uintptr_t)bytes);
 }
 
+// Rows of a 2-byte C start on 128-byte lines: the 4-wave schedule's
+// overlapped epilogue (Key::line).
+bool line_ok(int out, int ldc, const void* C) {
+  return out_bytes(out) == 2 && ldc % 64 == 0 && aligned(C, 128);
+}
+
 // The tiled schedules (4-wave, 8-wave) on a persistent grid: one workgroup
 // per CU at most (their 160 KiB of LDS allows no more), each walking tiles
 // w, w + grid, ...  `key.vec` is set here: 16-byte epilogue stores need
@@ -119,6 +125,7 @@ hipError_t launch_tiled(int variant, GemmArgs g, hk::Key key,
   const bool t128 = variant == HIPGEMM_VARIANT_TILE128;
   key.vec = vec_ok(key.out, g.N, g.ldc, g.C,
                    key.out == kOutF8 ? (t128 ? 4 : 16) : key.out == kOutF32 ? 4 : 8);
+  key.line = line_ok(key.out, g.ldc, g.C);
   const void* fn = nullptr;
   int threads = Cfg4w::kThreads;
   switch (variant) {
@@ -174,6 +181,7 @@ hipError_t launch_split(GemmArgs g4, GemmArgs g1, hk::Key key,
     prep(g4, Cfg4w::kBM, Cfg4w::kBN);
     prep(g1, CfgT128::kBM, CfgT128::kBN);
     key.vec = true;
+    key.line = line_ok(key.out, g4.ldc, g4.C);
     if (const void* fn = hk::split_plain(key)) {
       void* args[] = {&g4, &g1};
       const int grid = g4.workers > g1.workers ? g4.workers : g1.workers;

@@ -16,14 +16,16 @@ namespace hipgemm {
 namespace kernels {
 
 // One configuration: operand formats (bit 0 A, bit 1 B_T), extended
-// epilogue, its activation and output type, and the store width (16 bytes
-// per lane for the tiled schedules, 8 for the skinny one).
+// epilogue, its activation and output type, the store width (16 bytes per
+// lane for the tiled schedules, 8 for the skinny one), and whether C's rows
+// start on 128-byte lines (the 4-wave schedule's overlapped epilogue).
 struct Key {
   int fmt = 0;
   bool ext = false;
   int act = 0;
   int out = 0;
   bool vec = true;
+  bool line = false;
 };
 
 // Entry points (host handles for hipLaunchKernel), nullptr for a

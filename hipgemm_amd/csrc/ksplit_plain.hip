@@ -13,10 +13,11 @@ using namespace detail;
 static_assert(Cfg4w::kLdsBytes >= CfgT128::kLdsBytes, "one LDS array for both parts");
 static_assert(Cfg4w::kThreads == CfgT128::kThreads, "one workgroup shape");
 
-template <int kFmt>
+template <int kFmt, bool kLine>
 __global__ __launch_bounds__(256, 1) void k_fp8_gemm_split(GemmArgs g4, GemmArgs g1) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg4w::kLdsBytes];
-  gemm_4wave_body<true, 16, false, kFmt>(g4, (lds_u8*)lds);
+  gemm_4wave_body<true, 16, false, kFmt, kActNone, kOutBf16, false, kLine>(
+      g4, (lds_u8*)lds);
   // The 4-wave part has waited for its own DMAs; its waves may still read
   // their epilogue stages.
   __syncthreads();
@@ -27,7 +28,10 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm_split(GemmArgs g4, GemmArgs
 
 const void* split_plain(const Key& k) {
   return sel4(k.fmt, [&](auto F) {
-    return (const void*)&k_fp8_gemm_split<decltype(F)::value>;
+    return sel2(k.line, [&](auto L) {
+      return (const void*)&k_fp8_gemm_split<decltype(F)::value,
+                                            decltype(L)::value == 1>;
+    });
   });
 }
 

@@ -238,8 +238,15 @@ __device__ __forceinline__ TileSrc tile_src(const GemmArgs& g, int t,
 // (epilogue.hpp) -- template parameters, so that each instantiation has one
 // straight-line epilogue.
 // kMx: MX block scales from g.mx (16x16x128, per-tensor epilogue).
+// kLine: C's rows start on 128-byte lines (ldc a multiple of 64 elements, C
+// 128-byte aligned): the plain 16x16x128 epilogue with 16-byte stores then
+// runs inside the MFMA stream of the tile boundary (the overlapped epilogue
+// below), whose stores write 128 bytes of a row each -- whole lines only
+// when rows are line-aligned (with a 10000-byte row stride, 11 % slower than
+// the epilogue after the K loop, whose stores write 256 bytes of a row).
 template <bool kVecStore, int kMf = 32, bool kExt = false, int kFmt = 0,
-          int kAct = kActNone, int kOut = kOutBf16, bool kMx = false>
+          int kAct = kActNone, int kOut = kOutBf16, bool kMx = false,
+          bool kLine = false>
 __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
                                                 lds_u8* lds) {
   using Cfg = Cfg4w;
@@ -524,12 +531,15 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // MFMA of one accumulator are 4 apart; 16x16x128: 4 x 4 blocks).
   // kMx: the scale words of the step the MFMA belong to, w = {A frags 0-3,
   // A frags 4-7, B frags 0-3, B frags 4-7} (one byte per fragment).
+  // zc: the MFMA are the first of their blocks in a tile (accumulator
+  // input zero; the overlapped epilogue, 16x16x128 without MX only).
   auto quarter_mfma = [&](int qi, int qj, int from, int to,
-                          const uint32_t* w = nullptr) {
+                          const uint32_t* w = nullptr, bool zc = false) {
     if constexpr (k16) {
 #pragma unroll
       for (int n = from; n < to; ++n) {
         const int i = 4 * qi + n / 4, j = 4 * qj + n % 4;
+        const f32x4 c0 = zc ? f32x4{} : acc16[i][j];
         if constexpr (k4Mx) {
           const i32x8& x = fb16[j];
           const i32x8& y = fa16[i];
@@ -546,13 +556,13 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
         } else if constexpr (k4) {
           const i32x8& x = fb16[j];
           const i32x8& y = fa16[i];
-          acc16[i][j] = mfma_16x16x128<kFmtFp4, kFmtFp4>(x, y, acc16[i][j]);
+          acc16[i][j] = mfma_16x16x128<kFmtFp4, kFmtFp4>(x, y, c0);
           acc16[i][j] = mfma_16x16x128<kFmtFp4, kFmtFp4>(
               __builtin_shufflevector(x, x, 4, 5, 6, 7, 0, 1, 2, 3),
               __builtin_shufflevector(y, y, 4, 5, 6, 7, 0, 1, 2, 3), acc16[i][j]);
         } else {
           acc16[i][j] = mfma_16x16x128<fmt_b(kFmt), fmt_a(kFmt)>(
-              fb16[j], fa16[i], acc16[i][j]);
+              fb16[j], fa16[i], c0);
         }
       }
       return;
@@ -618,11 +628,18 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // built loops).
   // kMx: w / wt are the scale words of this quarter's step and of the
   // tail's.
+  // ep(n): epilogue work woven into slot n (0..14, after head MFMA n) and
+  // n = 15 (after the last head MFMA) of a 16x16x128 quarter with 8-bit or
+  // fp4 operands; see the overlapped epilogue below.  Every other caller
+  // passes no_ep.
+  auto no_ep = [](int) {};
+  // zh / zt: the head / tail MFMA start their blocks (quarter_mfma's zc).
   auto quarter = [&](auto edge, bool tail, int tqi, int tqj, int qi, int qj,
                      int rop, int rhi, int rst, int kb, int dst, int dop, int dhi,
-                     const uint32_t* w = nullptr, const uint32_t* wt = nullptr) {
+                     const uint32_t* w, const uint32_t* wt, auto&& ep,
+                     bool zh = false, bool zt = false) {
     if constexpr (k16) {
-      if (tail) quarter_mfma(tqi, tqj, QS::kHead, QS::kMfma, wt);
+      if (tail) quarter_mfma(tqi, tqj, QS::kHead, QS::kMfma, wt, zt);
       const DmaSrc d = dma_src(kb, dop, edge);
       sched_fence();
       if constexpr (k6) {
@@ -658,21 +675,29 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
       i32x4 rd[8];
 #pragma unroll
       for (int n = 0; n < 8; ++n) {
-        quarter_mfma(qi, qj, n, n + 1, w);
+        quarter_mfma(qi, qj, n, n + 1, w, zh);
         rd[n] = read16_one(rop, rhi, rst, n);
+        ep(n);
         __builtin_amdgcn_sched_group_barrier(0x008, kMfmaPerBlock, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         sched_fence();
       }
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        quarter_mfma(qi, qj, 8 + n, 9 + n, w);
+        quarter_mfma(qi, qj, 8 + n, 9 + n, w, zh);
         dma_one(d, dst, dop, dhi, n, edge);
+        ep(8 + n);
         __builtin_amdgcn_sched_group_barrier(0x008, kMfmaPerBlock, 0);
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         sched_fence();
       }
-      quarter_mfma(qi, qj, 12, QS::kHead, w);
+#pragma unroll
+      for (int n = 12; n < QS::kHead; ++n) {
+        quarter_mfma(qi, qj, n, n + 1, w, zh);
+        ep(n);
+        sched_fence();
+      }
+      ep(QS::kHead);
 #pragma unroll
       for (int f = 0; f < 4; ++f) {
         if (rop == 0)
@@ -740,16 +765,16 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
         if constexpr (kMx)
           if (s == 0) mx_load(kt0 + 2, mxn);
       }
-      quarter(edge, tail, 1, 1, 0, 0, 1, 1, s, kt + 2, s, 0, 0, w, mxp);
+      quarter(edge, tail, 1, 1, 0, 0, 1, 1, s, kt + 2, s, 0, 0, w, mxp, no_ep);
       wait_lgkmcnt<0>();  // Q01
-      quarter(edge, true, 0, 0, 0, 1, 0, 1, s, kt + 2, s, 1, 0, w, w);
+      quarter(edge, true, 0, 0, 0, 1, 0, 1, s, kt + 2, s, 1, 0, w, w, no_ep);
       wait_lgkmcnt<0>();
       if (kFirst && s == 0 && stores_in_flight && !k4Mx) wait_vmcnt<kWaitAfterStores>();
       else wait_vmcnt<kWaitSteady>();
       barrier();  // Q10
-      quarter(edge, true, 0, 1, 1, 0, 0, 0, s ^ 1, kt + 2, s, 1, 1, w, w);
+      quarter(edge, true, 0, 1, 1, 0, 0, 0, s ^ 1, kt + 2, s, 1, 1, w, w, no_ep);
       wait_lgkmcnt<0>();  // Q11
-      quarter(edge, true, 1, 0, 1, 1, 1, 0, s ^ 1, kt + 2, s, 0, 1, w, w);
+      quarter(edge, true, 1, 0, 1, 1, 1, 0, s ^ 1, kt + 2, s, 0, 1, w, w, no_ep);
       if constexpr (kMx)
 #pragma unroll
         for (int q = 0; q < kMxW; ++q) mxp[q] = w[q];
@@ -760,6 +785,145 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     if constexpr (kMx && !k4Mx)
 #pragma unroll
       for (int q = 0; q < 8; ++q) mxc[q] = mxn[q];
+  };
+
+  // ---- Overlapped epilogue (plain bf16 output, 16-byte stores, 16x16x128,
+  // 8-bit or fp4 operands) ---------------------------------------------------
+  // A wave's 128 x 128 accumulators are four 64 x 64 quadrants d = 2 qi + qj
+  // (rows 64 qi.., columns 64 qj..; blocks acc16[4 qi ..][4 qj ..]).  Quadrant
+  // d is final once quarter-step Qd of a tile's last step (L) has issued its
+  // tail MFMA -- at the start of the next quarter -- and is next written by
+  // quarter Qd of the next tile's first step (0').  Its conversion and its
+  // stores therefore run inside the MFMA stream of the quarters between:
+  //   Q01(L): convert 0              Q10(L): store 0, convert 1
+  //   Q11(L): store 1, convert 2     Q00(0'): store 2, convert 3
+  //   Q01(0'): store 3
+  // "Convert" is 16 blocks (acc * scale -> bf16 RNE -> the wave's 8 KiB LDS
+  // stage), one block per MFMA slot, the block whose tail MFMA opened the
+  // quarter last; the quarter ends by reading the quadrant back (16
+  // ds_read_b64 per lane, into 32 VGPRs).  "Store" is 8 buffer_store_dwordx4
+  // of whole 128-byte lines (8 rows x 128 B each), one per slot of the
+  // quarter's first half, ahead of its DMAs.  The quarters after the stores
+  // wait for them in vmcnt order: the barrier waits of Q00(0') / Q10(0') /
+  // Q00(1') allow 32 / 48 / 32 operations (16 DMAs plus the stores issued in
+  // the four quarters since the group they need), and every store has had
+  // five quarter-steps when Q10(1') waits with the steady 16.  Without a
+  // next tile, the rest of the epilogue runs after the K loop (drain).
+  //
+  // Stage layout: row r (0..63) of the quadrant at 128 r; its 8-byte piece x
+  // (columns 4 x .. 4 x + 3) at slot x ^ (r % 16).  A block write (16 rows of
+  // one piece per 16 lanes) covers 16 distinct slots; a read-back instruction
+  // (8 rows x 8 lanes of 8 bytes) covers each row whole.
+  constexpr bool kOverlap = kLine && k16 && kVecStore && !kExt && !kMx && !k6;
+  struct EpiTile {
+    __amdgpu_buffer_rsrc_t rsrc;  // the tile's window of C
+    int rows_left, cols_left;     // rows / columns of C from the wave's origin
+  };
+  auto epi_tile = [&](int tile) {
+    const TileCoord tc = grouped_tile_u(tile, tiles_m, tiles_n, g.group_m);
+    const int rows_c = min(Cfg::kBM, M - tc.m * Cfg::kBM);
+    return EpiTile{
+        make_rsrc(reinterpret_cast<uint8_t*>(g.C) +
+                      ((size_t)tc.m * Cfg::kBM * g.ldc + (size_t)tc.n * Cfg::kBN) * 2,
+                  (uint32_t)(((rows_c - 1) * g.ldc + Cfg::kBN) * 2)),
+        M - tc.m * Cfg::kBM - wm * 128, N - tc.n * Cfg::kBN - wn * 128};
+  };
+  lds_u8* const epi_stg = lds + Cfg::kStoreBase + wave * Cfg::kStoreStage;
+  // kOobOffset when x >= limit, as plain arithmetic (no lane masks).
+  auto oob_unless = [](int x, int limit) -> uint32_t {
+    return (uint32_t)((limit - 1 - x) >> 31) & kOobOffset;
+  };
+  u32x2 epi_rd[16];  // read-back quadrant: store p, 8-byte half h at [2p + h]
+  // The epilogue work of one quarter: store quadrant sq (from epi_rd) and
+  // convert quadrant vq (-1: none), for tile window et.  Lane-derived
+  // addresses hang off an opaque copy of the lane id (computed per quarter,
+  // not hoisted into the K loop).
+  auto epi_work = [&](int sq, int vq, const EpiTile& et) {
+    int el = lane;
+    asm volatile("" : "+v"(el));
+    const int wl = el & 15, wg = el >> 4;
+    // write: block (bi, bj) at bi * 2048 + (wbase ^ 32 bj)
+    const uint32_t wbase =
+        (uint32_t)(wl * 128 + (((wg ^ wl) & 3) << 3) + ((wl >> 2) << 5));
+    const int rl = el >> 3, c = el & 7;
+    // read-back p: pieces 2c and 2c + 1 of row 8p + rl
+    const uint32_t rbase = (uint32_t)(rl * 128 + (((2 * c) ^ rl) << 3));
+    const uint32_t vst = (uint32_t)((rl * g.ldc + wn * 128 + 8 * c) * 2);
+    // acc16, epi_rd and et by reference: the conversion clears the
+    // accumulators and the read-back fills epi_rd for the next quarter.
+    return [&, sq, vq, wbase, rbase, vst, rl, c](int slot) {
+      if (sq >= 0 && slot < 8) {
+        const int qi = sq >> 1, qj = sq & 1, p = slot;
+        int row8 = 64 * qi + 8 * p;
+        asm volatile("" : "+s"(row8));  // recompute per store, never hoist
+        const int srow = __builtin_amdgcn_readfirstlane((wm * 128 + row8) * g.ldc * 2);
+        const u32x2 lo = epi_rd[2 * p], hi = epi_rd[2 * p + 1];
+        store_b128<kStoreC>(
+            i32x4{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y}, et.rsrc,
+            (vst | oob_unless(64 * qj + 8 * c, et.cols_left) |
+             oob_unless(row8 + rl, et.rows_left)) + 128 * qj,
+            srow);
+      }
+      if (vq >= 0) {
+        const int qi = vq >> 1, qj = vq & 1;
+        auto convert = [&](int b) {
+          const int bi = b >> 2, bj = b & 3;
+          const f32x4& a = acc16[4 * qi + bi][4 * qj + bj];
+          lds_write8(epi_stg + bi * 2048 + (wbase ^ (uint32_t)(32 * bj)),
+                     u32x2{pack_bf16x2(acc_read(a[0]) * scale, acc_read(a[1]) * scale),
+                           pack_bf16x2(acc_read(a[2]) * scale, acc_read(a[3]) * scale)});
+        };
+        if (slot < QS::kHead) convert(slot);
+        if (slot == QS::kHead - 1) convert(QS::kHead);
+        if (slot == QS::kHead) {
+#pragma unroll
+          for (int p = 0; p < 8; ++p) {
+            const uint32_t o = (uint32_t)(p * 1024) + (rbase ^ (uint32_t)((p & 1) << 6));
+            epi_rd[2 * p] = lds_read8(epi_stg + o);
+            epi_rd[2 * p + 1] = lds_read8(epi_stg + (o ^ 8u));
+          }
+        }
+      }
+    };
+  };
+
+  // One pipeline step pair of the overlapped schedule (kOverlap).  kMode:
+  // 0 an ordinary pair; 1 the workgroup's first pair (no tail MFMA before
+  // its first quarter); 2 a tile's last pair (quadrants 0-2 of this tile's
+  // epilogue in its second step); 3 a tile's first pair after another tile
+  // (that tile's tail MFMA, quadrant 3 and the last stores in its first
+  // step).  The barrier waits count the stores (see above).
+  auto step_pair_ov = [&](int kt0, auto mode, auto edge, const EpiTile& et) {
+    constexpr int kMode = decltype(mode)::value;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int kt = kt0 + s;
+      const bool tail = !(kMode == 1 && s == 0);
+      const bool e2 = kMode == 2 && s == 1, e3 = kMode == 3 && s == 0;
+      // The tile's first step: its MFMA start from zero; so does the tail
+      // of its last quarter, issued in the next step's first quarter.
+      const bool z = (kMode == 1 || kMode == 3) && s == 0;
+      const bool z00 = (kMode == 1 || kMode == 3) && s == 1;
+      wait_lgkmcnt<0>();
+      if (kMode == 3) wait_vmcnt<kWaitSteady + 16>();
+      else wait_vmcnt<kWaitSteady>();
+      barrier();  // Q00
+      if (e3) quarter(edge, tail, 1, 1, 0, 0, 1, 1, s, kt + 2, s, 0, 0, nullptr, nullptr, epi_work(2, 3, et), z, z00);
+      else quarter(edge, tail, 1, 1, 0, 0, 1, 1, s, kt + 2, s, 0, 0, nullptr, nullptr, no_ep, z, z00);
+      wait_lgkmcnt<0>();  // Q01
+      if (e2) quarter(edge, true, 0, 0, 0, 1, 0, 1, s, kt + 2, s, 1, 0, nullptr, nullptr, epi_work(-1, 0, et), z, z);
+      else if (e3) quarter(edge, true, 0, 0, 0, 1, 0, 1, s, kt + 2, s, 1, 0, nullptr, nullptr, epi_work(3, -1, et), z, z);
+      else quarter(edge, true, 0, 0, 0, 1, 0, 1, s, kt + 2, s, 1, 0, nullptr, nullptr, no_ep, z, z);
+      wait_lgkmcnt<0>();
+      if (e3) wait_vmcnt<kWaitSteady + 32>();
+      else wait_vmcnt<kWaitSteady>();
+      barrier();  // Q10
+      if (e2) quarter(edge, true, 0, 1, 1, 0, 0, 0, s ^ 1, kt + 2, s, 1, 1, nullptr, nullptr, epi_work(0, 1, et), z, z);
+      else quarter(edge, true, 0, 1, 1, 0, 0, 0, s ^ 1, kt + 2, s, 1, 1, nullptr, nullptr, no_ep, z, z);
+      wait_lgkmcnt<0>();  // Q11
+      if (e2) quarter(edge, true, 1, 0, 1, 1, 1, 0, s ^ 1, kt + 2, s, 0, 1, nullptr, nullptr, epi_work(1, 2, et), z, z);
+      else quarter(edge, true, 1, 0, 1, 1, 1, 0, s ^ 1, kt + 2, s, 0, 1, nullptr, nullptr, no_ep, z, z);
+    }
   };
 
   // Prologue of the first tile: steps 0 and 1 (groups A lo, B lo, B hi,
@@ -787,6 +951,43 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   read_tile(0, 0, 0);
   read_tile(1, 0, 0);
 
+  if constexpr (kOverlap) {
+    const EpiTile none{};
+    step_pair_ov(0, std::integral_constant<int, 1>{}, std::true_type{}, none);
+    for (;;) {
+      int kt0 = 2;
+      for (; kt0 < kt_edge; kt0 += 2)
+        step_pair_ov(kt0, std::integral_constant<int, 0>{}, std::false_type{}, none);
+      for (; kt0 < kt_pad - 2; kt0 += 2)
+        step_pair_ov(kt0, std::integral_constant<int, 0>{}, std::true_type{}, none);
+      const EpiTile et = epi_tile(t);
+      step_pair_ov(kt_pad - 2, std::integral_constant<int, 2>{}, std::true_type{}, et);
+      t += walk.stride;
+      if (t >= walk.end) {
+        // Drain: the last quarter's tail MFMA, then quadrant 3 without a
+        // next tile to hide it in.
+        quarter_mfma(1, 1, QS::kHead, QS::kMfma);
+        asm volatile("" : "+a"(acc16[7][7]));
+        mfma_drain();
+        wait_lgkmcnt<0>();
+        auto ep = epi_work(2, 3, et);
+#pragma unroll
+        for (int n = 0; n <= QS::kHead; ++n) ep(n);
+        wait_lgkmcnt<0>();
+        auto ep3 = epi_work(3, -1, et);
+#pragma unroll
+        for (int n = 0; n < 8; ++n) ep3(n);
+        break;
+      }
+      cur = nxt;
+      nxt = tile_src(g, t + walk.stride, walk.end, tiles_m, tiles_n);
+      step_pair_ov(0, std::integral_constant<int, 3>{}, std::true_type{}, et);
+    }
+    // The last tile's look-ahead DMA (all zeros) still lands in LDS, and
+    // the last stores are in flight.
+    wait_vmcnt<0>();
+    return;
+  } else {
   // Lane-derived epilogue values hang off an opaque copy of the lane id so
   // the optimiser cannot hoist them out of the tile loop, where they would
   // stay live through the K loop and spill.
@@ -834,9 +1035,6 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     // so each lane holds 4 consecutive bf16 (8 bytes) per (i, j, r/4).
     // Out-of-range bit for "x < limit" as plain arithmetic (no lane masks,
     // which would pin scalar register pairs): kOobOffset when x >= limit.
-    auto oob_unless = [](int x, int limit) -> uint32_t {
-      return (uint32_t)((limit - 1 - x) >> 31) & kOobOffset;
-    };
     int elane = lane;
     asm volatile("" : "+v"(elane));
     const TileCoord tc = grouped_tile_u(t, tiles_m, tiles_n, g.group_m);
@@ -1183,6 +1381,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // The last tile's look-ahead DMA (all zeros) still lands in LDS: let it
   // finish before the workgroup's LDS can be handed to another workgroup.
   wait_vmcnt<0>();
+  }
 }
 
 }  // namespace detail

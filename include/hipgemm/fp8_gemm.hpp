@@ -65,8 +65,11 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4wave_256x256x128(
                       MxArgs{},
                       SplitArgs{}};
   // 16-byte epilogue stores: N a multiple of 8 (C itself must be 16-byte
-  // aligned, as every hipMalloc'd buffer is).
-  gemm_4wave_body<N % 8 == 0, 16>(args, (lds_u8*)lds);
+  // aligned, as every hipMalloc'd buffer is); the overlapped epilogue where
+  // rows of C are whole 128-byte lines (N a multiple of 64 and C line-
+  // aligned, as hipMalloc'd buffers are; an unaligned C stays correct).
+  gemm_4wave_body<N % 8 == 0, 16, false, 0, kActNone, kOutBf16, false,
+                  N % 64 == 0>(args, (lds_u8*)lds);
 }
 
 // The reference header's second kernel,
@@ -105,5 +108,6 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_4wave_256x256x128_ref(
                       EpiArgs{},
                       MxArgs{},
                       SplitArgs{}};
-  gemm_4wave_body<N % 8 == 0, 16>(args, (lds_u8*)lds);
+  gemm_4wave_body<N % 8 == 0, 16, false, 0, kActNone, kOutBf16, false,
+                  N % 64 == 0>(args, (lds_u8*)lds);
 }
