@@ -373,6 +373,8 @@ def _gemm_operands(a, b_t, out, variant, stream, out_dtype=None):
     ldc = out.stride(0) if M > 1 else max(N, 1)
     nbytes = workspace_size(M, N, K, variant) if M > 0 and N > 0 else 0
     ws = _workspace(a.device, stream, nbytes) if nbytes else None
+    if ws is None:
+        nbytes = 0
     return (a, b_t, out, M, N, K, lda, ldb, ldc,
             ws.data_ptr() if ws is not None else 0, nbytes, stream)
 
@@ -389,6 +391,15 @@ def fp8_gemm_bf16(a, b_t, scale_a=None, scale_b=None, out=None,
     """
     a, b_t, out, M, N, K, lda, ldb, ldc, ws, nbytes, stream = _gemm_operands(
         a, b_t, out, variant, stream)
+    if not ws:
+        # No workspace (none needed, or the stream is being captured): the
+        # entry point that takes none.
+        code = gemm_raw(a.data_ptr(), b_t.data_ptr(), out.data_ptr(), M, N, K,
+                        lda, ldb, ldc, _scale_ptr(scale_a, "scale_a"),
+                        _scale_ptr(scale_b, "scale_b"), variant,
+                        stream.cuda_stream)
+        _check(code, "hipgemm_fp8_gemm_bf16")
+        return out
     code = gemm_raw_ws(a.data_ptr(), b_t.data_ptr(), out.data_ptr(), M, N, K,
                        lda, ldb, ldc, _scale_ptr(scale_a, "scale_a"),
                        _scale_ptr(scale_b, "scale_b"), variant, ws, nbytes,
@@ -466,7 +477,7 @@ def gemm(a, b_t, *, a_format: int = FMT_E4M3, b_format: int = FMT_E4M3,
     if need != nbytes:  # the formats and MX scales decide the schedule
         w = _workspace(a.device, stream, need) if need else None
         d.workspace = w.data_ptr() if w is not None else None
-        d.workspace_bytes = need
+        d.workspace_bytes = need if w is not None else 0
     _check(gemm_desc_raw(d, stream.cuda_stream), "hipgemm_gemm")
     return out
 
@@ -497,22 +508,27 @@ def fp8_gemm_bf16_rowcol(a, b_t, scale_rows=None, scale_cols=None, out=None,
 # never freed once created: a CUDA graph captured with it keeps its address,
 # so a smaller one stays alive (in _retired) when a larger one replaces it.
 # Growth at least doubles the size, which bounds the retired bytes by the
-# live ones.  Creating or growing one while the stream is being captured is
-# refused: the allocation and its zero fill would only be recorded, not run.
+# live ones.  None is created or grown while the stream is being captured
+# (the allocation and its zero fill would only be recorded, not run): the
+# call then goes to the C ABI without one, which runs a schedule that would
+# split K unsplit (include/hipgemm.h).
 _workspaces: dict = {}
 _retired: list = []
 
 
 def _workspace(device, stream, nbytes: int):
+    """The stream's workspace of at least nbytes, or None while `stream` is
+    being captured and has none that large."""
     torch = _torch()
     key = (device.index, stream.cuda_stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        if torch.cuda.is_current_stream_capturing():
-            raise HipGemmError(
-                f"a {nbytes}-byte workspace is needed on this stream while it "
-                "is being captured; run the same call once before capture so "
-                "that the workspace exists", hipErrorInvalidValue)
+        # The capture status of `stream` itself (it need not be the current
+        # stream).
+        with torch.cuda.stream(stream):
+            capturing = torch.cuda.is_current_stream_capturing()
+        if capturing:
+            return None
         size = nbytes if ws is None else max(nbytes, 2 * ws.numel())
         with torch.cuda.stream(stream):
             new = torch.zeros(size, dtype=torch.uint8, device=device)

@@ -8,25 +8,8 @@
 
 #include <atomic>
 #include <cstdint>
-#include <mutex>
 
 #include "kernels.hpp"
-
-// Scratch memory of hipgemm_gemm_noalloc: a static device array, one copy
-// per GPU the library runs on, held until the process ends (no allocation
-// call ever creates or frees it).  Laid out as any workspace: arrival
-// counters first (zero between calls), then partial tiles.  Host code never
-// uses this name as an address: its per-device address comes from
-// hipGetSymbolAddress (scratch_on_device below).
-static __device__ __align__(256) uint8_t scratch[HIPGEMM_NOALLOC_SCRATCH_BYTES];
-
-// Clears n 4-byte words (the scratch counters at first use on a device): a
-// kernel, not a memset, so that it may also be recorded into a graph.
-__global__ void clear_words(uint32_t* p, int n) {
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += gridDim.x * blockDim.x)
-    p[i] = 0u;
-}
 
 namespace {
 
@@ -227,7 +210,9 @@ struct SkinnyPlan {
 // of A for its K-slice, so a narrower tile costs A traffic, and where the
 // 128-column tile already has two workgroups per CU, or neither has,
 // 64 columns measured 3-11 % slower).
-SkinnyPlan plan_skinny(int M, int N, int K) {
+// unsplit: one K-slice (no workspace), for a call under stream capture
+// that brings no workspace.
+SkinnyPlan plan_skinny(int M, int N, int K, bool unsplit = false) {
   const int kmb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
   const int steps = (K + CfgSkinny::kBK - 1) / CfgSkinny::kBK;
   const int cus = cu_count();
@@ -242,6 +227,7 @@ SkinnyPlan plan_skinny(int M, int N, int K) {
     *two = slices2 > slices && steps >= 12 * slices2;
     if (*two) slices = slices2;
     if (slices > steps) slices = steps;
+    if (unsplit) slices = 1;
     // One counter per column tile: more tiles than the counter region holds
     // (never with slices > 1 on a GPU of at most 4096 CUs) run unsplit.
     if (slices < 1 || p.tiles_n > kWsMaxCounters) slices = 1;
@@ -311,7 +297,7 @@ struct StripPlan {
   size_t ws_bytes;
 };
 
-StripPlan plan_strip(int M, int N, int K, int knb) {
+StripPlan plan_strip(int M, int N, int K, int knb, bool unsplit = false) {
   StripPlan p{};
   p.kmb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
   p.knb = knb;
@@ -321,7 +307,7 @@ StripPlan plan_strip(int M, int N, int K, int knb) {
   const int cus = cu_count();
   int slices = (cus + p.tiles_n - 1) / p.tiles_n;
   if (slices > steps / 4) slices = steps / 4;
-  if (slices < 1 || p.tiles_n > kWsMaxCounters) slices = 1;
+  if (slices < 1 || p.tiles_n > kWsMaxCounters || unsplit) slices = 1;
   p.slice_steps = steps > 0 ? (steps + slices - 1) / slices : 0;
   p.slices = p.slice_steps > 0 ? (steps + p.slice_steps - 1) / p.slice_steps : 1;
   if (p.slices > 1)
@@ -365,8 +351,9 @@ int fp4_variant(int variant, int M, int N, int Kb);
 // K-split plan of the 128 x 128 schedule: when its tiles fill at most a
 // quarter of the CUs and K has at least 16 steps of 128, K-slices of at
 // least 8 (even) steps so that tiles x slices approaches the CU count; when
-// they fill at most half of them and K has at least 64 steps, 2 slices of at
-// least 32 steps.  The workspace holds one 64 KiB fp32 partial tile per
+// they fill at most half of them and K has at least 64 steps, cus / tiles
+// slices (2, or 3 for 65-85 tiles on 256 CUs) of at least 8 steps each.  The
+// workspace holds one 64 KiB fp32 partial tile per
 // (tile, slice).  Measured against no split in one process:
 // 256 x 4096 x 14336 (64 tiles, 4 slices) 1.39x; 128 tiles, 2 slices, with
 // the reduce kernel's batched loads: 256 x 8192 x 8192 1.18x,
@@ -447,42 +434,6 @@ int split_columns(int M, int N, int cus) {
 }
 
 bool valid_code(int v, int count) { return v >= 0 && v < count; }
-
-// Device address of `scratch` on the current device, looked up once per
-// device (with that device current) on its first use; at that first use the
-// counter region is also cleared on `stream`, ahead of the call that needs
-// it (the array is zero-initialised when the code object is loaded; the
-// clear makes that explicit).  Returns nullptr with *err set on failure.
-void* scratch_on_device(hipStream_t stream, hipError_t* err) {
-  constexpr int kMaxDevices = 64;
-  static std::atomic<void*> ptrs[kMaxDevices];
-  static std::mutex init;
-  int dev = 0;
-  *err = hipGetDevice(&dev);
-  if (*err != hipSuccess) return nullptr;
-  if (dev < 0 || dev >= kMaxDevices) {
-    *err = hipErrorInvalidDevice;
-    return nullptr;
-  }
-  void* p = ptrs[dev].load(std::memory_order_acquire);
-  if (p) return p;
-  std::lock_guard<std::mutex> lock(init);
-  p = ptrs[dev].load(std::memory_order_relaxed);
-  if (p) return p;
-  *err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-  if (*err != hipSuccess || !p) {
-    if (*err == hipSuccess) *err = hipErrorInvalidSymbol;
-    return nullptr;
-  }
-  const int words = (int)(HIPGEMM_WS_COUNTER_BYTES / sizeof(uint32_t));
-  uint32_t* w = static_cast<uint32_t*>(p);
-  void* args[] = {&w, (void*)&words};
-  *err = hipLaunchKernel((const void*)clear_words, dim3(16), dim3(256), args,
-                         0, stream);
-  if (*err != hipSuccess) return nullptr;
-  ptrs[dev].store(p, std::memory_order_release);
-  return p;
-}
 
 // Shared body of the GEMM entry points.  `ws` may be null when `ws_given` is
 // false: a schedule that needs a workspace then takes a stream-ordered
@@ -601,6 +552,19 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   key.act = d.activation;
   key.out = d.out_dtype;
   if (dry_run) return hipSuccess;
+  // Whether a call that brings no workspace runs under stream capture: a
+  // schedule that would split K then runs unsplit, as the stream-ordered
+  // allocation of its partials would only be recorded into the caller's
+  // graph (the 128 x 128 schedule's K-slices from half-filled grids, the
+  // split-K and strip schedules' slices).
+  auto capturing = [&](bool* yes) -> hipError_t {
+    *yes = false;
+    if (ws_given) return hipSuccess;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    const hipError_t r = hipStreamIsCapturing(stream, &cap);
+    *yes = cap != hipStreamCaptureStatusNone;
+    return r;
+  };
   // A schedule that needs `need` bytes of workspace (the first `zero` of
   // them zero-filled): the caller's, or a stream-ordered allocation for the
   // call.
@@ -627,19 +591,32 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
   };
   switch (variant) {
     case HIPGEMM_VARIANT_SKINNY: {
-      const SkinnyPlan p = plan_skinny(M, N, K);
+      SkinnyPlan p = plan_skinny(M, N, K);
+      if (p.ws_bytes > 0) {
+        bool cap = false;
+        if (const hipError_t r = capturing(&cap); r != hipSuccess) return r;
+        if (cap) p = plan_skinny(M, N, K, true);
+      }
       return with_workspace(p.ws_bytes, p.counter_bytes, [&](void* w) {
         return launch_skinny(g, p, w, key, stream);
       });
     }
     case HIPGEMM_VARIANT_STRIP: {
-      const StripPlan p = plan_strip(M, N, K, strip_knb(M, N, K));
+      StripPlan p = plan_strip(M, N, K, strip_knb(M, N, K));
+      if (p.ws_bytes > 0) {
+        bool cap = false;
+        if (const hipError_t r = capturing(&cap); r != hipSuccess) return r;
+        if (cap) p = plan_strip(M, N, K, strip_knb(M, N, K), true);
+      }
       return with_workspace(p.ws_bytes, p.slices > 1 ? kWsCounterBytes : 0,
                             [&](void* w) { return launch_strip(g, p, w, key, stream); });
     }
     case HIPGEMM_VARIANT_TILE128: {
       const T128Plan p = plan_t128(M, N, K, cu_count(), fp6 ? 96 : CfgT128::kBK);
-      if (p.slices == 1) return launch_tiled(variant, g, key, stream);
+      bool cap = false;
+      if (p.slices > 1)
+        if (const hipError_t r = capturing(&cap); r != hipSuccess) return r;
+      if (p.slices == 1 || cap) return launch_tiled(variant, g, key, stream);
       return with_workspace(p.ws_bytes, 0, [&](void* w) {
         return launch_t128_split(g, p, w, key, stream);
       });
@@ -852,7 +829,7 @@ hipError_t hipgemm_gemm_noalloc(const hipgemm_gemm_desc* desc,
     // Argument errors come back before the scratch is touched.
     hipError_t e = run_gemm(d, false, stream, true);
     if (e != hipSuccess) return e;
-    d.workspace = scratch_on_device(stream, &e);
+    d.workspace = hk::noalloc_scratch(stream, &e);
     if (!d.workspace) return e;
     d.workspace_bytes = HIPGEMM_NOALLOC_SCRATCH_BYTES;
   }

@@ -54,6 +54,12 @@ inline const void* tile128_ext(const Key& k) {
 const void* tile128_split(const Key& k);            // kt128_plain.hip
 const void* tile128_reduce(const Key& k);           // kt128_plain.hip
 const void* split_plain(const Key& k);              // ksplit_plain.hip
+// hipgemm_gemm_noalloc's static scratch array on the current device
+// (noalloc_scratch.hip): its address, looked up once per device (with that
+// device current); at that first lookup its counter region is cleared on
+// `stream` unless the stream is being captured.  nullptr with *err set on
+// failure.
+void* noalloc_scratch(hipStream_t stream, hipError_t* err);
 // Packs [rows][ceil(K/32)] E8M0 scales (row stride ld) into MxArgs' layout.
 hipError_t mx_pack(const uint8_t* src, int rows, int K, int ld, uint8_t* dst,
                    hipStream_t stream);

@@ -84,8 +84,12 @@ enum {
    * fit in one round over the CUs, or for K <= 2048 on at most 128 tiles of
    * 256 x 256, and for 64 < M <= 128 (except as under SKINNY).  Splits K
    * into slices, summed by a second kernel, when its tiles fill at most a
-   * quarter of the CUs (a workspace then: hipgemm_workspace_size).  No
-   * reference counterpart (the reference has 256 x 256 tiles only). */
+   * quarter of the CUs and K has at least 16 steps of 128 bytes, or at most
+   * half of them and K has at least 64 steps (CUs / tiles slices: 2, or 3
+   * for 65-85 tiles on 256 CUs); a workspace then (hipgemm_workspace_size).
+   * A call with no workspace under stream capture runs unsplit (as do the
+   * split-K and strip schedules' calls there).  No reference counterpart
+   * (the reference has 256 x 256 tiles only). */
   HIPGEMM_VARIANT_TILE128 = 5,
   /* M <= 128 only: 256 threads, each workgroup a strip of 32 columns of C
    * (64 above 32 rows) over all of K (over a K-slice, with a workspace,
@@ -278,8 +282,12 @@ hipError_t hipgemm_gemm(const hipgemm_gemm_desc *desc, hipStream_t stream);
  * hipgemm_gemm that allocates nothing: schedules that need scratch memory
  * (the skinny schedule's split-K counters and partial tiles, the 128 x 128
  * schedule's K-slices) use a static device array of the library,
- * HIPGEMM_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on that
- * GPU until the process ends; no call makes an allocation or a memset.
+ * HIPGEMM_NOALLOC_SCRATCH_BYTES per GPU: it belongs to the code object of
+ * its own translation unit, which the HIP runtime loads on a GPU at the first
+ * hipgemm_gemm_noalloc call there that needs scratch, and holds until the
+ * process ends (with the runtime's deferred code-object loading; without
+ * it, on every GPU where the library's code is loaded).  No call makes an
+ * allocation or a memset.
  * desc->workspace must be NULL and desc->workspace_bytes 0.  Returns
  * hipErrorInvalidValue when the descriptor is invalid (as hipgemm_gemm) or
  * when the call would need more scratch than HIPGEMM_NOALLOC_SCRATCH_BYTES

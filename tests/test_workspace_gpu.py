@@ -6,10 +6,12 @@ HIPGEMM_WS_COUNTER_BYTES) and of graph capture around it.
   call that follows on the same workspace still finds its arrival counters
   at zero (a prefill-then-decode sequence on one stream).
 * The Python helpers never free a workspace a captured graph may hold, and
-  refuse to create one while the stream is being captured.
-* The raw C ABI refuses (hipErrorInvalidValue) to allocate a workspace for
-  a call on a capturing stream, instead of recording an allocation and a
-  memset into the caller's graph.
+  create none while the stream is being captured.
+* A call with no workspace on a capturing stream (the raw C ABI, or the
+  Python helpers on a stream that has none) runs its schedule unsplit
+  instead of recording an allocation and a memset into the caller's graph:
+  the 128 x 128 schedule's K-slices at 256 x 8192 x 8192 and the strip
+  schedule's at 16 x 4096 x 4096; every replay equals the oracle.
 """
 import numpy as np
 import pytest
@@ -93,14 +95,20 @@ def test_graph_replay_survives_workspace_growth(gpu, oracle):
         torch.cuda.synchronize()
 
 
-def test_capture_refuses_new_workspace(gpu):
+@pytest.mark.parametrize("M,N,K", [(256, 8192, 8192), (16, 4096, 4096)])
+def test_capture_without_workspace_runs_unsplit(gpu, oracle, M, N, K):
     torch = gpu
     s = torch.cuda.Stream()
-    M, N, K = 16, 4096, 4096
-    say(f"case ws-capture-refused {M}x{N}x{K}")
-    a = torch.zeros((M, K), dtype=torch.uint8, device="cuda")
-    b = torch.zeros((N, K), dtype=torch.uint8, device="cuda")
-    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    need = hg.workspace_size(M, N, K, 0)
+    say(f"case ws-capture-unsplit {M}x{N}x{K} (variant "
+        f"{hg.variant_name(hg.select_variant(M, N, K))}, split workspace "
+        f"{need} bytes)")
+    assert need > 0  # AUTO splits K here when a workspace is available
+    A, B = ternary((M, K), 70), ternary((N, K), 71)
+    want = oracle.gemm(A, B, 1.0, 1.0)
+    a, b = to_dev(torch, A), to_dev(torch, B)
+    outs = [torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+            for _ in range(2)]
     # Stream handles come from a pool and may repeat: make sure this one has
     # no workspace yet (keeping any old one alive, as the helpers do).
     old = hg._workspaces.pop((0, s.cuda_stream), None)
@@ -108,19 +116,21 @@ def test_capture_refuses_new_workspace(gpu):
         hg._retired.append(old)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    raised = None
     with torch.cuda.graph(graph, stream=s):  # a fresh stream: no workspace
-        out.zero_()
-        try:
-            hg.fp8_gemm_bf16(a, b, out=out)
-        except hg.HipGemmError as e:
-            raised = e
-        # The raw ABI without a workspace: refused, nothing recorded.
-        code = hg.gemm_raw(a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N,
-                           K, K, K, N, 0, 0, 0, s.cuda_stream)
+        hg.fp8_gemm_bf16(a, b, out=outs[0])
+        code = hg.gemm_raw(a.data_ptr(), b.data_ptr(), outs[1].data_ptr(), M,
+                           N, K, K, K, N, 0, 0, 0, s.cuda_stream)
     torch.cuda.synchronize()
-    assert raised is not None and raised.code == hg.hipErrorInvalidValue
-    assert code == hg.hipErrorInvalidValue
-    graph.replay()
-    torch.cuda.synchronize()
-    assert not out.view(torch.int16).any()
+    assert code == 0
+    assert (0, s.cuda_stream) not in hg._workspaces  # none created
+    for r in range(3):
+        for o in outs:
+            o.fill_(float("nan"))  # eager work between the replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, o in enumerate(outs):
+            got = from_dev_bf16(o)
+            say(f"    replay {r} output {i}: "
+                f"{int((got != want).sum())} of {M * N} differ")
+            assert np.array_equal(got, want)
