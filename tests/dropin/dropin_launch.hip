@@ -26,7 +26,11 @@ hipError_t launch(int kernel, const void* A, const void* B, void* C, int grid,
 struct Shape {
   int M, N, K;
 };
-constexpr Shape kShapes[] = {{512, 512, 512}, {4096, 4096, 4096}, {4000, 5000, 3584}};
+// The reference bench's default shape (bench.cpp:4-14) and its long-K
+// LLM shape come last.
+constexpr Shape kShapes[] = {{512, 512, 512},   {4096, 4096, 4096},
+                             {4000, 5000, 3584}, {8192, 8192, 8192},
+                             {8192, 8192, 28672}};
 
 }  // namespace
 
@@ -50,6 +54,8 @@ int dropin_launch(int kernel, int shape, const void* A, const void* B, void* C,
     case 0: return (int)launch<512, 512, 512>(kernel, A, B, C, grid, s);
     case 1: return (int)launch<4096, 4096, 4096>(kernel, A, B, C, grid, s);
     case 2: return (int)launch<4000, 5000, 3584>(kernel, A, B, C, grid, s);
+    case 3: return (int)launch<8192, 8192, 8192>(kernel, A, B, C, grid, s);
+    case 4: return (int)launch<8192, 8192, 28672>(kernel, A, B, C, grid, s);
     default: return (int)hipErrorInvalidValue;
   }
 }

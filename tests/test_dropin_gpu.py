@@ -7,7 +7,11 @@ exactly as the reference's callers launch them (test.cpp:79: a grid of
 (M * N) / 65536 workgroups of 256 threads, no dynamic LDS) through
 tests/dropin/libdropin.so, and compared with the oracle: bit-exactly on
 ternary inputs (every partial sum a small integer), within the 1e-2 metric
-on general ones, with canaries around C (no write outside M x N).
+on general ones, with canaries around C (no write outside M x N).  At the
+reference bench's shapes (8192^3, bench.cpp:4-14, and 8192 x 8192 x 28672)
+the whole of C is compared for ternary inputs at 8192^3; for general inputs
+and the long-K shape, about 200 rows (every tile row's edges and random
+ones) plus the row- and column-sum identities of the whole output.
 """
 import ctypes
 import os
@@ -16,6 +20,7 @@ import numpy as np
 import pytest
 
 from oracle import pyoracle as po
+from test_gemm_gpu import check_rows, check_sums, sample_rows
 from util import REL_TOL, compare, say, to_dev
 
 pytestmark = pytest.mark.gpu
@@ -106,3 +111,29 @@ def test_dropin_any_grid(gpu, oracle, dropin, kernel, grid):
     C = launch(gpu, dropin, kernel, 0, A, B, grid=grid)
     _, exact, _ = compare(C, oracle.gemm(A, B, 1.0, 1.0))
     assert exact == 1.0
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_dropin_bench_shape_ternary(gpu, oracle, dropin, kernel):
+    """8192^3, the reference bench's default: the whole output, bit-exact."""
+    M, N, K = shape_of(dropin, 3)
+    say(f"case dropin kernel={kernel} {M}x{N}x{K} ternary seed=35")
+    rng = np.random.default_rng(35)
+    A = TERNARY[rng.integers(0, 3, (M, K))]
+    B = TERNARY[rng.integers(0, 3, (N, K))]
+    C = launch(gpu, dropin, kernel, 3, A, B)
+    max_rel, exact, _ = compare(C, oracle.gemm(A, B, 1.0, 1.0))
+    say(f"    max_rel={max_rel:.3e} exact={exact:.6f}")
+    assert exact == 1.0
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
+@pytest.mark.parametrize("shape", [3, 4], ids=["8192", "8192x8192x28672"])
+def test_dropin_bench_shapes_general(gpu, oracle, dropin, kernel, shape):
+    M, N, K = shape_of(dropin, shape)
+    say(f"case dropin kernel={kernel} {M}x{N}x{K} normal(0,1) seeds 36/37")
+    A = oracle.fill((M, K), 36, po.NORMAL, 0.0, 1.0)
+    B = oracle.fill((N, K), 37, po.NORMAL, 0.0, 1.0)
+    C = launch(gpu, dropin, kernel, shape, A, B)
+    check_rows(oracle, C, A, B, 1.0, 1.0, sample_rows(M, 38, 128))
+    check_sums(oracle, C, A, B, 1.0)
