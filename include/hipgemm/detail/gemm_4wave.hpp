@@ -377,6 +377,15 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   const uint32_t row6_a = Cfg::kABase + (wm * 128 + rrow16) * Cfg::kBK;
   const uint32_t row6_b = Cfg::kBBase + (wn * 128 + rrow16) * Cfg::kBK;
 
+  // K direction: where every step is whole (K a multiple of two steps, no
+  // MX scales), every second tile of a workgroup walks K backwards.  Each
+  // XCD's consecutive rounds share their A row panels (tile_walk), so a
+  // round then starts on the K range the previous one ended on, which the
+  // L2 and the 256 MB MALL still hold: 8192 x 8192 x 28672 (448 MiB of
+  // operands) +1.6 %, 8192^3 and 8192 x 28672 x 8192 level (same process).
+  // The fp32 sums run in the other order on those tiles (deterministic).
+  const bool rev_ok = !kMx && K % (2 * kStep) == 0;
+  bool rev_cur = false;
   TileSrc cur = tile_src(g, t, walk.end, tiles_m, tiles_n);
   TileSrc nxt = tile_src(g, t + walk.stride, walk.end, tiles_m, tiles_n);
 
@@ -398,7 +407,9 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   auto dma_src = [&](int kb, int op, auto edge) {
     constexpr bool kEdge = decltype(edge)::value;
     const bool next = kEdge && kb >= kt_pad;  // wave-uniform
-    uint32_t k0 = (uint32_t)(next ? kb - kt_pad : kb) * kStep;
+    const int ks = next ? kb - kt_pad : kb;
+    const bool rv = next ? (rev_ok && !rev_cur) : rev_cur;
+    uint32_t k0 = (uint32_t)(rv ? kt_pad - 1 - ks : ks) * kStep;
     // Opaque to the optimiser: keeps the per-step lane masks from being
     // hoisted out of the tile loop (they would pin VGPRs and spill).
     asm volatile("" : "+s"(k0));
@@ -980,6 +991,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
         break;
       }
       cur = nxt;
+      rev_cur = rev_ok && !rev_cur;
       nxt = tile_src(g, t + walk.stride, walk.end, tiles_m, tiles_n);
       step_pair_ov(0, std::integral_constant<int, 3>{}, std::true_type{}, et);
     }
@@ -1376,6 +1388,7 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     t += walk.stride;
     if (t >= walk.end) break;
     cur = nxt;
+    rev_cur = rev_ok && !rev_cur;
     nxt = tile_src(g, t + walk.stride, walk.end, tiles_m, tiles_n);
   }
   // The last tile's look-ahead DMA (all zeros) still lands in LDS: let it
