@@ -29,6 +29,7 @@ __all__ = [
     "HipGemmError", "lib", "lib_path", "fp8_gemm_bf16", "fp8_gemm",
     "fp8_gemm_4wave_256x256x128", "gemm_raw", "select_variant", "split_columns",
     "variant_name", "version", "tile_order", "lds_slot", "lds_slot_kpair",
+    "lds_stage_slot",
     "VARIANTS",
     "declared_symbols", "gemm_raw_ws", "workspace_size",
     "fp8_gemm_bf16_rowcol", "gemm_raw_rowcol", "GemmDesc", "gemm_desc_raw",
@@ -156,6 +157,8 @@ def lib() -> ctypes.CDLL:
     L.hipgemm_lds_slot.restype = ci
     L.hipgemm_lds_slot_kpair.argtypes = [ci, ci]
     L.hipgemm_lds_slot_kpair.restype = ci
+    L.hipgemm_lds_stage_slot.argtypes = [ci, ci]
+    L.hipgemm_lds_stage_slot.restype = ci
     _lib = L
     return L
 
@@ -287,6 +290,12 @@ def lds_slot_kpair(row: int, chunk: int) -> int:
     """Slot of K-chunk `chunk` of LDS row `row` in the instruction K order
     (hipgemm_lds_slot_kpair)."""
     return int(lib().hipgemm_lds_slot_kpair(row, chunk))
+
+
+def lds_stage_slot(row: int, piece: int) -> int:
+    """8-byte slot of 8-byte piece `piece` of row `row` of the 4-wave
+    schedule's epilogue stage (hipgemm_lds_stage_slot)."""
+    return int(lib().hipgemm_lds_stage_slot(row, piece))
 
 
 # -- torch convenience layer ----------------------------------------------

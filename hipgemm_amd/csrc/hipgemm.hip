@@ -909,4 +909,9 @@ int hipgemm_lds_slot_kpair(int row, int chunk) {
   return kpair_slot(chunk) ^ slot_xor(row);
 }
 
+int hipgemm_lds_stage_slot(int row, int piece) {
+  if (row < 0 || piece < 0 || piece > 15) return -1;
+  return piece ^ stage_xor(row);
+}
+
 }  // extern "C"

@@ -391,6 +391,15 @@ int hipgemm_lds_slot(int row, int chunk);
  */
 int hipgemm_lds_slot_kpair(int row, int chunk);
 
+/*
+ * The 8-byte slot (0-15) of the 8-byte piece `piece` (0-15) of row `row` of
+ * the 4-wave schedule's epilogue stage (128-byte rows of bf16 C, staged
+ * between the accumulators and the 16-byte stores of whole 128-byte lines).
+ * -1 for out-of-range arguments.  No reference counterpart (its epilogue
+ * stores from the accumulators).
+ */
+int hipgemm_lds_stage_slot(int row, int piece);
+
 #ifdef __cplusplus
 }
 #endif

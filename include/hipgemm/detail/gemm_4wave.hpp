@@ -822,9 +822,8 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
   // next tile, the rest of the epilogue runs after the K loop (drain).
   //
   // Stage layout: row r (0..63) of the quadrant at 128 r; its 8-byte piece x
-  // (columns 4 x .. 4 x + 3) at slot x ^ (r % 16).  A block write (16 rows of
-  // one piece per 16 lanes) covers 16 distinct slots; a read-back instruction
-  // (8 rows x 8 lanes of 8 bytes) covers each row whole.
+  // (columns 4 x .. 4 x + 3) at slot x ^ stage_xor(r) (layout.hpp): block
+  // writes and read-backs without LDS bank conflicts.
   constexpr bool kOverlap = kLine && k16 && kVecStore && !kExt && !kMx && !k6;
   struct EpiTile {
     __amdgpu_buffer_rsrc_t rsrc;  // the tile's window of C
@@ -853,12 +852,15 @@ __device__ __forceinline__ void gemm_4wave_body(const GemmArgs& g,
     int el = lane;
     asm volatile("" : "+v"(el));
     const int wl = el & 15, wg = el >> 4;
-    // write: block (bi, bj) at bi * 2048 + (wbase ^ 32 bj)
+    // write: block (bi, bj) (rows 16 bi + wl, piece 4 bj + wg) at
+    // bi * 2048 + (wbase ^ 32 bj)
+    const int sw = stage_xor(wl);
     const uint32_t wbase =
-        (uint32_t)(wl * 128 + (((wg ^ wl) & 3) << 3) + ((wl >> 2) << 5));
+        (uint32_t)(wl * 128 + (((wg ^ sw) & 3) << 3) + ((sw >> 2) << 5));
     const int rl = el >> 3, c = el & 7;
-    // read-back p: pieces 2c and 2c + 1 of row 8p + rl
-    const uint32_t rbase = (uint32_t)(rl * 128 + (((2 * c) ^ rl) << 3));
+    // read-back p: pieces 2c and 2c + 1 of row 8p + rl, at p * 1024 + (rbase
+    // ^ 64 (p % 2)) and that ^ 8 (stage_xor(8 + r) = 8 + stage_xor(r))
+    const uint32_t rbase = (uint32_t)(rl * 128 + (((2 * c) ^ stage_xor(rl)) << 3));
     const uint32_t vst = (uint32_t)((rl * g.ldc + wn * 128 + 8 * c) * 2);
     // acc16, epi_rd and et by reference: the conversion clears the
     // accumulators and the read-back fills epi_rd for the next quarter.

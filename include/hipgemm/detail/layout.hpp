@@ -47,6 +47,18 @@ namespace detail {
 constexpr int kNumXcds = 8;
 
 __host__ __device__ constexpr int slot_xor(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+// Epilogue stage of the 4-wave schedule's overlapped epilogue: 64 rows of
+// 128 bytes, the 8-byte piece x (0..15) of row r at 8-byte slot
+// x ^ stage_xor(r), which depends on r mod 16 only.  Its block writes
+// (ds_write_b64: lane l writes one piece of row l % 16) and read-backs
+// (ds_read_b64: lane l reads piece 2 (l % 8) + h of row l / 8) measured no
+// SQ_LDS_BANK_CONFLICT cycle on gfx950, where a probe replaying each pattern
+// measured, per instruction (write, read-back): x ^ (r mod 16) 0 and 2,
+// x ^ ((r & 14) | ((r >> 1) & 1)) 4 and 0, this layout 0 and 0.  The two
+// conditions that fit: the 16 rows of a block take 16 distinct slots
+// (stage_xor is a permutation of r mod 16), and rows r and r + 2 opposite
+// slot parities.
+__host__ __device__ constexpr int stage_xor(int r) { return (r & 15) ^ ((r >> 1) & 1); }
 // Instruction K order: slot (before the XOR) of K-chunk c, and its inverse.
 __host__ __device__ constexpr int kpair_slot(int c) { return ((c & 3) << 1) | (c >> 2); }
 __host__ __device__ constexpr int kpair_chunk(int s) { return ((s & 1) << 2) | (s >> 1); }

@@ -139,3 +139,36 @@ def test_tile_order_xcd_blocks_are_compact():
         wave0 = [first[b] for b in range(x, grid, 8)][:32]
         assert len({m for m, _ in wave0}) <= 4
         assert len({n for _, n in wave0}) <= 8
+
+
+# ---- the 4-wave schedule's epilogue stage (hipgemm_lds_stage_slot) -------
+# 64 rows x 128 bytes per wave.  Measured on gfx950 with a probe kernel that
+# replays one access pattern under SQ_LDS_BANK_CONFLICT (per instruction,
+# block write / read-back): slot x ^ (r mod 16): 0 / 2 cycles;
+# x ^ ((r & 14) | ((r >> 1) & 1)): 4 / 0; the layout used: 0 / 0.  The two
+# conditions below are the ones those results fit.
+
+def test_stage_slot_is_permutation_per_row():
+    for r in range(64):
+        assert sorted(hg.lds_stage_slot(r, x) for x in range(16)) == list(range(16))
+        assert [hg.lds_stage_slot(r, x) for x in range(16)] == \
+            [hg.lds_stage_slot(r % 16, x) for x in range(16)]
+    assert hg.lds_stage_slot(-1, 0) == -1 and hg.lds_stage_slot(0, 16) == -1
+
+
+def test_stage_block_writes_take_16_slots():
+    """A block write (ds_write_b64): lane l writes piece 4 bj + l / 16 of row
+    16 bi + l % 16; the 16 lanes of one piece index take 16 distinct slots."""
+    for x in range(16):
+        assert sorted(hg.lds_stage_slot(r, x) for r in range(16)) == list(range(16))
+
+
+def test_stage_readback_rows_two_apart_disjoint():
+    """A read-back (ds_read_b64): lane l reads piece 2 (l % 8) + h of row
+    8 p + l / 8; rows r and r + 2 (256 bytes apart) read disjoint slot
+    sets, i.e. opposite slot parities."""
+    for r in range(64):
+        for h in range(2):
+            a = {hg.lds_stage_slot(r, 2 * c + h) for c in range(8)}
+            b = {hg.lds_stage_slot(r + 2, 2 * c + h) for c in range(8)}
+            assert not a & b, (r, h)
