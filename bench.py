@@ -40,6 +40,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_FP8_TFLOPS = 5000.0      # MI355X dense FP8 MFMA peak (published)
+PEAK_CLOCK_MHZ = 2400.0       # the GFX clock that peak is quoted at
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E (published)
 ROTATE_BYTES = 512 << 20      # bench.cpp:24
 
@@ -180,17 +181,115 @@ def mfma_ceiling(dev, stream, prewarm_s, steps=100, iters=256):
         if code != 0:
             raise RuntimeError(f"hipgemm_probe_mfma_ceiling returned {code}")
 
-    res = time_kernel(launch, 20, steps, stream, prewarm_s)
+    monitor = GpuMonitor(0).start()
+    res = time_kernel(launch, 20, steps, stream, prewarm_s, monitor)
+    monitor.stop()
+    live = None
+    if "timed_end" in monitor.marks:
+        live = monitor.window(monitor.marks["timed_end"] - 1.0,
+                              monitor.marks["timed_end"])
     flop = grid * 4 * iters * 64 * 2.0 * 16 * 16 * 128
     tflops = flop / (res["event_ms"] * 1e-3) / 1e12
     return {"achieved": round(tflops, 1), "unit": "TFLOP/s",
             "kernel_ms_avg": round(res["event_ms"], 5),
+            "gpu_monitor": live,
             "kernel": "mfma_ceiling_16x16x128 (hipgemm_amd/probe/"
                       "mfma_ceiling.hip)",
             "what": (f"{grid} workgroups x 4 waves, {iters} x 64 "
                      "register-resident 16x16x128 e4m3 MFMA per wave, "
                      "normal(0,1) operands, no memory traffic; "
                      f"{res['prewarm_launches']} pre-warm launches")}
+
+
+class GpuMonitor:
+    """The GPU's GFX clock and socket power while a kernel runs, sampled by a
+    background thread through amdsmi (the ROCm SMI library): the mean of
+    the per-XCD current_gfxclks and current_socket_power of the GPU's
+    metrics table, every 5 ms, each sample with its host time.  window()
+    summarises the samples between two marks.  Every field is None where
+    amdsmi or a metric is unavailable; the monitor never fails the bench."""
+
+    def __init__(self, dev_index=0):
+        import threading
+        self.ok, self.h, self.samples, self.marks = False, None, [], {}
+        self.cap_w = None
+        self._stop = threading.Event()
+        self._thread = None
+        try:
+            import amdsmi
+            self.smi = amdsmi
+            amdsmi.amdsmi_init()
+            hs = amdsmi.amdsmi_get_processor_handles()
+            if len(hs) == 1:
+                self.h = hs[0]
+            else:
+                import torch
+                p = torch.cuda.get_device_properties(dev_index)
+                want = (getattr(p, "pci_domain_id", 0), p.pci_bus_id,
+                        p.pci_device_id)
+                for h in hs:
+                    bdf = amdsmi.amdsmi_get_gpu_device_bdf(h)
+                    dom, bus, rest = bdf.split(":")
+                    if (int(dom, 16), int(bus, 16),
+                            int(rest.split(".")[0], 16)) == want:
+                        self.h = h
+            if self.h is not None:
+                self._sample()
+                self.ok = bool(self.samples)
+                self.samples.clear()
+                try:
+                    cap = amdsmi.amdsmi_get_power_cap_info(self.h)["power_cap"]
+                    # microwatts in the ROCm 7 API, watts in older ones
+                    self.cap_w = round(cap / 1e6 if cap > 1e5 else cap, 1)
+                except Exception:
+                    self.cap_w = None
+        except Exception:
+            self.ok = False
+
+    def _sample(self):
+        m = self.smi.amdsmi_get_gpu_metrics_info(self.h)
+        clks = [c for c in (m.get("current_gfxclks") or [])
+                if isinstance(c, (int, float)) and c > 0]
+        if not clks and isinstance(m.get("current_gfxclk"), (int, float)):
+            clks = [m["current_gfxclk"]]
+        pw = m.get("current_socket_power")
+        if clks:
+            self.samples.append((time.perf_counter(), sum(clks) / len(clks),
+                                 pw if isinstance(pw, (int, float)) else None))
+
+    def _run(self):
+        while not self._stop.is_set():
+            try:
+                self._sample()
+            except Exception:
+                return
+            self._stop.wait(0.005)
+
+    def start(self):
+        import threading
+        if self.ok:
+            self._thread = threading.Thread(target=self._run, daemon=True)
+            self._thread.start()
+        return self
+
+    def mark(self, name):
+        self.marks[name] = time.perf_counter()
+
+    def stop(self):
+        if self._thread:
+            self._stop.set()
+            self._thread.join()
+
+    def window(self, t0, t1):
+        s = [x for x in self.samples if t0 <= x[0] <= t1]
+        if not s:
+            return None
+        clk = [x[1] for x in s]
+        pw = [x[2] for x in s if x[2] is not None]
+        return {"gfxclk_mhz": round(sum(clk) / len(clk), 1),
+                "gfxclk_mhz_range": [round(min(clk), 1), round(max(clk), 1)],
+                "socket_power_w": round(sum(pw) / len(pw), 1) if pw else None,
+                "power_cap_w": self.cap_w, "samples": len(s)}
 
 
 def prewarm(launch, seconds):
@@ -217,7 +316,7 @@ def prewarm(launch, seconds):
         chunk = max(1, min(100000, int(0.1 / max(per, 1e-7))))
 
 
-def time_kernel(launch, warmup, steps, stream, prewarm_s=0.0):
+def time_kernel(launch, warmup, steps, stream, prewarm_s=0.0, monitor=None):
     """The contract's timed loop, then a per-launch pass for diagnostics.
 
     Pre-warm (prewarm_s seconds of launches, then `warmup` more), then the
@@ -235,12 +334,16 @@ def time_kernel(launch, warmup, steps, stream, prewarm_s=0.0):
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    if monitor:
+        monitor.mark("timed_start")
     e0.record(stream)
     for i in range(steps):
         launch(warmup + i)
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    if monitor:
+        monitor.mark("timed_end")
     event_ms = e0.elapsed_time(e1) / steps
     ev = [(torch.cuda.Event(enable_timing=True),
            torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
@@ -329,8 +432,18 @@ def main():
         del src, dst
 
     flop = 2.0 * M * N * K
+    monitor = GpuMonitor(0).start()
     res = time_kernel(launch, args.warmup, args.steps, stream,
-                      args.prewarm_seconds)
+                      args.prewarm_seconds, monitor)
+    monitor.stop()
+    # The clock of the timed loop: the samples of its last second of
+    # back-to-back launches (the pre-warm's end, the warm-up and the loop;
+    # the metrics table refreshes far more slowly than a short loop lasts).
+    live = None
+    if "timed_end" in monitor.marks:
+        live = monitor.window(monitor.marks["timed_end"] - 1.0,
+                              monitor.marks["timed_end"])
+    log(f"bench: GPU monitor over the timed loop's last second: {live}")
     ms_per_step = res["wall_ms"]
     value = flop / (ms_per_step * 1e-3) / 1e12
     avg_ms = res["event_ms"]
@@ -364,6 +477,14 @@ def main():
                     "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
                     **measured}
+        # The same peak at the clock the GPU ran the loop at (measured in
+        # this run): the rate the matrix unit allows at that clock, and the
+        # share of it the kernel reaches.
+        if live and live.get("gfxclk_mhz"):
+            pk = PEAK_FP8_TFLOPS * live["gfxclk_mhz"] / PEAK_CLOCK_MHZ
+            roofline["peak_at_measured_clock"] = round(pk, 1)
+            roofline["frac_at_measured_clock"] = round(achieved / pk, 4)
+    roofline["gpu_monitor"] = live
     result = {
         "metric": ("FP8 GEMM TFLOP/s at M=N=K=8192 (% of dense FP8 peak) "
                    "+ MFMA busy %"),

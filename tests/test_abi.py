@@ -365,3 +365,27 @@ def test_mfma_ceiling_probe_library():
     assert f(FAKE, FAKE, 0, 256, None) == INVALID
     assert f(FAKE, FAKE, 256, 0, None) == INVALID
     assert not hasattr(hg.lib(), "hipgemm_probe_mfma_ceiling")
+
+
+def test_bench_gpu_monitor_window():
+    """bench.py's clock/power monitor: window() averages the samples between
+    two host times (mean clock, its range, mean power) and gives None for an
+    empty window; without a GPU the monitor starts, stops and reports
+    nothing rather than failing the bench."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, root)
+    import bench
+    m = bench.GpuMonitor.__new__(bench.GpuMonitor)
+    m.cap_w = 1400.0
+    m.samples = [(1.0, 2000.0, 1000.0), (2.0, 1800.0, 1400.0),
+                 (3.0, 1700.0, None), (9.0, 100.0, 10.0)]
+    w = m.window(1.5, 3.5)
+    assert w == {"gfxclk_mhz": 1750.0, "gfxclk_mhz_range": [1700.0, 1800.0],
+                 "socket_power_w": 1400.0, "power_cap_w": 1400.0,
+                 "samples": 2}
+    assert m.window(4.0, 8.0) is None
+    import torch
+    if not torch.cuda.is_available():
+        g = bench.GpuMonitor(0).start()
+        g.stop()
+        assert not g.ok and g.window(0.0, 1e18) is None
