@@ -381,8 +381,8 @@ T128Plan plan_t128(int M, int N, int K, int cus, int step_bytes = CfgT128::kBK) 
   if (sl < 2) return p;
   p.slices = sl;
   p.slice_steps = ss;
-  // Partial tiles after the counter region (which this schedule leaves
-  // untouched).
+  // Arrival counters (4 per tile, the per-tensor epilogue), then the
+  // partial tiles.
   p.ws_bytes = kWsCounterBytes + (size_t)tiles * sl * 65536;
   return p;
 }
@@ -397,12 +397,24 @@ hipError_t launch_t128_split(GemmArgs g, const T128Plan& p, void* ws,
   g.split.slices = p.slices;
   g.split.slice_steps = p.slice_steps;
   g.split.partial = reinterpret_cast<float*>(static_cast<char*>(ws) + kWsCounterBytes);
+  // Per-tensor bf16 epilogue without MX scales, at most 4 slices: the last
+  // slice to arrive at each quadrant sums it in the split kernel (4
+  // counters per tile in the workspace's counter region).  Else the reduce
+  // kernel, which spreads the sum over 16 workgroups per tile.  Same
+  // process, caller workspace, against the reduce kernel: 256 x 8192 x 8192
+  // (2 slices) +12 %, 128 x 8192 x 16384 (4) +2 %, 128 x 8192 x 8192 (4)
+  // level; 96 x 4096 x 28672 (8 slices, the last arrival reading 7 partial
+  // quadrants) -7 %.
+  const bool fused = !g.mx.a && !key.ext && p.slices <= 4 &&
+                     4 * tiles <= kWsMaxCounters;
+  g.split.arrivals = fused ? static_cast<int*>(ws) : nullptr;
+  if (fused) key.vec = vec_ok(key.out, g.N, g.ldc, g.C, 8);
   const void* fn = g.mx.a ? hk::tile128_split_mx(key) : hk::tile128_split(key);
   if (!fn) return hipErrorInvalidValue;
   void* args[] = {&g};
   hipError_t e = hipLaunchKernel(fn, dim3(g.workers), dim3(CfgT128::kThreads),
                                  args, 0, stream);
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || fused) return e;
   key.vec = vec_ok(key.out, g.N, g.ldc, g.C, 4);
   fn = hk::tile128_reduce(key);
   if (!fn) return hipErrorInvalidValue;
@@ -617,7 +629,7 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
       if (p.slices > 1)
         if (const hipError_t r = capturing(&cap); r != hipSuccess) return r;
       if (p.slices == 1 || cap) return launch_tiled(variant, g, key, stream);
-      return with_workspace(p.ws_bytes, 0, [&](void* w) {
+      return with_workspace(p.ws_bytes, kWsCounterBytes, [&](void* w) {
         return launch_t128_split(g, p, w, key, stream);
       });
     }

@@ -14,12 +14,13 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm_t128(GemmArgs g) {
   gemm_t128_body<kVec, false, kFmt>(g, (lds_u8*)lds);
 }
 
-// K-slices: the partial tiles, then the reduce kernel (one wave per
-// workgroup) with either epilogue.
-template <int kFmt>
+// K-slices: the partial tiles, summed by the last slice to arrive at each
+// quadrant (g.split.arrivals, per-tensor epilogue, kVec: 16-byte C stores)
+// or by the reduce kernel (one wave per workgroup) with either epilogue.
+template <bool kVec, int kFmt>
 __global__ __launch_bounds__(256, 1) void k_fp8_gemm_t128_split(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[CfgT128::kLdsBytes];
-  gemm_t128_body<true, false, kFmt, kActNone, kOutBf16, true>(g, (lds_u8*)lds);
+  gemm_t128_body<kVec, false, kFmt, kActNone, kOutBf16, true>(g, (lds_u8*)lds);
 }
 
 template <bool kVec8, bool kExt>
@@ -31,7 +32,10 @@ __global__ __launch_bounds__(64) void k_fp8_gemm_t128_reduce(GemmArgs g) {
 
 const void* tile128_split(const Key& k) {
   return sel_fmt_t128(k.fmt, [&](auto F) {
-    return (const void*)&k_fp8_gemm_t128_split<decltype(F)::value>;
+    return sel2(k.vec, [&](auto V) {
+      return (const void*)&k_fp8_gemm_t128_split<decltype(V)::value == 1,
+                                                 decltype(F)::value>;
+    });
   });
 }
 

@@ -83,10 +83,13 @@ enum {
    * 256 tiles underfill the CUs: AUTO's choice for M > 128 when its tiles
    * fit in one round over the CUs, or for K <= 2048 on at most 128 tiles of
    * 256 x 256, and for 64 < M <= 128 (except as under SKINNY).  Splits K
-   * into slices, summed by a second kernel, when its tiles fill at most a
-   * quarter of the CUs and K has at least 16 steps of 128 bytes, or at most
-   * half of them and K has at least 64 steps (CUs / tiles slices: 2, or 3
-   * for 65-85 tiles on 256 CUs); a workspace then (hipgemm_workspace_size).
+   * into slices when its tiles fill at most a quarter of the CUs and K has
+   * at least 16 steps of 128 bytes, or at most half of them and K has at
+   * least 64 steps (CUs / tiles slices: 2, or 3 for 65-85 tiles on 256
+   * CUs); a workspace then (hipgemm_workspace_size).  With the per-tensor
+   * epilogue and no MX scales, the slice that finishes a 64 x 64 quadrant
+   * last sums it in the same kernel (arrival counters in the workspace);
+   * else a second kernel sums the slices.
    * A call with no workspace under stream capture runs unsplit (as do the
    * split-K and strip schedules' calls there).  No reference counterpart
    * (the reference has 256 x 256 tiles only). */
@@ -217,9 +220,9 @@ hipError_t hipgemm_fp8_gemm_bf16(const void *A, const void *B_T, void *C,
 /*
  * hipgemm_fp8_gemm_bf16 with a caller-provided workspace.  A schedule that
  * needs scratch memory (hipgemm_workspace_size(M, N, K, variant) > 0: the
- * skinny split-K schedule keeps its per-tile arrival counters and fp32
- * partial tiles there, the 128 x 128 schedule's K-slices their partial
- * tiles) uses `workspace` instead of taking a stream-ordered allocation
+ * skinny split-K schedule and the 128 x 128 schedule's K-slices keep
+ * their arrival counters and fp32 partial tiles there) uses `workspace`
+ * instead of taking a stream-ordered allocation
  * (hipMallocAsync, a clear of the counters, hipFreeAsync) on `stream` for
  * the call, as hipgemm_fp8_gemm_bf16 does.  The workspace must be 256-byte
  * aligned and at least that size, and its first HIPGEMM_WS_COUNTER_BYTES

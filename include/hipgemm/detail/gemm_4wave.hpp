@@ -97,6 +97,10 @@ struct SplitArgs {
   int slices = 1;
   int slice_steps = 0;
   float* partial = nullptr;
+  // Non-null: one arrival counter per (tile, wave quadrant), zero between
+  // calls; the last slice to arrive at a quadrant sums it and writes C (no
+  // reduce kernel).  Null: the reduce kernel sums the partials.
+  int* arrivals = nullptr;
 };
 
 struct GemmArgs {

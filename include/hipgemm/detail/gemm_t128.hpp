@@ -70,7 +70,16 @@ struct CfgT128 {
 };
 
 // kSplit: work units are (tile, K-slice) pairs (g.split); each writes its
-// fp32 partial tile instead of C, and gemm_t128_reduce_body sums them.
+// fp32 partial tile (written through to the coherent level, sc1: the slices
+// of a tile run on several XCDs, whose L2s are not coherent with each
+// other).  With g.split.arrivals, each wave then waits for its own partial
+// stores, counts its quadrant's arrival (a relaxed agent-scope atomic), and
+// the wave that arrives last at a quadrant sums the quadrant's partials in
+// slice order (its own from its accumulators, the others read back with
+// sc1) and runs the epilogue on the sum: no waiting on other workgroups and
+// no barrier, so waves of one workgroup may take different paths here.
+// Without it, gemm_t128_reduce_body sums them in a kernel of its own; both
+// add +0 + slice 0 + slice 1 + ... in fp32, so their outputs are the same.
 // kMx: MX block scales from g.mx (the packed layout of MxArgs; per-tensor
 // epilogue).  Each step also loads, for the next step, each operand's 16
 // scale bytes of the lane into registers (one buffer load per operand).
@@ -93,7 +102,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   // 16 x 16 bytes of partial, or 16 straight from the accumulators (fp32 /
   // e4m3 output, one per block).
   constexpr int kStores = kSplit || (kExt && kOut >= kOutF32) ? 16 : Cfg::kStores;
-  static_assert(!(kSplit && kExt), "the reduce kernel applies the epilogue");
+  static_assert(!(kSplit && kExt), "the split kernels take the plain epilogue");
   static_assert(S >= 3, "pipeline depth");
   static_assert((S - 3) * kD + kStores + kScaleDma + kD < 64, "vmcnt range");
   const int lane = lane_id();
@@ -443,20 +452,89 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
     }
 
     // ---- epilogue ---------------------------------------------------------
+    bool write_c = !kSplit;
     if constexpr (kSplit) {
       // The unit's fp32 partial: wave w's 16 blocks at ((t * 4 + w) * 16 +
-      // 4 i + j) KiB of g.split.partial, lane l's 16 bytes at + 16 l.
+      // 4 i + j) KiB of g.split.partial, lane l's 16 bytes at + 16 l (unit
+      // t = slice * tiles + tile).
+      constexpr int kCoherent = 16;  // cache policy: sc1
+      const int slices = g.split.slices;
       const __amdgpu_buffer_rsrc_t rp = make_rsrc(
-          g.split.partial + (size_t)(t * 4 + wave) * 16 * 256, 16u * 1024u);
+          g.split.partial, (uint32_t)tiles * (uint32_t)slices * 65536u);
+      const uint32_t lo = (uint32_t)lane * 16u;
+      // Wave-uniform offsets in scalar registers (t's division ran on the
+      // VALU): a buffer instruction whose scalar operand sits in a VGPR is
+      // wrapped in a readfirstlane loop.
+      const uint32_t mine =
+          (uint32_t)__builtin_amdgcn_readfirstlane((t * 4 + wave) * 16384);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          store_b128<0>(
-              __builtin_bit_cast(i32x4, acc[i][j]), rp,
-              (uint32_t)((4 * i + j) * 1024 + lane * 16), 0);
-    } else {
-    const TileCoord tc = grouped_tile_u(t, tiles_m, tiles_n, g.group_m);
+          store_b128<kCoherent>(__builtin_bit_cast(i32x4, acc[i][j]), rp,
+                                lo + (uint32_t)((4 * i + j) * 1024), mine);
+      if (g.split.arrivals) {
+        const int tile = __builtin_amdgcn_readfirstlane(t % tiles);
+        const int own = __builtin_amdgcn_readfirstlane(t / tiles);
+        int* const ctr = g.split.arrivals + tile * 4 + wave;
+        // This wave's partial stores (and every other operation of it) are
+        // complete before its arrival is counted.
+        wait_vmcnt<0>();
+        int before = 0;
+        if (lane == 0)
+          before = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+        before = __builtin_amdgcn_readfirstlane(before);
+        if (before == slices - 1) {
+          // Last arrival: +0 + slice 0 + slice 1 + ..., two slices' loads
+          // in flight at a time; the own slice comes from the accumulators,
+          // slices past the last read zero (offset out of range: +0, which
+          // leaves every sum unchanged).
+          f32x4 sum[4][4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sum[i][j] = f32x4{};
+          for (int q0 = 0; q0 < slices; q0 += 2) {
+            f32x4 v[2][4][4];
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+              const int q = q0 + b;
+              const uint32_t so =
+                  (uint32_t)(((q < slices ? q : 0) * tiles + tile) * 4 + wave) * 16384u;
+              const uint32_t oob = q < slices && q != own ? 0u : kOobOffset;
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                  v[b][i][j] = __builtin_bit_cast(
+                      f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                 rp, (lo + (uint32_t)((4 * i + j) * 1024)) | oob, so,
+                                 kCoherent));
+            }
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+              const bool mine = q0 + b == own;
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                  sum[i][j] += mine ? acc[i][j] : v[b][i][j];
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = sum[i][j];
+          // Every lane stores the same zero: no branch on the lane.
+          __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          write_c = true;
+        }
+      }
+    }
+    if (write_c) {
+    const TileCoord tc =
+        grouped_tile_u(kSplit ? t % tiles : t, tiles_m, tiles_n, g.group_m);
     const int rows_left = M - tc.m * Cfg::kBM - wm * 64;  // from wave row 0
     const int cols_left = N - tc.n * Cfg::kBN - wn * 64;  // from wave col 0
     auto oob_unless = [](int x, int limit) -> uint32_t {
@@ -564,7 +642,7 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
         }
     }
 
-    }  // !kSplit
+    }  // write_c
 
     t += walk.stride;
     if (t >= walk.end) break;
