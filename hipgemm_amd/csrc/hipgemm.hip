@@ -387,8 +387,13 @@ T128Plan plan_t128(int M, int N, int K, int cus, int step_bytes = CfgT128::kBK) 
   return p;
 }
 
+// counters_zero: `ws` is a caller's workspace (or the no-alloc scratch),
+// whose counter region is zero by contract; a workspace allocated for the
+// call is not cleared for this schedule, which then sums the slices in the
+// reduce kernel (a clear would be one more launch per call).
 hipError_t launch_t128_split(GemmArgs g, const T128Plan& p, void* ws,
-                             hk::Key key, hipStream_t stream) {
+                             bool counters_zero, hk::Key key,
+                             hipStream_t stream) {
   const int tm = (g.M + CfgT128::kBM - 1) / CfgT128::kBM;
   const int tn = (g.N + CfgT128::kBN - 1) / CfgT128::kBN;
   const int tiles = tm * tn, units = tiles * p.slices, cus = cu_count();
@@ -405,7 +410,7 @@ hipError_t launch_t128_split(GemmArgs g, const T128Plan& p, void* ws,
   // (2 slices) +12 %, 128 x 8192 x 16384 (4) +2 %, 128 x 8192 x 8192 (4)
   // level; 96 x 4096 x 28672 (8 slices, the last arrival reading 7 partial
   // quadrants) -7 %.
-  const bool fused = !g.mx.a && !key.ext && p.slices <= 4 &&
+  const bool fused = counters_zero && !g.mx.a && !key.ext && p.slices <= 4 &&
                      4 * tiles <= kWsMaxCounters;
   g.split.arrivals = fused ? static_cast<int*>(ws) : nullptr;
   if (fused) key.vec = vec_ok(key.out, g.N, g.ldc, g.C, 8);
@@ -629,8 +634,8 @@ hipError_t run_gemm(const hipgemm_gemm_desc& d, bool ws_given,
       if (p.slices > 1)
         if (const hipError_t r = capturing(&cap); r != hipSuccess) return r;
       if (p.slices == 1 || cap) return launch_tiled(variant, g, key, stream);
-      return with_workspace(p.ws_bytes, kWsCounterBytes, [&](void* w) {
-        return launch_t128_split(g, p, w, key, stream);
+      return with_workspace(p.ws_bytes, 0, [&](void* w) {
+        return launch_t128_split(g, p, w, ws_given, key, stream);
       });
     }
     default:

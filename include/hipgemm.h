@@ -86,10 +86,11 @@ enum {
    * into slices when its tiles fill at most a quarter of the CUs and K has
    * at least 16 steps of 128 bytes, or at most half of them and K has at
    * least 64 steps (CUs / tiles slices: 2, or 3 for 65-85 tiles on 256
-   * CUs); a workspace then (hipgemm_workspace_size).  With the per-tensor
-   * epilogue and no MX scales, the slice that finishes a 64 x 64 quadrant
-   * last sums it in the same kernel (arrival counters in the workspace);
-   * else a second kernel sums the slices.
+   * CUs); a workspace then (hipgemm_workspace_size).  With a caller's
+   * workspace (or hipgemm_gemm_noalloc), the per-tensor epilogue, no MX
+   * scales and at most 4 slices, the slice that finishes a 64 x 64
+   * quadrant last sums it in the same kernel (arrival counters in the
+   * workspace); else a second kernel sums the slices.
    * A call with no workspace under stream capture runs unsplit (as do the
    * split-K and strip schedules' calls there).  No reference counterpart
    * (the reference has 256 x 256 tiles only). */
