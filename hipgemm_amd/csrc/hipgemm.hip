@@ -711,7 +711,18 @@ int hipgemm_select_variant(int M, int N, int K) {
   // half of them busy) over a B_T of 12 MiB or more, where the split-K
   // schedule, which fills every CU, stays ahead: 128 x 4096 x 4096 14.0 us
   // against 16.1, 128 x 2048 x 8192 14.5 / 16.1, 128 x 8192 x 2048
-  // 14.2 / 16.2 (80 rows alike).  Above, the 4-wave
+  // 14.2 / 16.2 (80 rows alike).  From 33 to 64 rows the same two where
+  // the strips fall short: the split-K schedule on the same half-filled
+  // K-splits (64 x 4096 x 4096 10.8 us against 13.0 on the strip, 40 rows
+  // 11.1 / 12.5, 64 x 2048 x 8192 11.8 / 13.5), else the 128 x 128 one for
+  // N >= 12288 (the 64-column strips then take a round and a part:
+  // 64 x 28672 x 4096 27.5 / 34.6, 40 x 14336 x 14336 43.9 / 50.9,
+  // 36 x 14336 x 4096 21.2 / 23.4) and, above 48 rows, for K >= 12288
+  // (64 x 8192 x 14336 29.8 / 31.8, 64 x 4096 x 28672 30.0 / 32.2); the
+  // strip keeps the rest (64 x 8192 x 8192 21.1 / 21.7, 40 x 8192 x 8192
+  // 18.8 / 21.3, 48 x 8192 x 14336 29.7 / 29.7).  Up to 32 rows the strip
+  // throughout (16 x 28672 x 8192 40.6 / 51.4, 32 x 28672 x 8192 50.6 /
+  // 52.8).  Above, the 4-wave
   // 16x16x128 schedule (3-7 % ahead of the 8-wave one from 2048 x 4096 up),
   // except where the 128 x 128 tiles fit in one round over the CUs (the
   // 256 x 256 ones then fill at most a quarter of them; 2048^3: 1.69x the
@@ -723,14 +734,15 @@ int hipgemm_select_variant(int M, int N, int K) {
   // process.  AUTO also splits C between the 4-wave and 128 x 128 schedules
   // for a short last round (hipgemm_split_columns); this returns the 4-wave
   // one then.
-  if (M <= 64) return HIPGEMM_VARIANT_STRIP;
+  if (M <= 32) return HIPGEMM_VARIANT_STRIP;
   if (M <= CfgSkinny::kMaxM) {
     const int cus = cu_count();
     const T128Plan p = plan_t128(M, N, K, cus);
     const int units = ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN) * p.slices;
     const bool half_filled = p.slices > 1 && 2 * units <= cus;
-    return half_filled && (long long)N * K >= (12ll << 20) ? HIPGEMM_VARIANT_SKINNY
-                                                          : HIPGEMM_VARIANT_TILE128;
+    if (half_filled && (long long)N * K >= (12ll << 20)) return HIPGEMM_VARIANT_SKINNY;
+    if (M <= 64 && N < 12288 && (M <= 48 || K < 12288)) return HIPGEMM_VARIANT_STRIP;
+    return HIPGEMM_VARIANT_TILE128;
   }
   if (ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN) <= cu_count())
     return HIPGEMM_VARIANT_TILE128;

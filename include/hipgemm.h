@@ -65,9 +65,10 @@ enum {
   HIPGEMM_VARIANT_4WAVE_MFMA16 = 2,
   /* M <= 128 only: split-K over every CU for the HBM-bound skinny shapes,
    * operands streamed straight into registers, a deterministic in-kernel
-   * reduction of the K-slices.  AUTO's choice for 64 < M <= 128 only where
+   * reduction of the K-slices.  AUTO's choice for 32 < M <= 128 only where
    * the 128 x 128 schedule's K-split would leave at least half the CUs idle
-   * over a B_T of 12 MiB or more (e.g. 128 x 4096 x 4096).  Needs a
+   * over a B_T of 12 MiB or more (e.g. 128 x 4096 x 4096, 64 x 2048 x
+   * 8192).  Needs a
    * workspace (hipgemm_workspace_size) when it splits K. */
   HIPGEMM_VARIANT_SKINNY = 3,
   /* 512 threads (8 waves, two per SIMD, in two groups that alternate
@@ -82,7 +83,9 @@ enum {
    * times as many tiles as the 256 x 256 schedules, for shapes whose 256 x
    * 256 tiles underfill the CUs: AUTO's choice for M > 128 when its tiles
    * fit in one round over the CUs, or for K <= 2048 on at most 128 tiles of
-   * 256 x 256, and for 64 < M <= 128 (except as under SKINNY).  Splits K
+   * 256 x 256, for 64 < M <= 128 (except as under SKINNY), and for
+   * 32 < M <= 64 where N >= 12288, or above 48 rows K >= 12288 (except as
+   * under SKINNY).  Splits K
    * into slices when its tiles fill at most a quarter of the CUs and K has
    * at least 16 steps of 128 bytes, or at most half of them and K has at
    * least 64 steps (CUs / tiles slices: 2, or 3 for 65-85 tiles on 256
@@ -99,8 +102,9 @@ enum {
    * (64 above 32 rows) over all of K (over a K-slice, with a workspace,
    * when the strips alone are fewer than the CUs), its 4 waves each a
    * quarter of the K-steps, summed in LDS; B_T streamed by whole-line DMA
-   * into LDS, A straight into registers.  AUTO's choice for M <= 64.  No
-   * reference counterpart. */
+   * into LDS, A straight into registers.  AUTO's choice for M <= 32, and
+   * for 32 < M <= 64 where neither SKINNY nor TILE128 is.  No reference
+   * counterpart. */
   HIPGEMM_VARIANT_STRIP = 6,
   HIPGEMM_VARIANT_COUNT = 7
 };

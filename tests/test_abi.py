@@ -51,6 +51,11 @@ def test_version_and_variants():
     assert hg.select_variant(65, 2048, 8192) == 3
     assert hg.select_variant(64, 8192, 8192) == 6
     assert hg.select_variant(16, 8192, 8192) == 6
+    assert hg.select_variant(16, 28672, 8192) == 6   # strips up to 32 rows
+    assert hg.select_variant(64, 4096, 4096) == 3    # half-filled K-split
+    assert hg.select_variant(40, 28672, 4096) == 5   # N >= 12288
+    assert hg.select_variant(64, 8192, 14336) == 5   # 49-64 rows, long K
+    assert hg.select_variant(48, 8192, 14336) == 6
     assert hg.select_variant(129, 8192, 8192) == 5   # 2 x 64 tiles of 128
 
 
