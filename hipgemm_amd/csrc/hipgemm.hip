@@ -726,8 +726,10 @@ int hipgemm_select_variant(int M, int N, int K) {
   // 16x16x128 schedule (3-7 % ahead of the 8-wave one from 2048 x 4096 up),
   // except where the 128 x 128 tiles fit in one round over the CUs (the
   // 256 x 256 ones then fill at most a quarter of them; 2048^3: 1.69x the
-  // 8-wave one), and for short K on at most 128 tiles of 256 x 256 (half a
-  // round), where the 128 x 128 schedule is level or ahead (3072 x 2048 x
+  // 8-wave one), where its tiles fit in less than two rounds and the 256 x
+  // 256 ones fill at most half the CUs (below), and for short K on at most
+  // 128 tiles of 256 x 256 (half a round), where the 128 x 128 schedule is
+  // level or ahead (3072 x 2048 x
   // 2048 +12 %, 2048 x 4096 x 512 +8 %, 2048 x 4096 x 2048 +1.4 %,
   // 2048 x 4096 x 1024 -0.6 %; from K = 3072, or above 128 tiles, the 4-wave
   // one leads by 3-48 %).  Measured on MI355X, schedules compared in one
@@ -744,9 +746,17 @@ int hipgemm_select_variant(int M, int N, int K) {
     if (M <= 64 && N < 12288 && (M <= 48 || K < 12288)) return HIPGEMM_VARIANT_STRIP;
     return HIPGEMM_VARIANT_TILE128;
   }
-  if (ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN) <= cu_count())
-    return HIPGEMM_VARIANT_TILE128;
+  const int cus = cu_count();
+  const int t1 = ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN);
+  if (t1 <= cus) return HIPGEMM_VARIANT_TILE128;
   if (K <= 2048 && tiles_of(M, N) <= 128) return HIPGEMM_VARIANT_TILE128;
+  // 256 x 256 tiles on at most half the CUs, 128 x 128 ones in less than
+  // two rounds: 1536 x 4096 x 4096 35.3 us against 39.2, x 8192 64.8 /
+  // 71.5, 1280 x 4096 x 8192 64.6 / 71.3, 1792 x 4096 x 4096 36.5 / 39.1,
+  // 1152 x 4096 x 4096 35.4 / 37.4, 768 x 8192 x 8192 72.9 / 71.9; in two
+  // full rounds the 4-wave one stays ahead (1024 x 8192 x 4096 40.5 /
+  // 41.2, 2048 x 4096 x 8192 71.3 / 74.1).
+  if (2 * tiles_of(M, N) <= cus && t1 < 2 * cus) return HIPGEMM_VARIANT_TILE128;
   return HIPGEMM_VARIANT_4WAVE_MFMA16;
 }
 
