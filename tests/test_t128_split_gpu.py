@@ -10,7 +10,8 @@ out 16-byte stores (ldc not a multiple of 8: the 2-byte epilogue), and two
 Ternary inputs (every sum exact) must equal the oracle bit for bit, with a
 canary-guarded C; each case runs twice on one workspace, which must give
 the same bits and leave the workspace's arrival counters at zero.  Normal
-inputs at the skinny BASELINE shape stay within the tolerance.
+inputs at the skinny BASELINE shape stay within the tolerance, and with
+normal inputs the in-kernel sum and the reduce kernel give the same bits.
 """
 import numpy as np
 import pytest
@@ -89,4 +90,34 @@ def test_t128_split_fused_normal_within_tolerance(gpu, oracle):
     assert guard
     max_rel, exact, _ = compare(C, oracle.gemm(A, B, sa, sb))
     say(f"    max_rel={max_rel:.3e} exact={exact:.6f}")
+    assert max_rel <= REL_TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 8192, 8192), (256, 8192, 8192),
+                                   (128, 10240, 8192)])
+def test_t128_split_sum_in_kernel_equals_reduce_kernel(gpu, oracle, M, N, K):
+    """Normal inputs (sums not exact): the in-kernel sum (caller workspace)
+    and the reduce kernel (no workspace: the library allocates one for the
+    call and sums in a second kernel) add the same slices in the same order,
+    so C is the same bit for bit."""
+    torch = gpu
+    say(f"case t128-split fused-vs-reduce M={M} N={N} K={K} seed=91")
+    A = oracle.fill((M, K), 9101, po.NORMAL, 0.0, 1.0)
+    B = oracle.fill((N, K), 9102, po.NORMAL, 0.0, 1.0)
+    ws = torch.zeros(hg.workspace_size(M, N, K, TILE128), dtype=torch.uint8,
+                     device="cuda")
+    fused, guard = run(torch, A, B, M, N, K, N, 0.75, 1.5, ws)
+    assert guard
+    a, b = to_dev(torch, A), to_dev(torch, B)
+    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    ta, tb = scale_tensor(torch, 0.75), scale_tensor(torch, 1.5)
+    code = hg.gemm_raw(a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, K,
+                       K, N, ta.data_ptr(), tb.data_ptr(), TILE128,
+                       torch.cuda.current_stream().cuda_stream)
+    assert code == 0
+    torch.cuda.synchronize()
+    reduced = out.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(fused, reduced), (
+        f"{int((fused != reduced).sum())} of {M * N} outputs differ")
+    max_rel, _, _ = compare(fused, oracle.gemm(A, B, 0.75, 1.5))
     assert max_rel <= REL_TOL
