@@ -465,14 +465,14 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
       // Wave-uniform offsets in scalar registers (t's division ran on the
       // VALU): a buffer instruction whose scalar operand sits in a VGPR is
       // wrapped in a readfirstlane loop.
-      const uint32_t mine =
+      const uint32_t own_off =
           (uint32_t)__builtin_amdgcn_readfirstlane((t * 4 + wave) * 16384);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           store_b128<kCoherent>(__builtin_bit_cast(i32x4, acc[i][j]), rp,
-                                lo + (uint32_t)((4 * i + j) * 1024), mine);
+                                lo + (uint32_t)((4 * i + j) * 1024), own_off);
       if (g.split.arrivals) {
         const int tile = __builtin_amdgcn_readfirstlane(t % tiles);
         const int own = __builtin_amdgcn_readfirstlane(t / tiles);
@@ -514,12 +514,12 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
             }
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-              const bool mine = q0 + b == own;
+              const bool is_own = q0 + b == own;
 #pragma unroll
               for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                  sum[i][j] += mine ? acc[i][j] : v[b][i][j];
+                  sum[i][j] += is_own ? acc[i][j] : v[b][i][j];
             }
           }
 #pragma unroll
