@@ -8,7 +8,8 @@ the same inputs, stream and output buffer, in the same process: the C ABI's
 default choice and each schedule, and the C++ drop-in template
 (include/fp8_4wave.hpp, launched as the reference's bench.cpp:78 launches
 its kernel, through tests/dropin/libdropin.so) where it is instantiated.
-The test prints the rates.  Its gate compares the default with the
+The test prints the rates, with the GFX clock and socket power of each
+timed loop (amdsmi, where present).  Its gate compares the default with the
 reference in blocks of launches that alternate between the two (ABBA
 order, so that the GPU's drift in clock over the run falls on both alike;
 consecutive rounds of one kernel in the report above differ by up to about
@@ -95,16 +96,29 @@ def test_speed_vs_reference_kernel(gpu, M, N, K):
     kernels = [("reference", theirs)] + [
         (hg.variant_name(v), mine_v(v)) for v in (0, 1, 2, 4)] + extra
     rates = {name: [] for name, _ in kernels}
+    # GFX clock and socket power over each timed loop's last half second
+    # (bench.GpuMonitor; None without amdsmi).
+    gpu = {name: [] for name, _ in kernels}
     for rnd in range(2):
         for name, fn in (kernels if rnd == 0 else kernels[::-1]):
             say(f"speed {M}x{N}x{K}: round {rnd} {name}, {steps} steps")
-            r = bench.time_kernel(fn, steps, steps, stream, 0.5)
+            mon = bench.GpuMonitor(0).start()
+            r = bench.time_kernel(fn, steps, steps, stream, 0.5, mon)
+            mon.stop()
+            if "timed_end" in mon.marks:
+                gpu[name].append(mon.window(mon.marks["timed_end"] - 0.5,
+                                            mon.marks["timed_end"]))
             rates[name].append(flop / (r["wall_ms"] * 1e-3) / 1e12)
     tr = sum(rates["reference"]) / 2
     for name, _ in kernels:
         t = sum(rates[name]) / 2
+        w = [x for x in gpu[name] if x]
+        clk = (f"; {sum(x['gfxclk_mhz'] for x in w) / len(w):.0f} MHz, "
+               f"{sum(x['socket_power_w'] or 0 for x in w) / len(w):.0f} W"
+               if w else "")
         say(f"speed {M}x{N}x{K}: {name} {t:.1f} TFLOP/s (rounds "
-            f"{rates[name][0]:.1f}, {rates[name][1]:.1f}); ratio {t / tr:.3f}")
+            f"{rates[name][0]:.1f}, {rates[name][1]:.1f}); ratio {t / tr:.3f}"
+            f"{clk}")
     # The gate: blocks of `steps` launches, reference and default in ABBA
     # order, each block between its own pair of events on the stream.
     pair = [theirs, mine_v(0)]
