@@ -21,14 +21,14 @@
 //     ring of L + 1 stages private to the wave, with the non-temporal hint:
 //     measured on a 64 MiB B_T, whole lines with nt stream at 5.4 TB/s, the
 //     16-rows-by-64-bytes pattern of a direct register load at 4.5.  The
-//     stage rows are 128 bytes with the slot_xor swizzle (layout.hpp) in
-//     the plain K order.  The MFMA operand reads (chunks g and g + 4 of 16
-//     rows per lane group g) then cost 4 LDS conflict cycles each; the
-//     instruction K order of layout.hpp removes them, but its DMA (each
-//     lane quad fetching two 32-byte pieces of a line instead of one
-//     64-byte run) measured 2.5 % slower on this HBM-bound kernel (same
-//     L1 request count, 6 % more address-stall cycles).  The LDS is a few
-//     percent busy here, so the conflicts cost nothing measurable.
+//     stage rows are 128 bytes in the plain K order with the strip_xor
+//     swizzle (layout.hpp), under which the MFMA operand reads (chunks g
+//     and g + 4 of 16 rows per lane group g) have no LDS bank conflict and
+//     each DMA lane quad fetches one 64-byte run.  (With slot_xor, the
+//     other schedules' swizzle, the same reads cost 4 conflict cycles each;
+//     its conflict-free alternative, the instruction K order of layout.hpp,
+//     makes each lane quad fetch two 32-byte pieces, which measured 2.5 %
+//     slower on this HBM-bound kernel.)
 //   * A (at most 128 rows, read by every strip, so L2-resident) goes
 //     straight into registers, L steps ahead like B.
 //   * K order inside a step: lane group g = l / 16 of the MFMA holds
@@ -121,14 +121,14 @@ __device__ __forceinline__ void gemm_strip_body(const StripArgs& g, lds_u8* lds)
       make_rsrc(g.B + (size_t)n0 * g.ldb, (uint32_t)rows_b * (uint32_t)g.ldb);
 
   // DMA lane geometry: instruction j covers strip rows 8j .. 8j + 7; lane l
-  // fetches row 8j + l/8, K-chunk (l%8) ^ slot_xor(row) -> LDS slot l % 8.
+  // fetches row 8j + l/8, K-chunk (l%8) ^ strip_xor(row) -> LDS slot l % 8.
   const int drow = lane >> 3;
   uint32_t voff_b[kDmaB];
   int dch[kDmaB];
 #pragma unroll
   for (int j = 0; j < kDmaB; ++j) {
     const int row = 8 * j + drow;
-    dch[j] = (lane & 7) ^ slot_xor(row & 15);
+    dch[j] = (lane & 7) ^ strip_xor(row);
     voff_b[j] = (uint32_t)row * (uint32_t)g.ldb + (uint32_t)dch[j] * 16u;
   }
   // MFMA lane geometry: row r = l % 16 of a block, lane group gq = l / 16
@@ -138,7 +138,7 @@ __device__ __forceinline__ void gemm_strip_body(const StripArgs& g, lds_u8* lds)
 #pragma unroll
   for (int m = 0; m < kMB; ++m)
     voff_a[m] = (uint32_t)(16 * m + r16) * (uint32_t)g.lda + 16u * gq;
-  const int sx = slot_xor(r16);
+  const int sx = strip_xor(r16);
   lds_u8* ring = lds + wave * R * kStageB;
   const uint32_t rd0 = (uint32_t)(r16 * Cfg::kBK + ((gq ^ sx) * 16));
   const uint32_t rd1 = (uint32_t)(r16 * Cfg::kBK + (((gq + 4) ^ sx) * 16));

@@ -13,10 +13,11 @@
 //    group g.  Measured on gfx950 (SQ_LDS_BANK_CONFLICT of single
 //    ds_read_b128 patterns): the groups reading slots 2g ^ slot_xor(r) -- or
 //    (2g + 1) ^ slot_xor(r) -- cost no conflict cycle; slots g ^ slot_xor(r)
-//    or (g + 4) ^ slot_xor(r) cost 4 per instruction, with this or any other
-//    per-row XOR tried.  In the 8 slots of a 16-row block each row parity
-//    gets 8 distinct slots (tests/test_layout.py checks this through the
-//    built library).
+//    or (g + 4) ^ slot_xor(r) cost 4 per instruction, and 4 to 12 under six
+//    other per-row XORs tried; under r & 7 (strip_xor, below) they cost
+//    none.  In the 8 slots of a 16-row block each row parity gets 8
+//    distinct slots (tests/test_layout.py checks this through the built
+//    library).
 //
 //    Instruction K order.  The f8f6f4 MFMA's lane group g holds K-chunks g
 //    and g + 4 of its row (K 16g .. 16g + 15 and 64 + 16g .. 64 + 16g + 15).
@@ -59,6 +60,14 @@ __host__ __device__ constexpr int slot_xor(int r) { return (r & 7) ^ ((r >> 3) &
 // (stage_xor is a permutation of r mod 16), and rows r and r + 2 opposite
 // slot parities.
 __host__ __device__ constexpr int stage_xor(int r) { return (r & 15) ^ ((r >> 1) & 1); }
+// B_T stages of the column-strip schedule: 128-byte rows in the plain K
+// order, K-chunk c of row r at slot c ^ strip_xor(r), read by lane group g at
+// chunks g and g + 4 (the order of its register-loaded A).  Measured on
+// gfx950 (ds_read_b128, 16 rows per lane group): this swizzle gives those
+// reads no conflict cycle, where slot_xor gives 4 per instruction; its chunk
+// 2g / 2g + 1 reads would cost 4.  Each DMA lane quad still fetches one
+// aligned 64-byte half of a line.
+__host__ __device__ constexpr int strip_xor(int r) { return r & 7; }
 // Instruction K order: slot (before the XOR) of K-chunk c, and its inverse.
 __host__ __device__ constexpr int kpair_slot(int c) { return ((c & 3) << 1) | (c >> 2); }
 __host__ __device__ constexpr int kpair_chunk(int s) { return ((s & 1) << 2) | (s >> 1); }
