@@ -226,19 +226,20 @@ hipError_t hipgemm_fp8_gemm_bf16(const void *A, const void *B_T, void *C,
 /*
  * hipgemm_fp8_gemm_bf16 with a caller-provided workspace.  A schedule that
  * needs scratch memory (hipgemm_workspace_size(M, N, K, variant) > 0: the
- * skinny split-K schedule and the 128 x 128 schedule's K-slices keep
- * their arrival counters and fp32 partial tiles there) uses `workspace`
- * instead of taking a stream-ordered allocation
- * (hipMallocAsync, a clear of the counters, hipFreeAsync) on `stream` for
- * the call, as hipgemm_fp8_gemm_bf16 does.  The workspace must be 256-byte
- * aligned and at least that size, and its first HIPGEMM_WS_COUNTER_BYTES
- * bytes zero before its first use (every call leaves them zero: see
- * HIPGEMM_WS_COUNTER_BYTES).  Calls that may run concurrently must not
- * share a workspace.  Returns hipErrorInvalidValue if it is missing or too
- * small when needed.
- * While `stream` is being captured into a graph, an entry point that would
- * allocate a workspace for the call (none given, one needed) returns
- * hipErrorInvalidValue instead: pass a workspace there.
+ * skinny split-K and column-strip schedules' K-slices and the 128 x 128
+ * schedule's keep their arrival counters and fp32 partial tiles there) uses
+ * `workspace` instead of taking a stream-ordered allocation
+ * (hipMallocAsync, a clear of the counters, hipFreeAsync: about 12 us of
+ * host time) on `stream` for the call, as hipgemm_fp8_gemm_bf16 does.  The
+ * workspace must be 256-byte aligned and at least that size, and its first
+ * HIPGEMM_WS_COUNTER_BYTES bytes zero before its first use (every call
+ * leaves them zero: see HIPGEMM_WS_COUNTER_BYTES).  Calls that may run
+ * concurrently must not share a workspace.  Returns hipErrorInvalidValue if
+ * it is missing or too small when needed.
+ * While `stream` is being captured into a graph, an entry point given no
+ * workspace allocates none: a schedule that would split K runs with one
+ * K-slice (the same result within rounding, slower on the shapes that
+ * split).  Pass a workspace there to keep the split.
  * Replaces: the same reference launch (the reference has no workspace and no
  * split-K path).
  */
