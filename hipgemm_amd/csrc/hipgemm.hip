@@ -753,10 +753,17 @@ int hipgemm_select_variant(int M, int N, int K) {
   // 256 x 256 tiles on at most half the CUs, 128 x 128 ones in less than
   // two rounds: 1536 x 4096 x 4096 35.3 us against 39.2, x 8192 64.8 /
   // 71.5, 1280 x 4096 x 8192 64.6 / 71.3, 1792 x 4096 x 4096 36.5 / 39.1,
-  // 1152 x 4096 x 4096 35.4 / 37.4, 768 x 8192 x 8192 72.9 / 71.9; in two
+  // 1152 x 4096 x 4096 35.4 / 37.4, 4096 x 1536 x 4096 38.6 / 39.1; in two
   // full rounds the 4-wave one stays ahead (1024 x 8192 x 4096 40.5 /
-  // 41.2, 2048 x 4096 x 8192 71.3 / 74.1).
-  if (2 * tiles_of(M, N) <= cus && t1 < 2 * cus) return HIPGEMM_VARIANT_TILE128;
+  // 41.2, 2048 x 4096 x 8192 71.3 / 74.1).  Except with a side of 8192 or
+  // more and K from 4096, where the 4-wave one leads: 640 x 8192 x 8192
+  // 72.5 / 67.4, x 4096 39.6 / 37.6, x 16384 134.2 / 128.4, 896 x 8192 x
+  // 8192 74.0 / 67.9, 8192 x 640 x 8192 72.3 / 67.9, 768 x 8192 x 8192
+  // 74.0 / 72.7 (768 x 8192 x 16384 135.0 / 140.9 the one exception seen);
+  // with K = 2048 the two are level there (640 x 8192 x 2048 22.7 / 23.0).
+  const bool long_side = (M >= 8192 || N >= 8192) && K >= 4096;
+  if (2 * tiles_of(M, N) <= cus && t1 < 2 * cus && !long_side)
+    return HIPGEMM_VARIANT_TILE128;
   return HIPGEMM_VARIANT_4WAVE_MFMA16;
 }
 

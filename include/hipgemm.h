@@ -83,7 +83,8 @@ enum {
    * times as many tiles as the 256 x 256 schedules, for shapes whose 256 x
    * 256 tiles underfill the CUs: AUTO's choice for M > 128 when its tiles
    * fit in one round over the CUs, or in less than two where the 256 x 256
-   * ones fill at most half of them, or for K <= 2048 on at most 128 tiles
+   * ones fill at most half of them (unless M or N >= 8192 and K >= 4096),
+   * or for K <= 2048 on at most 128 tiles
    * of 256 x 256, for 64 < M <= 128 (except as under SKINNY), and for
    * 32 < M <= 64 where N >= 12288, or above 48 rows K >= 12288 (except as
    * under SKINNY).  Splits K

@@ -46,6 +46,9 @@ def test_version_and_variants():
     assert hg.select_variant(2048, 4096, 2048) == 5   # short K, 128 tiles
     assert hg.select_variant(2048, 4096, 4096) == 2   # 2 full rounds of 128x128
     assert hg.select_variant(1536, 4096, 4096) == 5   # 96 tiles, 1.5 rounds
+    assert hg.select_variant(640, 8192, 8192) == 2    # the same with a side of 8192
+    assert hg.select_variant(8192, 896, 4096) == 2
+    assert hg.select_variant(640, 8192, 2048) == 5    # short K
     assert hg.select_variant(128, 8192, 8192) == 5   # 64 tiles x 4 K-slices
     assert hg.select_variant(80, 8192, 1024) == 5    # short K, no K-slices
     assert hg.select_variant(128, 4096, 4096) == 3   # half-filled K-split

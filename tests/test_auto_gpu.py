@@ -30,6 +30,7 @@ TERNARY = np.array([0xB8, 0x00, 0x38], np.uint8)  # -1, 0, +1
     (32, 28672, 8192, "strip"),     # up to 32 rows
     (1536, 4096, 4096, "tile128"),  # 96 tiles of 256, 384 of 128
     (1152, 4096, 4096, "tile128"),
+    (640, 8192, 4096, "4wave_mfma16"),   # the same region, a side of 8192
     (2048, 4096, 4096, "4wave_mfma16"),  # 512 tiles of 128: two full rounds
 ])
 def test_auto_pick_bit_exact(gpu, oracle, M, N, K, pick):
