@@ -709,9 +709,13 @@ int hipgemm_select_variant(int M, int N, int K) {
   // 128 x 8192 x 1024 7.9 / 12.8, 128 x 512 x 8192 11.8 / 17.2.  Except
   // where its K-split stops at 8-step slices short of the CUs (at most
   // half of them busy) over a B_T of 12 MiB or more, where the split-K
-  // schedule, which fills every CU, stays ahead: 128 x 4096 x 4096 14.0 us
-  // against 16.1, 128 x 2048 x 8192 14.5 / 16.1, 128 x 8192 x 2048
-  // 14.2 / 16.2 (80 rows alike).  From 33 to 64 rows the same two where
+  // schedule, which fills every CU, stays ahead: 128 x 4096 x 4096 14.4 us
+  // against 16.3, 128 x 2048 x 8192 14.7 / 16.2, 128 x 4096 x 3072
+  // 13.5 / 16.2 (100 rows alike) -- but not, from 65 rows, where the
+  // split has only 2 slices, whose partials the 128 x 128 schedule sums in
+  // its split kernel with a caller's workspace: 128 x 8192 x 2048 14.5 /
+  // 13.7, 128 x 6144 x 2048 15.6 / 13.0, 128 x 8192 x 2560 18.0 / 16.1,
+  // 72 x 8192 x 2048 13.9 / 13.1.  From 33 to 64 rows the same two where
   // the strips fall short: the split-K schedule on the same half-filled
   // K-splits (64 x 4096 x 4096 10.8 us against 13.0 on the strip, 40 rows
   // 11.1 / 12.5, 64 x 2048 x 8192 11.8 / 13.5), else the 128 x 128 one for
@@ -742,7 +746,8 @@ int hipgemm_select_variant(int M, int N, int K) {
     const T128Plan p = plan_t128(M, N, K, cus);
     const int units = ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN) * p.slices;
     const bool half_filled = p.slices > 1 && 2 * units <= cus;
-    if (half_filled && (long long)N * K >= (12ll << 20)) return HIPGEMM_VARIANT_SKINNY;
+    if (half_filled && (long long)N * K >= (12ll << 20) && (M <= 64 || p.slices > 2))
+      return HIPGEMM_VARIANT_SKINNY;
     if (M <= 64 && N < 12288 && (M <= 48 || K < 12288)) return HIPGEMM_VARIANT_STRIP;
     return HIPGEMM_VARIANT_TILE128;
   }

@@ -67,8 +67,9 @@ enum {
    * operands streamed straight into registers, a deterministic in-kernel
    * reduction of the K-slices.  AUTO's choice for 32 < M <= 128 only where
    * the 128 x 128 schedule's K-split would leave at least half the CUs idle
-   * over a B_T of 12 MiB or more (e.g. 128 x 4096 x 4096, 64 x 2048 x
-   * 8192).  Needs a
+   * over a B_T of 12 MiB or more, above 64 rows only when that split has
+   * 3 slices or more (e.g. 128 x 4096 x 4096, 64 x 2048 x 8192; not
+   * 128 x 8192 x 2048).  Needs a
    * workspace (hipgemm_workspace_size) when it splits K. */
   HIPGEMM_VARIANT_SKINNY = 3,
   /* 512 threads (8 waves, two per SIMD, in two groups that alternate

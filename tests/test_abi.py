@@ -52,6 +52,8 @@ def test_version_and_variants():
     assert hg.select_variant(128, 8192, 8192) == 5   # 64 tiles x 4 K-slices
     assert hg.select_variant(80, 8192, 1024) == 5    # short K, no K-slices
     assert hg.select_variant(128, 4096, 4096) == 3   # half-filled K-split
+    assert hg.select_variant(128, 8192, 2048) == 5   # ... of 2 slices only
+    assert hg.select_variant(64, 8192, 2048) == 3
     assert hg.select_variant(65, 2048, 8192) == 3
     assert hg.select_variant(64, 8192, 8192) == 6
     assert hg.select_variant(16, 8192, 8192) == 6

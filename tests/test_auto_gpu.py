@@ -22,6 +22,7 @@ TERNARY = np.array([0xB8, 0x00, 0x38], np.uint8)  # -1, 0, +1
 @pytest.mark.parametrize("M,N,K,pick", [
     (64, 4096, 4096, "skinny"),     # half-filled K-split, 16 MiB of B_T
     (40, 2048, 8192, "skinny"),
+    (128, 6144, 2048, "tile128"),   # half-filled, but 2 slices
     (40, 28672, 4096, "tile128"),   # N >= 12288
     (36, 14336, 4096, "tile128"),
     (64, 8192, 14336, "tile128"),   # above 48 rows, K >= 12288
