@@ -697,36 +697,39 @@ int fp4_variant(int variant, int M, int N, int Kb) {
 extern "C" {
 
 int hipgemm_select_variant(int M, int N, int K) {
-  // Up to 128 rows the GEMM is a stream over B_T.  Up to 64 rows the
-  // column-strip schedule (whole-line DMA of B_T, no split-K partials when
-  // N / 32 fills the CUs): 16 x 8192 x 8192 12.9 us against 17.8 on the
-  // split-K schedule, 32 rows 15.1 against 21.6, 64 rows 21.0 against 24.9.
-  // From 65 to 128 rows the 128 x 128 schedule (K-sliced where its tiles
-  // fill at most a quarter of the CUs, plan_t128), which DMAs whole lines of
-  // A and B_T and reads A once per 128 columns: 128 x 8192 x 8192 22.6 us
-  // against 28.0 on the split-K schedule, 80 x 8192 x 8192 21.8 / 26.3,
-  // 128 x 28672 x 8192 52.7 / 74.3, 128 x 4096 x 28672 32.9 / 43.6,
-  // 128 x 8192 x 1024 7.9 / 12.8, 128 x 512 x 8192 11.8 / 17.2.  Except
-  // where its K-split stops at 8-step slices short of the CUs (at most
-  // half of them busy) over a B_T of 12 MiB or more, where the split-K
-  // schedule, which fills every CU, stays ahead: 128 x 4096 x 4096 14.4 us
-  // against 16.3, 128 x 2048 x 8192 14.7 / 16.2, 128 x 4096 x 3072
-  // 13.5 / 16.2 (100 rows alike) -- but not, from 65 rows, where the
-  // split has only 2 slices, whose partials the 128 x 128 schedule sums in
-  // its split kernel with a caller's workspace: 128 x 8192 x 2048 14.5 /
-  // 13.7, 128 x 6144 x 2048 15.6 / 13.0, 128 x 8192 x 2560 18.0 / 16.1,
-  // 72 x 8192 x 2048 13.9 / 13.1.  From 33 to 64 rows the same two where
-  // the strips fall short: the split-K schedule on the same half-filled
-  // K-splits (64 x 4096 x 4096 10.8 us against 13.0 on the strip, 40 rows
-  // 11.1 / 12.5, 64 x 2048 x 8192 11.8 / 13.5), else the 128 x 128 one for
-  // N >= 12288 (the 64-column strips then take a round and a part:
-  // 64 x 28672 x 4096 27.5 / 34.6, 40 x 14336 x 14336 43.9 / 50.9,
-  // 36 x 14336 x 4096 21.2 / 23.4) and, above 48 rows, for K >= 12288
-  // (64 x 8192 x 14336 29.8 / 31.8, 64 x 4096 x 28672 30.0 / 32.2); the
-  // strip keeps the rest (64 x 8192 x 8192 21.1 / 21.7, 40 x 8192 x 8192
-  // 18.8 / 21.3, 48 x 8192 x 14336 29.7 / 29.7).  Up to 32 rows the strip
-  // throughout (16 x 28672 x 8192 40.6 / 51.4, 32 x 28672 x 8192 50.6 /
-  // 52.8).  Above, the 4-wave
+  // Up to 128 rows the GEMM is a stream over B_T (times: us, caller
+  // workspace, schedules compared in one process on MI355X).
+  //  * Up to 32 rows the column-strip schedule (whole-line DMA of B_T, no
+  //    split-K partials when N / 32 fills the CUs): 16 x 8192 x 8192 12.9
+  //    against 17.8 on the split-K schedule, 32 rows 15.1 / 21.6,
+  //    16 x 28672 x 8192 40.6 / 51.4, 32 x 8192 x 1024 5.8 / 12.3 (8.0 on
+  //    the 128 x 128 one).
+  //  * "Half-filled": the 128 x 128 schedule's K-split (plan_t128) stops
+  //    at its 8-step slice floor with at most half the CUs busy.  The
+  //    split-K schedule, which fills every CU, is then ahead from 33 to 64
+  //    rows for N >= 1024 (64 x 2048 x 4096 10.3 against 12.4 on the strip
+  //    and 14.8 on the 128 x 128 one, 64 x 1024 x 8192 11.7 / 15.1 / 12.3,
+  //    40 x 4096 x 2048 9.1 / 11.5 / 12.3, 64 x 4096 x 4096 10.8 / 13.1 /
+  //    16.0), and from 65 rows for N >= 2048 with 3 slices or more
+  //    (128 x 4096 x 4096 14.4 / 16.3 on the 128 x 128 one, 128 x 2048 x
+  //    8192 14.7 / 16.2, 120 x 2560 x 4096 13.9 / 15.0, 80 x 2048 x 4096
+  //    12.9 / 15.0).  With 2 slices the 128 x 128 schedule sums the two
+  //    partials in its split kernel and stays ahead (128 x 6144 x 2048 13.0
+  //    / 15.6, 128 x 8192 x 2048 13.7 / 14.5), as below 2048 columns
+  //    (100 x 1536 x 8192 13.9 / 15.9, 128 x 1024 x 8192 12.6 / 14.2).
+  //  * Else from 33 to 64 rows: the 128 x 128 schedule for K <= 1024,
+  //    where each of the strip's four waves would get two steps or fewer
+  //    (64 x 2048 x 1024 7.4 against 10.2, 64 x 6144 x 1024 8.1 / 11.0),
+  //    and for N >= 12288 (the 64-column strips then take a round and a
+  //    part: 64 x 28672 x 4096 30.1 / 34.5, 40 x 14336 x 14336 44.0 / 50.4)
+  //    and, above 48 rows, for K >= 12288 (64 x 8192 x 14336 29.9 / 31.3);
+  //    the strip keeps the rest (64 x 8192 x 8192 21.0 / 21.7, 40 x 8192 x
+  //    8192 18.9 / 21.4).
+  //  * Else from 65 rows the 128 x 128 schedule, which DMAs whole lines of
+  //    A and B_T and reads A once per 128 columns: 128 x 8192 x 8192 22.6
+  //    against 28.0 on the split-K schedule, 128 x 28672 x 8192 52.7 /
+  //    74.3, 128 x 4096 x 28672 32.9 / 43.6, 128 x 8192 x 1024 7.9 / 12.8.
+  // Above 128 rows the 4-wave
   // 16x16x128 schedule (3-7 % ahead of the 8-wave one from 2048 x 4096 up),
   // except where the 128 x 128 tiles fit in one round over the CUs (the
   // 256 x 256 ones then fill at most a quarter of them; 2048^3: 1.69x the
@@ -736,19 +739,22 @@ int hipgemm_select_variant(int M, int N, int K) {
   // level or ahead (3072 x 2048 x
   // 2048 +12 %, 2048 x 4096 x 512 +8 %, 2048 x 4096 x 2048 +1.4 %,
   // 2048 x 4096 x 1024 -0.6 %; from K = 3072, or above 128 tiles, the 4-wave
-  // one leads by 3-48 %).  Measured on MI355X, schedules compared in one
-  // process.  AUTO also splits C between the 4-wave and 128 x 128 schedules
-  // for a short last round (hipgemm_split_columns); this returns the 4-wave
-  // one then.
+  // one leads by 3-48 %).  AUTO also splits C between the 4-wave and 128 x
+  // 128 schedules for a short last round (hipgemm_split_columns); this
+  // returns the 4-wave one then.
   if (M <= 32) return HIPGEMM_VARIANT_STRIP;
   if (M <= CfgSkinny::kMaxM) {
     const int cus = cu_count();
     const T128Plan p = plan_t128(M, N, K, cus);
     const int units = ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN) * p.slices;
     const bool half_filled = p.slices > 1 && 2 * units <= cus;
-    if (half_filled && (long long)N * K >= (12ll << 20) && (M <= 64 || p.slices > 2))
-      return HIPGEMM_VARIANT_SKINNY;
-    if (M <= 64 && N < 12288 && (M <= 48 || K < 12288)) return HIPGEMM_VARIANT_STRIP;
+    if (M <= 64) {
+      if (half_filled && N >= 1024) return HIPGEMM_VARIANT_SKINNY;
+      if (K <= 1024) return HIPGEMM_VARIANT_TILE128;
+      if (N < 12288 && (M <= 48 || K < 12288)) return HIPGEMM_VARIANT_STRIP;
+      return HIPGEMM_VARIANT_TILE128;
+    }
+    if (half_filled && N >= 2048 && p.slices > 2) return HIPGEMM_VARIANT_SKINNY;
     return HIPGEMM_VARIANT_TILE128;
   }
   const int cus = cu_count();

@@ -66,11 +66,11 @@ enum {
   /* M <= 128 only: split-K over every CU for the HBM-bound skinny shapes,
    * operands streamed straight into registers, a deterministic in-kernel
    * reduction of the K-slices.  AUTO's choice for 32 < M <= 128 only where
-   * the 128 x 128 schedule's K-split would leave at least half the CUs idle
-   * over a B_T of 12 MiB or more, above 64 rows only when that split has
-   * 3 slices or more (e.g. 128 x 4096 x 4096, 64 x 2048 x 8192; not
-   * 128 x 8192 x 2048).  Needs a
-   * workspace (hipgemm_workspace_size) when it splits K. */
+   * the 128 x 128 schedule's K-split would leave at least half the CUs
+   * idle: up to 64 rows for N >= 1024, above 64 rows for N >= 2048 when
+   * that split has 3 slices or more (e.g. 128 x 4096 x 4096, 64 x 2048 x
+   * 2048; not 128 x 8192 x 2048).  Needs a workspace
+   * (hipgemm_workspace_size) when it splits K. */
   HIPGEMM_VARIANT_SKINNY = 3,
   /* 512 threads (8 waves, two per SIMD, in two groups that alternate
    * between LDS/DMA work and MFMAs), 256 x 256 tile, each wave 128 x 64 of
@@ -87,8 +87,8 @@ enum {
    * ones fill at most half of them (unless M or N >= 8192 and K >= 4096),
    * or for K <= 2048 on at most 128 tiles
    * of 256 x 256, for 64 < M <= 128 (except as under SKINNY), and for
-   * 32 < M <= 64 where N >= 12288, or above 48 rows K >= 12288 (except as
-   * under SKINNY).  Splits K
+   * 32 < M <= 64 where K <= 1024, N >= 12288, or above 48 rows K >= 12288
+   * (except as under SKINNY).  Splits K
    * into slices when its tiles fill at most a quarter of the CUs and K has
    * at least 16 steps of 128 bytes, or at most half of them and K has at
    * least 64 steps (CUs / tiles slices: 2, or 3 for 65-85 tiles on 256

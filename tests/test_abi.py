@@ -54,6 +54,10 @@ def test_version_and_variants():
     assert hg.select_variant(128, 4096, 4096) == 3   # half-filled K-split
     assert hg.select_variant(128, 8192, 2048) == 5   # ... of 2 slices only
     assert hg.select_variant(64, 8192, 2048) == 3
+    assert hg.select_variant(64, 2048, 2048) == 3    # half-filled, B_T of 4 MiB
+    assert hg.select_variant(48, 1024, 1024) == 5    # 33-64 rows, K <= 1024
+    assert hg.select_variant(100, 1536, 8192) == 5   # 65-128 rows, N < 2048
+    assert hg.select_variant(120, 2560, 4096) == 3
     assert hg.select_variant(65, 2048, 8192) == 3
     assert hg.select_variant(64, 8192, 8192) == 6
     assert hg.select_variant(16, 8192, 8192) == 6

@@ -1,11 +1,11 @@
 """GPU parity of AUTO's picks in the regions its rules name one by one
-(hipgemm_select_variant): 33-64 rows (the split-K schedule on half-filled
-K-splits, the 128 x 128 one for wide N or, above 48 rows, long K, the strip
-elsewhere), and M > 128 where 128 x 128 tiles take under two rounds while
-256 x 256 ones fill at most half the CUs.  Each case checks the pick, then
-runs AUTO through the plain entry point (a workspace allocated for the call)
-and through the workspace entry point on ternary inputs (every sum exact):
-both must equal the oracle bit for bit.
+(hipgemm_select_variant): 33-128 rows (the split-K schedule on half-filled
+K-splits, the 128 x 128 one for short K, wide N or, above 48 rows, long K,
+the strip elsewhere up to 64 rows), and M > 128 where 128 x 128 tiles take
+under two rounds while 256 x 256 ones fill at most half the CUs.  Each case
+checks the pick, then runs AUTO through the plain entry point (a workspace
+allocated for the call) and through the workspace entry point on ternary
+inputs (every sum exact): both must equal the oracle bit for bit.
 """
 import numpy as np
 import pytest
@@ -23,6 +23,9 @@ TERNARY = np.array([0xB8, 0x00, 0x38], np.uint8)  # -1, 0, +1
     (64, 4096, 4096, "skinny"),     # half-filled K-split, 16 MiB of B_T
     (40, 2048, 8192, "skinny"),
     (128, 6144, 2048, "tile128"),   # half-filled, but 2 slices
+    (64, 2048, 2048, "skinny"),     # half-filled, small B_T
+    (48, 1024, 1024, "tile128"),    # 33-64 rows, K <= 1024
+    (120, 2560, 4096, "skinny"),
     (40, 28672, 4096, "tile128"),   # N >= 12288
     (36, 14336, 4096, "tile128"),
     (64, 8192, 14336, "tile128"),   # above 48 rows, K >= 12288
