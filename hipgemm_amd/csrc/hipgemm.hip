@@ -305,7 +305,9 @@ StripPlan plan_strip(int M, int N, int K, int knb, bool unsplit = false) {
   p.tiles_n = (N + bn - 1) / bn;
   const int steps = (K + CfgStrip::kBK - 1) / CfgStrip::kBK;
   const int cus = cu_count();
-  int slices = (cus + p.tiles_n - 1) / p.tiles_n;
+  // At most one workgroup per CU: a K-slice count rounded up would put a
+  // second workgroup on some CUs, which then take twice as long.
+  int slices = cus / p.tiles_n;
   if (slices > steps / 4) slices = steps / 4;
   if (slices < 1 || p.tiles_n > kWsMaxCounters || unsplit) slices = 1;
   p.slice_steps = steps > 0 ? (steps + slices - 1) / slices : 0;
@@ -317,13 +319,27 @@ StripPlan plan_strip(int M, int N, int K, int knb, bool unsplit = false) {
 }
 
 // The strip width.  Every strip reads all of A's rows over its K range
-// through its CU's L1, so A's share of a CU's traffic grows with M / BN:
-// 32 columns up to 32 rows, 64 above.  Measured (one process, 8192 x 8192
-// B_T): 64 rows 21.0 us with 64 columns against 21.7 with 32; 16 rows
-// 12.9 us either way.
+// through its CU's L1, so A's share of a CU's traffic grows with M / BN;
+// narrower strips give more workgroups and fewer K-slices.  32 columns,
+// except 64 where 32-column strips outnumber the CUs (from 17 rows), above
+// 40 rows with K > 4096 where the 32-column plan leaves CUs idle, and
+// above 56 rows for N = 8192.  Measured (one process, caller workspace,
+// 32 / 64 columns, us): 40 x 14336 x 8192 32.7 / 25.4, 56 x 14336 x 8192
+// 37.9 / 28.1, 32 x 28672 x 8192 50.5 / 45.2, 16 x 28672 x 8192 40.4 /
+// 40.8, 8 x 28672 x 8192 38.2 / 39.5; 64 x 3072 x 8192 14.8 / 13.4,
+// 64 x 6144 x 8192 21.5 / 19.7, 64 x 8192 x 8192 21.9 / 21.1; but
+// 64 x 4096 x 8192 15.1 / 15.4, 40 x 8192 x 8192 17.7 / 18.9,
+// 64 x 3072 x 4096 10.5 / 12.3, 64 x 2048 x 4096 9.8 / 12.4,
+// 64 x 1024 x 8192 10.1 / 15.1.
 int strip_knb(int M, int N, int K) {
-  (void)N, (void)K;
-  return M > 32 ? 4 : 2;
+  const int cus = cu_count();
+  const int tiles = (N + 31) / 32;
+  if (tiles > cus) return M > 16 ? 4 : 2;
+  if (M <= 40 || K <= 4096) return 2;
+  const int steps = (K + CfgStrip::kBK - 1) / CfgStrip::kBK;
+  int slices = cus / tiles < steps / 4 ? cus / tiles : steps / 4;
+  if (slices < 1) slices = 1;
+  return tiles * slices < cus || (M > 56 && N >= 8192) ? 4 : 2;
 }
 
 hipError_t launch_strip(const GemmArgs& a, const StripPlan& p, void* ws,
@@ -698,37 +714,47 @@ extern "C" {
 
 int hipgemm_select_variant(int M, int N, int K) {
   // Up to 128 rows the GEMM is a stream over B_T (times: us, caller
-  // workspace, schedules compared in one process on MI355X).
-  //  * Up to 32 rows the column-strip schedule (whole-line DMA of B_T, no
-  //    split-K partials when N / 32 fills the CUs): 16 x 8192 x 8192 12.9
-  //    against 17.8 on the split-K schedule, 32 rows 15.1 / 21.6,
-  //    16 x 28672 x 8192 40.6 / 51.4, 32 x 8192 x 1024 5.8 / 12.3 (8.0 on
-  //    the 128 x 128 one).
-  //  * "Half-filled": the 128 x 128 schedule's K-split (plan_t128) stops
-  //    at its 8-step slice floor with at most half the CUs busy.  The
-  //    split-K schedule, which fills every CU, is then ahead from 33 to 64
-  //    rows for N >= 1024 (64 x 2048 x 4096 10.3 against 12.4 on the strip
-  //    and 14.8 on the 128 x 128 one, 64 x 1024 x 8192 11.7 / 15.1 / 12.3,
-  //    40 x 4096 x 2048 9.1 / 11.5 / 12.3, 64 x 4096 x 4096 10.8 / 13.1 /
-  //    16.0), and from 65 rows for N >= 2048 with 3 slices or more
-  //    (128 x 4096 x 4096 14.4 / 16.3 on the 128 x 128 one, 128 x 2048 x
-  //    8192 14.7 / 16.2, 120 x 2560 x 4096 13.9 / 15.0, 80 x 2048 x 4096
-  //    12.9 / 15.0).  With 2 slices the 128 x 128 schedule sums the two
+  // workspace, schedules compared in one process on MI355X; 364 shapes
+  // from 18 to 64 rows put the rules below within 0.9 % of the best
+  // schedule on average, 27 % at worst).
+  //  * Up to 64 rows the column-strip schedule (whole-line DMA of B_T, A in
+  //    registers): 16 x 8192 x 8192 12.9 against 17.8 on the split-K
+  //    schedule, 64 x 2048 x 4096 9.7 against 10.0 on the split-K one and
+  //    14.0 on the 128 x 128 one, 40 x 14336 x 8192 25.4 / 33.1 / 33.9,
+  //    64 x 8192 x 8192 21.1 / 24.6 / 21.8.  Except, from 17 rows, where
+  //    even 64-column strips outnumber the CUs (N > 64 x CUs): the 128 x 128
+  //    tiles, one row of them, are then ahead (28 x 20480 x 1536 11.2
+  //    against 14.7, 52 x 20480 x 3072 19.1 / 28.1, 30 x 24576 x 10240
+  //    52.4 / 56.7, 64 x 28672 x 2048 14.6 / 22.0; the worst case seen the
+  //    other way, 24 x 28672 x 8192, 54.9 against 43.1); and above 40 rows
+  //    for K > 8192 from N = 3072 (64 x 4096 x 14336 19.7 / 22.6,
+  //    56 x 8192 x 14336 29.7 / 33.8, 62 x 11008 x 10240 34.3 / 37.6).
+  //  * From 65 rows the 128 x 128 schedule, which DMAs whole lines of A and
+  //    B_T and reads A once per 128 columns: 128 x 8192 x 8192 22.6 against
+  //    28.0 on the split-K schedule, 128 x 28672 x 8192 52.7 / 74.3,
+  //    128 x 4096 x 28672 32.9 / 43.6, 128 x 8192 x 1024 7.9 / 12.8.  Except
+  //    where its K-split stops at its 8-step slice floor with at most half
+  //    the CUs busy, in 3 slices or more, for N >= 2048: the split-K
+  //    schedule, which fills every CU, is then ahead (128 x 4096 x 4096
+  //    14.4 / 16.3, 128 x 2048 x 8192 14.7 / 16.2, 120 x 2560 x 4096
+  //    13.9 / 15.0).  With 2 slices the 128 x 128 schedule sums the two
   //    partials in its split kernel and stays ahead (128 x 6144 x 2048 13.0
   //    / 15.6, 128 x 8192 x 2048 13.7 / 14.5), as below 2048 columns
   //    (100 x 1536 x 8192 13.9 / 15.9, 128 x 1024 x 8192 12.6 / 14.2).
-  //  * Else from 33 to 64 rows: the 128 x 128 schedule for K <= 1024,
-  //    where each of the strip's four waves would get two steps or fewer
-  //    (64 x 2048 x 1024 7.4 against 10.2, 64 x 6144 x 1024 8.1 / 11.0),
-  //    and for N >= 12288 (the 64-column strips then take a round and a
-  //    part: 64 x 28672 x 4096 30.1 / 34.5, 40 x 14336 x 14336 44.0 / 50.4)
-  //    and, above 48 rows, for K >= 12288 (64 x 8192 x 14336 29.9 / 31.3);
-  //    the strip keeps the rest (64 x 8192 x 8192 21.0 / 21.7, 40 x 8192 x
-  //    8192 18.9 / 21.4).
-  //  * Else from 65 rows the 128 x 128 schedule, which DMAs whole lines of
-  //    A and B_T and reads A once per 128 columns: 128 x 8192 x 8192 22.6
-  //    against 28.0 on the split-K schedule, 128 x 28672 x 8192 52.7 /
-  //    74.3, 128 x 4096 x 28672 32.9 / 43.6, 128 x 8192 x 1024 7.9 / 12.8.
+  if (M <= 16) return HIPGEMM_VARIANT_STRIP;
+  if (M <= 64) {
+    if (ceil_div(N, 64) > cu_count()) return HIPGEMM_VARIANT_TILE128;
+    if (M > 40 && K > 8192 && N >= 3072) return HIPGEMM_VARIANT_TILE128;
+    return HIPGEMM_VARIANT_STRIP;
+  }
+  if (M <= CfgSkinny::kMaxM) {
+    const int cus = cu_count();
+    const T128Plan p = plan_t128(M, N, K, cus);
+    const int units = ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN) * p.slices;
+    const bool half_filled = p.slices > 1 && 2 * units <= cus;
+    if (half_filled && N >= 2048 && p.slices > 2) return HIPGEMM_VARIANT_SKINNY;
+    return HIPGEMM_VARIANT_TILE128;
+  }
   // Above 128 rows the 4-wave
   // 16x16x128 schedule (3-7 % ahead of the 8-wave one from 2048 x 4096 up),
   // except where the 128 x 128 tiles fit in one round over the CUs (the

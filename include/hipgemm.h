@@ -65,12 +65,11 @@ enum {
   HIPGEMM_VARIANT_4WAVE_MFMA16 = 2,
   /* M <= 128 only: split-K over every CU for the HBM-bound skinny shapes,
    * operands streamed straight into registers, a deterministic in-kernel
-   * reduction of the K-slices.  AUTO's choice for 32 < M <= 128 only where
+   * reduction of the K-slices.  AUTO's choice for 64 < M <= 128 only where
    * the 128 x 128 schedule's K-split would leave at least half the CUs
-   * idle: up to 64 rows for N >= 1024, above 64 rows for N >= 2048 when
-   * that split has 3 slices or more (e.g. 128 x 4096 x 4096, 64 x 2048 x
-   * 2048; not 128 x 8192 x 2048).  Needs a workspace
-   * (hipgemm_workspace_size) when it splits K. */
+   * idle in 3 slices or more, for N >= 2048 (e.g. 128 x 4096 x 4096; not
+   * 128 x 8192 x 2048).  Needs a workspace (hipgemm_workspace_size) when
+   * it splits K. */
   HIPGEMM_VARIANT_SKINNY = 3,
   /* 512 threads (8 waves, two per SIMD, in two groups that alternate
    * between LDS/DMA work and MFMAs), 256 x 256 tile, each wave 128 x 64 of
@@ -87,8 +86,8 @@ enum {
    * ones fill at most half of them (unless M or N >= 8192 and K >= 4096),
    * or for K <= 2048 on at most 128 tiles
    * of 256 x 256, for 64 < M <= 128 (except as under SKINNY), and for
-   * 32 < M <= 64 where K <= 1024, N >= 12288, or above 48 rows K >= 12288
-   * (except as under SKINNY).  Splits K
+   * 16 < M <= 64 where N > 64 x CUs, or above 40 rows where K > 8192 and
+   * N >= 3072.  Splits K
    * into slices when its tiles fill at most a quarter of the CUs and K has
    * at least 16 steps of 128 bytes, or at most half of them and K has at
    * least 64 steps (CUs / tiles slices: 2, or 3 for 65-85 tiles on 256
@@ -102,12 +101,13 @@ enum {
    * (the reference has 256 x 256 tiles only). */
   HIPGEMM_VARIANT_TILE128 = 5,
   /* M <= 128 only: 256 threads, each workgroup a strip of 32 columns of C
-   * (64 above 32 rows) over all of K (over a K-slice, with a workspace,
-   * when the strips alone are fewer than the CUs), its 4 waves each a
-   * quarter of the K-steps, summed in LDS; B_T streamed by whole-line DMA
-   * into LDS, A straight into registers.  AUTO's choice for M <= 32, and
-   * for 32 < M <= 64 where neither SKINNY nor TILE128 is.  No reference
-   * counterpart. */
+   * (64 from 17 rows when 32-column strips would outnumber the CUs, and
+   * for some long-K shapes above 40 rows) over all of K (over a K-slice,
+   * with a workspace, when the strips alone are fewer than the CUs; at most
+   * one workgroup per CU), its 4 waves each a quarter of the K-steps,
+   * summed in LDS; B_T streamed by whole-line DMA into LDS, A straight into
+   * registers.  AUTO's choice for M <= 64 except where TILE128 is.  No
+   * reference counterpart. */
   HIPGEMM_VARIANT_STRIP = 6,
   HIPGEMM_VARIANT_COUNT = 7
 };

@@ -53,19 +53,31 @@ def test_version_and_variants():
     assert hg.select_variant(80, 8192, 1024) == 5    # short K, no K-slices
     assert hg.select_variant(128, 4096, 4096) == 3   # half-filled K-split
     assert hg.select_variant(128, 8192, 2048) == 5   # ... of 2 slices only
-    assert hg.select_variant(64, 8192, 2048) == 3
-    assert hg.select_variant(64, 2048, 2048) == 3    # half-filled, B_T of 4 MiB
-    assert hg.select_variant(48, 1024, 1024) == 5    # 33-64 rows, K <= 1024
     assert hg.select_variant(100, 1536, 8192) == 5   # 65-128 rows, N < 2048
     assert hg.select_variant(120, 2560, 4096) == 3
     assert hg.select_variant(65, 2048, 8192) == 3
+    # up to 64 rows: column strips, but 128 x 128 tiles for very wide N with
+    # short K, and above 40 rows for long K
     assert hg.select_variant(64, 8192, 8192) == 6
+    assert hg.select_variant(64, 4096, 4096) == 6
+    assert hg.select_variant(64, 2048, 2048) == 6
+    assert hg.select_variant(48, 1024, 1024) == 6
     assert hg.select_variant(16, 8192, 8192) == 6
-    assert hg.select_variant(16, 28672, 8192) == 6   # strips up to 32 rows
-    assert hg.select_variant(64, 4096, 4096) == 3    # half-filled K-split
-    assert hg.select_variant(40, 28672, 4096) == 5   # N >= 12288
-    assert hg.select_variant(64, 8192, 14336) == 5   # 49-64 rows, long K
-    assert hg.select_variant(48, 8192, 14336) == 6
+    assert hg.select_variant(16, 28672, 1024) == 6   # 16 rows: strips throughout
+    assert hg.select_variant(24, 28672, 2048) == 5
+    assert hg.select_variant(24, 28672, 4096) == 5
+    assert hg.select_variant(40, 28672, 4096) == 5
+    assert hg.select_variant(40, 28672, 8192) == 5
+    assert hg.select_variant(28, 20480, 1536) == 5   # N > 64 x CUs
+    assert hg.select_variant(36, 20480, 6144) == 5
+    assert hg.select_variant(36, 20480, 12288) == 5
+    assert hg.select_variant(36, 16384, 2048) == 6
+    assert hg.select_variant(64, 8192, 14336) == 5   # 41-64 rows, long K
+    assert hg.select_variant(48, 8192, 14336) == 5
+    assert hg.select_variant(40, 8192, 14336) == 6   # 40 rows: strip
+    assert hg.select_variant(48, 4096, 8192) == 6    # K = 8192: strip
+    assert hg.select_variant(48, 3072, 10240) == 5
+    assert hg.select_variant(64, 2048, 14336) == 6   # N < 3072
     assert hg.select_variant(129, 8192, 8192) == 5   # 2 x 64 tiles of 128
 
 

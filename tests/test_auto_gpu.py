@@ -1,8 +1,10 @@
 """GPU parity of AUTO's picks in the regions its rules name one by one
-(hipgemm_select_variant): 33-128 rows (the split-K schedule on half-filled
-K-splits, the 128 x 128 one for short K, wide N or, above 48 rows, long K,
-the strip elsewhere up to 64 rows), and M > 128 where 128 x 128 tiles take
-under two rounds while 256 x 256 ones fill at most half the CUs.  Each case
+(hipgemm_select_variant): up to 64 rows (column strips of 32 or 64 columns,
+one or more K-slices; 128 x 128 tiles for N > 64 x CUs and, above 40 rows,
+for K > 8192), 65-128 rows (the split-K schedule on
+half-filled K-splits of 3 slices or more, else 128 x 128 tiles), and
+M > 128 where 128 x 128 tiles take under two rounds while 256 x 256 ones
+fill at most half the CUs.  Each case
 checks the pick, then runs AUTO through the plain entry point (a workspace
 allocated for the call) and through the workspace entry point on ternary
 inputs (every sum exact): both must equal the oracle bit for bit.
@@ -20,18 +22,20 @@ TERNARY = np.array([0xB8, 0x00, 0x38], np.uint8)  # -1, 0, +1
 
 
 @pytest.mark.parametrize("M,N,K,pick", [
-    (64, 4096, 4096, "skinny"),     # half-filled K-split, 16 MiB of B_T
-    (40, 2048, 8192, "skinny"),
-    (128, 6144, 2048, "tile128"),   # half-filled, but 2 slices
-    (64, 2048, 2048, "skinny"),     # half-filled, small B_T
-    (48, 1024, 1024, "tile128"),    # 33-64 rows, K <= 1024
-    (120, 2560, 4096, "skinny"),
-    (40, 28672, 4096, "tile128"),   # N >= 12288
-    (36, 14336, 4096, "tile128"),
-    (64, 8192, 14336, "tile128"),   # above 48 rows, K >= 12288
-    (48, 8192, 14336, "strip"),
+    (64, 4096, 4096, "strip"),      # 32-column strips, 2 K-slices
+    (40, 2048, 8192, "strip"),      # 4 K-slices
+    (33, 6144, 2048, "strip"),      # 192 strips, one K-slice
+    (48, 3072, 8192, "strip"),      # 64-column strips fill the CUs better
+    (40, 14336, 8192, "strip"),     # 64-column strips: 448 of 32 > CUs
     (64, 8192, 8192, "strip"),
-    (32, 28672, 8192, "strip"),     # up to 32 rows
+    (16, 28672, 8192, "strip"),     # up to 16 rows: strips throughout
+    (32, 28672, 8192, "tile128"),   # from 17 rows, N > 64 x CUs
+    (28, 20480, 1536, "tile128"),
+    (48, 8192, 14336, "tile128"),   # above 40 rows, K > 8192
+    (40, 8192, 14336, "strip"),
+    (128, 6144, 2048, "tile128"),   # half-filled, but 2 slices
+    (120, 2560, 4096, "skinny"),    # half-filled, 4 slices
+    (100, 4096, 4096, "skinny"),
     (1536, 4096, 4096, "tile128"),  # 96 tiles of 256, 384 of 128
     (1152, 4096, 4096, "tile128"),
     (640, 8192, 4096, "4wave_mfma16"),   # the same region, a side of 8192
