@@ -729,10 +729,15 @@ int hipgemm_select_variant(int M, int N, int K) {
   //    other way, 24 x 28672 x 8192, 54.9 against 43.1); and above 40 rows
   //    for K > 8192 from N = 3072 (64 x 4096 x 14336 19.7 / 22.6,
   //    56 x 8192 x 14336 29.7 / 33.8, 62 x 11008 x 10240 34.3 / 37.6).
-  //  * From 65 rows the 128 x 128 schedule, which DMAs whole lines of A and
+  //  * From 65 rows the strip still for a B_T of at most 8 MiB (96 x 2048 x
+  //    4096 12.0 against 13.0 on the split-K schedule and 15.1 on the
+  //    128 x 128 one, 72 x 1024 x 8192 12.1 / 13.9 / 12.4, 128 x 2048 x
+  //    2048 11.4 / 12.8 / 11.9; 54 shapes from 72 to 128 rows: within
+  //    0.6 % of the best on average).  Above that the 128 x 128 schedule,
+  //    which DMAs whole lines of A and
   //    B_T and reads A once per 128 columns: 128 x 8192 x 8192 22.6 against
   //    28.0 on the split-K schedule, 128 x 28672 x 8192 52.7 / 74.3,
-  //    128 x 4096 x 28672 32.9 / 43.6, 128 x 8192 x 1024 7.9 / 12.8.  Except
+  //    128 x 4096 x 28672 32.9 / 43.6.  Except
   //    where its K-split stops at its 8-step slice floor with at most half
   //    the CUs busy, in 3 slices or more, for N >= 2048: the split-K
   //    schedule, which fills every CU, is then ahead (128 x 4096 x 4096
@@ -740,7 +745,7 @@ int hipgemm_select_variant(int M, int N, int K) {
   //    13.9 / 15.0).  With 2 slices the 128 x 128 schedule sums the two
   //    partials in its split kernel and stays ahead (128 x 6144 x 2048 13.0
   //    / 15.6, 128 x 8192 x 2048 13.7 / 14.5), as below 2048 columns
-  //    (100 x 1536 x 8192 13.9 / 15.9, 128 x 1024 x 8192 12.6 / 14.2).
+  //    (100 x 1536 x 8192 13.9 / 15.9).
   if (M <= 16) return HIPGEMM_VARIANT_STRIP;
   if (M <= 64) {
     if (ceil_div(N, 64) > cu_count()) return HIPGEMM_VARIANT_TILE128;
@@ -748,6 +753,7 @@ int hipgemm_select_variant(int M, int N, int K) {
     return HIPGEMM_VARIANT_STRIP;
   }
   if (M <= CfgSkinny::kMaxM) {
+    if ((long long)N * K <= (8ll << 20)) return HIPGEMM_VARIANT_STRIP;
     const int cus = cu_count();
     const T128Plan p = plan_t128(M, N, K, cus);
     const int units = ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN) * p.slices;
@@ -770,6 +776,7 @@ int hipgemm_select_variant(int M, int N, int K) {
   // returns the 4-wave one then.
   if (M <= 32) return HIPGEMM_VARIANT_STRIP;
   if (M <= CfgSkinny::kMaxM) {
+    if ((long long)N * K <= (8ll << 20)) return HIPGEMM_VARIANT_STRIP;
     const int cus = cu_count();
     const T128Plan p = plan_t128(M, N, K, cus);
     const int units = ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN) * p.slices;

@@ -66,9 +66,9 @@ enum {
   /* M <= 128 only: split-K over every CU for the HBM-bound skinny shapes,
    * operands streamed straight into registers, a deterministic in-kernel
    * reduction of the K-slices.  AUTO's choice for 64 < M <= 128 only where
-   * the 128 x 128 schedule's K-split would leave at least half the CUs
-   * idle in 3 slices or more, for N >= 2048 (e.g. 128 x 4096 x 4096; not
-   * 128 x 8192 x 2048).  Needs a workspace (hipgemm_workspace_size) when
+   * B_T exceeds 8 MiB and the 128 x 128 schedule's K-split would leave at
+   * least half the CUs idle in 3 slices or more, for N >= 2048 (e.g.
+   * 128 x 4096 x 4096; not 128 x 8192 x 2048).  Needs a workspace (hipgemm_workspace_size) when
    * it splits K. */
   HIPGEMM_VARIANT_SKINNY = 3,
   /* 512 threads (8 waves, two per SIMD, in two groups that alternate
@@ -85,7 +85,8 @@ enum {
    * fit in one round over the CUs, or in less than two where the 256 x 256
    * ones fill at most half of them (unless M or N >= 8192 and K >= 4096),
    * or for K <= 2048 on at most 128 tiles
-   * of 256 x 256, for 64 < M <= 128 (except as under SKINNY), and for
+   * of 256 x 256, for 64 < M <= 128 (except as under STRIP and SKINNY),
+   * and for
    * 16 < M <= 64 where N > 64 x CUs, or above 40 rows where K > 8192 and
    * N >= 3072.  Splits K
    * into slices when its tiles fill at most a quarter of the CUs and K has
@@ -106,8 +107,9 @@ enum {
    * with a workspace, when the strips alone are fewer than the CUs; at most
    * one workgroup per CU), its 4 waves each a quarter of the K-steps,
    * summed in LDS; B_T streamed by whole-line DMA into LDS, A straight into
-   * registers.  AUTO's choice for M <= 64 except where TILE128 is.  No
-   * reference counterpart. */
+   * registers.  AUTO's choice for M <= 64 except where TILE128 is, and for
+   * 64 < M <= 128 with a B_T of at most 8 MiB.  No reference
+   * counterpart. */
   HIPGEMM_VARIANT_STRIP = 6,
   HIPGEMM_VARIANT_COUNT = 7
 };

@@ -50,7 +50,8 @@ def test_version_and_variants():
     assert hg.select_variant(8192, 896, 4096) == 2
     assert hg.select_variant(640, 8192, 2048) == 5    # short K
     assert hg.select_variant(128, 8192, 8192) == 5   # 64 tiles x 4 K-slices
-    assert hg.select_variant(80, 8192, 1024) == 5    # short K, no K-slices
+    assert hg.select_variant(80, 8192, 1024) == 6    # B_T of 8 MiB: strips
+    assert hg.select_variant(96, 2048, 4096) == 6
     assert hg.select_variant(128, 4096, 4096) == 3   # half-filled K-split
     assert hg.select_variant(128, 8192, 2048) == 5   # ... of 2 slices only
     assert hg.select_variant(100, 1536, 8192) == 5   # 65-128 rows, N < 2048

@@ -1,8 +1,9 @@
 """GPU parity of AUTO's picks in the regions its rules name one by one
 (hipgemm_select_variant): up to 64 rows (column strips of 32 or 64 columns,
 one or more K-slices; 128 x 128 tiles for N > 64 x CUs and, above 40 rows,
-for K > 8192), 65-128 rows (the split-K schedule on
-half-filled K-splits of 3 slices or more, else 128 x 128 tiles), and
+for K > 8192), 65-128 rows (strips for a B_T of at most 8 MiB, the
+split-K schedule on half-filled K-splits of 3 slices or more, else 128 x
+128 tiles), and
 M > 128 where 128 x 128 tiles take under two rounds while 256 x 256 ones
 fill at most half the CUs.  Each case
 checks the pick, then runs AUTO through the plain entry point (a workspace
@@ -33,6 +34,7 @@ TERNARY = np.array([0xB8, 0x00, 0x38], np.uint8)  # -1, 0, +1
     (28, 20480, 1536, "tile128"),
     (48, 8192, 14336, "tile128"),   # above 40 rows, K > 8192
     (40, 8192, 14336, "strip"),
+    (96, 2048, 4096, "strip"),      # 65-128 rows, B_T of at most 8 MiB
     (128, 6144, 2048, "tile128"),   # half-filled, but 2 slices
     (120, 2560, 4096, "skinny"),    # half-filled, 4 slices
     (100, 4096, 4096, "skinny"),
