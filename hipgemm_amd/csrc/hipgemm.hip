@@ -320,26 +320,35 @@ StripPlan plan_strip(int M, int N, int K, int knb, bool unsplit = false) {
 
 // The strip width.  Every strip reads all of A's rows over its K range
 // through its CU's L1, so A's share of a CU's traffic grows with M / BN;
-// narrower strips give more workgroups and fewer K-slices.  32 columns,
-// except 64 where 32-column strips outnumber the CUs (from 17 rows), above
-// 40 rows with K > 4096 where the 32-column plan leaves CUs idle, and
-// above 56 rows for N = 8192.  Measured (one process, caller workspace,
-// 32 / 64 columns, us): 40 x 14336 x 8192 32.7 / 25.4, 56 x 14336 x 8192
-// 37.9 / 28.1, 32 x 28672 x 8192 50.5 / 45.2, 16 x 28672 x 8192 40.4 /
-// 40.8, 8 x 28672 x 8192 38.2 / 39.5; 64 x 3072 x 8192 14.8 / 13.4,
-// 64 x 6144 x 8192 21.5 / 19.7, 64 x 8192 x 8192 21.9 / 21.1; but
+// narrower strips give more workgroups, fewer K-slices and smaller partial
+// strips for the last arrival to sum.  32 columns, except 64 where
+// 32-column strips outnumber the CUs (from 17 rows), and above 40 rows
+// with K > 4096 where the 32-column plan fills at most 3/4 of the CUs, or
+// fewer than all of them with K >= 12288 and the 64-column plan in at most
+// 2 K-slices, or at N = 8192 above 56 rows.  Measured (one process, caller
+// workspace, 32 / 64 columns, us): 40 x 14336 x 8192 32.7 / 25.4,
+// 56 x 14336 x 8192 37.9 / 28.1, 32 x 28672 x 8192 50.5 / 45.2,
+// 16 x 28672 x 8192 40.4 / 40.8; 64 x 3072 x 8192 14.8 / 13.4,
+// 64 x 6144 x 8192 21.5 / 19.7, 60 x 7168 x 12288 31.6 / 27.0,
+// 64 x 8192 x 8192 21.9 / 21.1; but 60 x 1536 x 6144 9.7 / 13.4
+// (64-column strips: 10 K-slices), 44 x 3584 x 6144 12.3 / 13.3,
 // 64 x 4096 x 8192 15.1 / 15.4, 40 x 8192 x 8192 17.7 / 18.9,
-// 64 x 3072 x 4096 10.5 / 12.3, 64 x 2048 x 4096 9.8 / 12.4,
-// 64 x 1024 x 8192 10.1 / 15.1.
+// 64 x 2048 x 4096 9.8 / 12.4, 64 x 1024 x 8192 10.1 / 15.1.  Over 54
+// such pairs this choice is 0.2 % behind the faster on average.
 int strip_knb(int M, int N, int K) {
   const int cus = cu_count();
+  const int steps = (K + CfgStrip::kBK - 1) / CfgStrip::kBK;
+  auto slices_of = [&](int strips) {
+    const int s = cus / strips < steps / 4 ? cus / strips : steps / 4;
+    return s < 1 ? 1 : s;
+  };
   const int tiles = (N + 31) / 32;
   if (tiles > cus) return M > 16 ? 4 : 2;
   if (M <= 40 || K <= 4096) return 2;
-  const int steps = (K + CfgStrip::kBK - 1) / CfgStrip::kBK;
-  int slices = cus / tiles < steps / 4 ? cus / tiles : steps / 4;
-  if (slices < 1) slices = 1;
-  return tiles * slices < cus || (M > 56 && N >= 8192) ? 4 : 2;
+  const int busy = tiles * slices_of(tiles);  // workgroups at 32 columns
+  if (4 * busy <= 3 * cus) return 4;
+  if (busy < cus && K >= 12288 && slices_of((N + 63) / 64) <= 2) return 4;
+  return M > 56 && N >= 8192 ? 4 : 2;
 }
 
 hipError_t launch_strip(const GemmArgs& a, const StripPlan& p, void* ws,
@@ -714,9 +723,7 @@ extern "C" {
 
 int hipgemm_select_variant(int M, int N, int K) {
   // Up to 128 rows the GEMM is a stream over B_T (times: us, caller
-  // workspace, schedules compared in one process on MI355X; 364 shapes
-  // from 18 to 64 rows put the rules below within 0.9 % of the best
-  // schedule on average, 27 % at worst).
+  // workspace, schedules compared in one process on MI355X).
   //  * Up to 64 rows the column-strip schedule (whole-line DMA of B_T, A in
   //    registers): 16 x 8192 x 8192 12.9 against 17.8 on the split-K
   //    schedule, 64 x 2048 x 4096 9.7 against 10.0 on the split-K one and
@@ -726,9 +733,15 @@ int hipgemm_select_variant(int M, int N, int K) {
   //    tiles, one row of them, are then ahead (28 x 20480 x 1536 11.2
   //    against 14.7, 52 x 20480 x 3072 19.1 / 28.1, 30 x 24576 x 10240
   //    52.4 / 56.7, 64 x 28672 x 2048 14.6 / 22.0; the worst case seen the
-  //    other way, 24 x 28672 x 8192, 54.9 against 43.1); and above 40 rows
-  //    for K > 8192 from N = 3072 (64 x 4096 x 14336 19.7 / 22.6,
-  //    56 x 8192 x 14336 29.7 / 33.8, 62 x 11008 x 10240 34.3 / 37.6).
+  //    other way, 24 x 28672 x 8192, 54.9 against 43.1); above 32 rows for
+  //    K <= 1024 unless 32-column strips fill between half and all of the
+  //    CUs in one K-slice, each wave then taking 2 of the 8 steps (64 x 2048
+  //    x 1024 7.2 against 8.3, 56 x 14336 x 1024 8.5 / 9.4; but 48 x 8192 x
+  //    1024 8.2 / 6.9); and above 40 rows for K > 8192 from N = 3072
+  //    (64 x 4096 x 14336 19.7 / 22.6, 56 x 8192 x 14336 29.7 / 33.8,
+  //    62 x 11008 x 10240 34.3 / 37.6).  A sweep of 464 shapes up to 128
+  //    rows (python -m hipgemm_amd.sweep) put these rules within 0.5 % of
+  //    the best schedule on average, 26 % at worst.
   //  * From 65 rows the strip still for a B_T of at most 8 MiB (96 x 2048 x
   //    4096 12.0 against 13.0 on the split-K schedule and 15.1 on the
   //    128 x 128 one, 72 x 1024 x 8192 12.1 / 13.9 / 12.4, 128 x 2048 x
@@ -748,7 +761,12 @@ int hipgemm_select_variant(int M, int N, int K) {
   //    (100 x 1536 x 8192 13.9 / 15.9).
   if (M <= 16) return HIPGEMM_VARIANT_STRIP;
   if (M <= 64) {
-    if (ceil_div(N, 64) > cu_count()) return HIPGEMM_VARIANT_TILE128;
+    const int cus = cu_count();
+    if (ceil_div(N, 64) > cus) return HIPGEMM_VARIANT_TILE128;
+    if (M > 32 && K <= 1024) {
+      const int strips = ceil_div(N, 32);
+      if (strips > cus || 2 * strips <= cus) return HIPGEMM_VARIANT_TILE128;
+    }
     if (M > 40 && K > 8192 && N >= 3072) return HIPGEMM_VARIANT_TILE128;
     return HIPGEMM_VARIANT_STRIP;
   }

@@ -87,7 +87,8 @@ enum {
    * or for K <= 2048 on at most 128 tiles
    * of 256 x 256, for 64 < M <= 128 (except as under STRIP and SKINNY),
    * and for
-   * 16 < M <= 64 where N > 64 x CUs, or above 40 rows where K > 8192 and
+   * 16 < M <= 64 where N > 64 x CUs, above 32 rows where K <= 1024 (unless
+   * N / 32 lies in (CUs / 2, CUs]), or above 40 rows where K > 8192 and
    * N >= 3072.  Splits K
    * into slices when its tiles fill at most a quarter of the CUs and K has
    * at least 16 steps of 128 bytes, or at most half of them and K has at

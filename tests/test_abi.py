@@ -62,7 +62,9 @@ def test_version_and_variants():
     assert hg.select_variant(64, 8192, 8192) == 6
     assert hg.select_variant(64, 4096, 4096) == 6
     assert hg.select_variant(64, 2048, 2048) == 6
-    assert hg.select_variant(48, 1024, 1024) == 6
+    assert hg.select_variant(48, 1024, 1024) == 5    # K <= 1024, 32 strips
+    assert hg.select_variant(48, 8192, 1024) == 6    # ... 256 strips
+    assert hg.select_variant(32, 1024, 1024) == 6
     assert hg.select_variant(16, 8192, 8192) == 6
     assert hg.select_variant(16, 28672, 1024) == 6   # 16 rows: strips throughout
     assert hg.select_variant(24, 28672, 2048) == 5
@@ -417,3 +419,16 @@ def test_bench_gpu_monitor_window():
         g = bench.GpuMonitor(0).start()
         g.stop()
         assert not g.ok and g.window(0.0, 1e18) is None
+
+
+def test_sweep_shape_parser():
+    from hipgemm_amd import sweep
+    assert sweep.parse_shapes("64x4096x4096,1X2x3") == [(64, 4096, 4096), (1, 2, 3)]
+    with pytest.raises(ValueError):
+        sweep.parse_shapes("0x1x1")
+    with pytest.raises(ValueError):
+        sweep.parse_shapes("64x4096")
+    assert sweep.parse_grid("16,32:4096:1024,2048") == [
+        (16, 4096, 1024), (16, 4096, 2048), (32, 4096, 1024), (32, 4096, 2048)]
+    with pytest.raises(ValueError):
+        sweep.parse_grid("16:4096")

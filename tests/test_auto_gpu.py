@@ -73,3 +73,19 @@ def test_auto_pick_bit_exact(gpu, oracle, M, N, K, pick):
         f"workspace entry: {int((got != want).sum())} of {M * N} outputs differ")
     if need:
         assert not ws[:16384].cpu().numpy().any(), "counters not left zero"
+
+
+def test_sweep_module_reports_auto(gpu):
+    """hipgemm_amd.sweep times the schedules that take a shape and reports
+    AUTO's pick against the fastest (measurement only)."""
+    import io
+
+    from hipgemm_amd import sweep
+
+    say("case sweep 64x1024x1024 strip/tile128, 128x256x256 all")
+    buf = io.StringIO()
+    r = sweep.sweep([(64, 1024, 1024), (128, 256, 256)], [V["strip"], V["tile128"], V["skinny"]],
+                    rounds=2, launches=10, out=buf)
+    text = buf.getvalue()
+    assert len(r) == 2 and all(x >= 1.0 for x in r), text
+    assert "64x1024x1024:" in text and "summary: 2 shapes" in text
