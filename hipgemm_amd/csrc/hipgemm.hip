@@ -729,19 +729,20 @@ int hipgemm_select_variant(int M, int N, int K) {
   //    schedule, 64 x 2048 x 4096 9.7 against 10.0 on the split-K one and
   //    14.0 on the 128 x 128 one, 40 x 14336 x 8192 25.4 / 33.1 / 33.9,
   //    64 x 8192 x 8192 21.1 / 24.6 / 21.8.  Except, from 17 rows, where
-  //    even 64-column strips outnumber the CUs (N > 64 x CUs): the 128 x 128
-  //    tiles, one row of them, are then ahead (28 x 20480 x 1536 11.2
-  //    against 14.7, 52 x 20480 x 3072 19.1 / 28.1, 30 x 24576 x 10240
-  //    52.4 / 56.7, 64 x 28672 x 2048 14.6 / 22.0; the worst case seen the
-  //    other way, 24 x 28672 x 8192, 54.9 against 43.1); above 32 rows for
+  //    even 64-column strips outnumber the CUs (N > 64 x CUs) -- up to 32
+  //    rows only for K <= 3072: the 128 x 128 tiles, one row of them, are
+  //    then ahead (28 x 20480 x 1024 8.9 against 12.6, 24 x 28672 x 2048
+  //    14.2 / 16.0, 52 x 20480 x 3072 19.1 / 28.1, 34 x 24576 x 10240 52.8 /
+  //    60.6, 64 x 28672 x 2048 14.6 / 22.0; but 24 x 28672 x 8192 55.1 /
+  //    43.3, 20 x 32768 x 4096 34.1 / 26.6); above 32 rows for
   //    K <= 1024 unless 32-column strips fill between half and all of the
   //    CUs in one K-slice, each wave then taking 2 of the 8 steps (64 x 2048
   //    x 1024 7.2 against 8.3, 56 x 14336 x 1024 8.5 / 9.4; but 48 x 8192 x
   //    1024 8.2 / 6.9); and above 40 rows for K > 8192 from N = 3072
   //    (64 x 4096 x 14336 19.7 / 22.6, 56 x 8192 x 14336 29.7 / 33.8,
-  //    62 x 11008 x 10240 34.3 / 37.6).  A sweep of 464 shapes up to 128
+  //    62 x 11008 x 10240 34.3 / 37.6).  A sweep of 584 shapes up to 128
   //    rows (python -m hipgemm_amd.sweep) put these rules within 0.5 % of
-  //    the best schedule on average, 26 % at worst.
+  //    the best schedule on average, 18 % at worst.
   //  * From 65 rows the strip still for a B_T of at most 8 MiB (96 x 2048 x
   //    4096 12.0 against 13.0 on the split-K schedule and 15.1 on the
   //    128 x 128 one, 72 x 1024 x 8192 12.1 / 13.9 / 12.4, 128 x 2048 x
@@ -762,7 +763,7 @@ int hipgemm_select_variant(int M, int N, int K) {
   if (M <= 16) return HIPGEMM_VARIANT_STRIP;
   if (M <= 64) {
     const int cus = cu_count();
-    if (ceil_div(N, 64) > cus) return HIPGEMM_VARIANT_TILE128;
+    if (ceil_div(N, 64) > cus && (M > 32 || K <= 3072)) return HIPGEMM_VARIANT_TILE128;
     if (M > 32 && K <= 1024) {
       const int strips = ceil_div(N, 32);
       if (strips > cus || 2 * strips <= cus) return HIPGEMM_VARIANT_TILE128;

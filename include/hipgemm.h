@@ -83,24 +83,22 @@ enum {
    * times as many tiles as the 256 x 256 schedules, for shapes whose 256 x
    * 256 tiles underfill the CUs: AUTO's choice for M > 128 when its tiles
    * fit in one round over the CUs, or in less than two where the 256 x 256
-   * ones fill at most half of them (unless M or N >= 8192 and K >= 4096),
-   * or for K <= 2048 on at most 128 tiles
-   * of 256 x 256, for 64 < M <= 128 (except as under STRIP and SKINNY),
-   * and for
-   * 16 < M <= 64 where N > 64 x CUs, above 32 rows where K <= 1024 (unless
-   * N / 32 lies in (CUs / 2, CUs]), or above 40 rows where K > 8192 and
-   * N >= 3072.  Splits K
-   * into slices when its tiles fill at most a quarter of the CUs and K has
-   * at least 16 steps of 128 bytes, or at most half of them and K has at
-   * least 64 steps (CUs / tiles slices: 2, or 3 for 65-85 tiles on 256
-   * CUs); a workspace then (hipgemm_workspace_size).  With a caller's
-   * workspace (or hipgemm_gemm_noalloc), the per-tensor epilogue, no MX
-   * scales and at most 4 slices, the slice that finishes a 64 x 64
-   * quadrant last sums it in the same kernel (arrival counters in the
-   * workspace); else a second kernel sums the slices.
-   * A call with no workspace under stream capture runs unsplit (as do the
-   * split-K and strip schedules' calls there).  No reference counterpart
-   * (the reference has 256 x 256 tiles only). */
+   * ones fill at most half of them (unless M or N >= 8192 and K >= 4096), or
+   * for K <= 2048 on at most 128 tiles of 256 x 256, for 64 < M <= 128
+   * (except as under STRIP and SKINNY), and for 16 < M <= 64 where N > 64 x
+   * CUs (up to 32 rows with K <= 3072), above 32 rows where K <= 1024
+   * (unless N / 32 lies in (CUs / 2, CUs]), or above 40 rows where K > 8192
+   * and N >= 3072. Splits K into slices when its tiles fill at most a
+   * quarter of the CUs and K has at least 16 steps of 128 bytes, or at most
+   * half of them and K has at least 64 steps (CUs / tiles slices: 2, or 3
+   * for 65-85 tiles on 256 CUs); a workspace then (hipgemm_workspace_size).
+   * With a caller's workspace (or hipgemm_gemm_noalloc), the per-tensor
+   * epilogue, no MX scales and at most 4 slices, the slice that finishes a
+   * 64 x 64 quadrant last sums it in the same kernel (arrival counters in
+   * the workspace); else a second kernel sums the slices. A call with no
+   * workspace under stream capture runs unsplit (as do the split-K and strip
+   * schedules' calls there). No reference counterpart (the reference has 256
+   * x 256 tiles only). */
   HIPGEMM_VARIANT_TILE128 = 5,
   /* M <= 128 only: 256 threads, each workgroup a strip of 32 columns of C
    * (64 from 17 rows when 32-column strips would outnumber the CUs, and

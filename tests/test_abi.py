@@ -68,7 +68,7 @@ def test_version_and_variants():
     assert hg.select_variant(16, 8192, 8192) == 6
     assert hg.select_variant(16, 28672, 1024) == 6   # 16 rows: strips throughout
     assert hg.select_variant(24, 28672, 2048) == 5
-    assert hg.select_variant(24, 28672, 4096) == 5
+    assert hg.select_variant(24, 28672, 4096) == 6   # up to 32 rows: K <= 3072 only
     assert hg.select_variant(40, 28672, 4096) == 5
     assert hg.select_variant(40, 28672, 8192) == 5
     assert hg.select_variant(28, 20480, 1536) == 5   # N > 64 x CUs

@@ -1,12 +1,11 @@
 """GPU parity of AUTO's picks in the regions its rules name one by one
 (hipgemm_select_variant): up to 64 rows (column strips of 32 or 64 columns,
-one or more K-slices; 128 x 128 tiles for N > 64 x CUs and, above 40 rows,
-for K > 8192), 65-128 rows (strips for a B_T of at most 8 MiB, the
-split-K schedule on half-filled K-splits of 3 slices or more, else 128 x
-128 tiles), and
-M > 128 where 128 x 128 tiles take under two rounds while 256 x 256 ones
-fill at most half the CUs.  Each case
-checks the pick, then runs AUTO through the plain entry point (a workspace
+one or more K-slices; 128 x 128 tiles for N > 64 x CUs (up to 32 rows with K
+<= 3072) and, above 40 rows, for K > 8192), 65-128 rows (strips for a B_T of
+at most 8 MiB, the split-K schedule on half-filled K-splits of 3 slices or
+more, else 128 x 128 tiles), and M > 128 where 128 x 128 tiles take under
+two rounds while 256 x 256 ones fill at most half the CUs. Each case checks
+the pick, then runs AUTO through the plain entry point (a workspace
 allocated for the call) and through the workspace entry point on ternary
 inputs (every sum exact): both must equal the oracle bit for bit.
 """
@@ -30,8 +29,9 @@ TERNARY = np.array([0xB8, 0x00, 0x38], np.uint8)  # -1, 0, +1
     (40, 14336, 8192, "strip"),     # 64-column strips: 448 of 32 > CUs
     (64, 8192, 8192, "strip"),
     (16, 28672, 8192, "strip"),     # up to 16 rows: strips throughout
-    (32, 28672, 8192, "tile128"),   # from 17 rows, N > 64 x CUs
-    (28, 20480, 1536, "tile128"),
+    (32, 28672, 8192, "strip"),     # N > 64 x CUs, but K > 3072
+    (28, 20480, 1536, "tile128"),   # N > 64 x CUs, up to 32 rows K <= 3072
+    (40, 24576, 8192, "tile128"),   # ... any K above 32 rows
     (48, 8192, 14336, "tile128"),   # above 40 rows, K > 8192
     (40, 8192, 14336, "strip"),
     (96, 2048, 4096, "strip"),      # 65-128 rows, B_T of at most 8 MiB
