@@ -793,22 +793,6 @@ int hipgemm_select_variant(int M, int N, int K) {
   // one leads by 3-48 %).  AUTO also splits C between the 4-wave and 128 x
   // 128 schedules for a short last round (hipgemm_split_columns); this
   // returns the 4-wave one then.
-  if (M <= 32) return HIPGEMM_VARIANT_STRIP;
-  if (M <= CfgSkinny::kMaxM) {
-    if ((long long)N * K <= (8ll << 20)) return HIPGEMM_VARIANT_STRIP;
-    const int cus = cu_count();
-    const T128Plan p = plan_t128(M, N, K, cus);
-    const int units = ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN) * p.slices;
-    const bool half_filled = p.slices > 1 && 2 * units <= cus;
-    if (M <= 64) {
-      if (half_filled && N >= 1024) return HIPGEMM_VARIANT_SKINNY;
-      if (K <= 1024) return HIPGEMM_VARIANT_TILE128;
-      if (N < 12288 && (M <= 48 || K < 12288)) return HIPGEMM_VARIANT_STRIP;
-      return HIPGEMM_VARIANT_TILE128;
-    }
-    if (half_filled && N >= 2048 && p.slices > 2) return HIPGEMM_VARIANT_SKINNY;
-    return HIPGEMM_VARIANT_TILE128;
-  }
   const int cus = cu_count();
   const int t1 = ceil_div(M, CfgT128::kBM) * ceil_div(N, CfgT128::kBN);
   if (t1 <= cus) return HIPGEMM_VARIANT_TILE128;
