@@ -432,3 +432,29 @@ def test_sweep_shape_parser():
         (16, 4096, 1024), (16, 4096, 2048), (32, 4096, 1024), (32, 4096, 2048)]
     with pytest.raises(ValueError):
         sweep.parse_grid("16:4096")
+
+
+def test_auto_picks_fit_their_shape_and_the_noalloc_scratch():
+    """Over a grid of shapes: AUTO picks one of the schedules it documents
+    (never the 32x32x64 or 8-wave ones), the skinny-M schedules only up to
+    128 rows, and the workspace its pick needs fits the no-allocation
+    entry point's static scratch (HIPGEMM_NOALLOC_SCRATCH_BYTES), so that
+    entry point takes every shape AUTO does.  (On the CPU the library
+    assumes 256 CUs.)"""
+    scratch = (16 << 10) + (32 << 20)
+    V = hg.VARIANTS
+    rows = [1, 8, 16, 17, 24, 32, 33, 40, 41, 48, 56, 64, 65, 72, 96, 100, 128,
+            129, 200, 256, 384, 512, 640, 1024, 1536, 2048, 4000, 8192]
+    cols = [16, 512, 1000, 1024, 1536, 2048, 3072, 4096, 5000, 6144, 8192,
+            12288, 16384, 17408, 20480, 28672, 32768]
+    ks = [16, 128, 1024, 2048, 3072, 4096, 6144, 8192, 12288, 14336, 28672]
+    for M in rows:
+        for N in cols:
+            for K in ks:
+                v = hg.select_variant(M, N, K)
+                assert v in (V["4wave_mfma16"], V["tile128"], V["skinny"], V["strip"]), (M, N, K, v)
+                if v in (V["skinny"], V["strip"]):
+                    assert M <= 128, (M, N, K, v)
+                ws = hg.workspace_size(M, N, K, 0)
+                assert ws == hg.workspace_size(M, N, K, v), (M, N, K)
+                assert ws <= scratch, (M, N, K, v, ws)
