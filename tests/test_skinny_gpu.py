@@ -110,15 +110,21 @@ def test_skinny_deterministic_and_workspace_left_zero(gpu, oracle):
     assert max_rel <= REL_TOL
 
 
-def test_skinny_plain_entry_allocates_its_workspace(gpu, oracle):
-    """hipgemm_fp8_gemm_bf16 (no workspace argument) takes a stream-ordered
-    allocation for a schedule that splits K (AUTO picks the strip schedule
-    for M <= 64, here with 4 K-slices); the result equals the workspace
-    entry point's."""
+@pytest.mark.parametrize("M,N,K,splits", [
+    (16, 1024, 32768, True),   # 1.5 MiB of A and B_T per strip: K-slices
+    (16, 2048, 4096, False),   # 192 KiB per strip: one K-slice
+])
+def test_strip_plain_entry_without_workspace(gpu, oracle, M, N, K, splits):
+    """hipgemm_fp8_gemm_bf16 (no workspace argument) on the strip schedule:
+    where each strip would stream more than 1 MiB of A and B_T it takes a
+    stream-ordered allocation for its K-slices and equals the workspace
+    entry point bit for bit; below that it runs one K-slice, allocating
+    nothing, and stays within the tolerance of the oracle (its sums run in
+    another order than the workspace entry point's)."""
     torch = gpu
-    M, N, K = 16, 2048, 4096
-    say(f"case skinny-plain M={M} N={N} K={K}")
+    say(f"case strip-plain M={M} N={N} K={K} splits={splits}")
     assert hg.select_variant(M, N, K) == STRIP
+    assert hg.workspace_size(M, N, K, 0) > 0
     A = oracle.fill((M, K), 71, po.UNIFORM, -1.0, 1.0)
     B = oracle.fill((N, K), 72, po.UNIFORM, -1.0, 1.0)
     a, b = to_dev(torch, A), to_dev(torch, B)
@@ -128,9 +134,13 @@ def test_skinny_plain_entry_allocates_its_workspace(gpu, oracle):
                        torch.cuda.current_stream().cuda_stream)
     assert code == 0
     torch.cuda.synchronize()
-    assert hg.workspace_size(M, N, K, 0) > 0
+    C_plain = from_dev_bf16(out)
     C_ws, _, _ = run_ws(torch, A, B, M, N, K, variant=STRIP)
-    assert np.array_equal(from_dev_bf16(out), C_ws)
+    if splits:
+        assert np.array_equal(C_plain, C_ws)
+    max_rel, _, _ = compare(C_plain, oracle.gemm(A, B))
+    say(f"    max_rel={max_rel:.3e}")
+    assert max_rel <= REL_TOL
 
 
 def test_skinny_torch_helper(gpu, oracle):
