@@ -88,7 +88,9 @@ def sweep(shapes, variants, rounds: int = 4, launches: int = 100, out=sys.stdout
             continue
         for v in ok:
             for i in range(launches // 2):
-                launch(v, i)
+                code = launch(v, i)
+                if code != 0:
+                    raise RuntimeError(f"{variant_name(v)} on {M}x{N}x{K}: error {code}")
         torch.cuda.synchronize()
         us = {v: 0.0 for v in ok}
         for r in range(rounds):
