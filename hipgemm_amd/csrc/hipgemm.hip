@@ -900,8 +900,10 @@ size_t hipgemm_gemm_workspace_size(const hipgemm_gemm_desc* d) {
       return 0;
     return plan_t128(d->M, d->N, d->K / 2, cu_count()).ws_bytes;
   }
-  const bool fp6 = d->a_format == HIPGEMM_FMT_FP6_E2M3 ||
-                   d->a_format == HIPGEMM_FMT_FP6_E3M2;
+  auto is6 = [](int f) {
+    return f == HIPGEMM_FMT_FP6_E2M3 || f == HIPGEMM_FMT_FP6_E3M2;
+  };
+  const bool fp6 = is6(d->a_format) || is6(d->b_format);
   if (fp6) {
     if (fp4_variant(d->variant, d->M, d->N, d->K / 4 * 3) ==
         HIPGEMM_VARIANT_4WAVE_MFMA16)
