@@ -30,7 +30,10 @@
 //     makes each lane quad fetch two 32-byte pieces, which measured 2.5 %
 //     slower on this HBM-bound kernel.)
 //   * A (at most 128 rows, read by every strip, so L2-resident) goes
-//     straight into registers, L steps ahead like B.
+//     straight into registers, L steps ahead like B -- except for 32 rows
+//     on 32-column strips, where it takes the same DMA path as B_T into a
+//     ring of its own (CfgStrip::a_in_lds: measured faster there, slower
+//     for 16 rows).
 //   * K order inside a step: lane group g = l / 16 of the MFMA holds
 //     K-chunks g and g + 4 of its row (the instruction's own order), for A
 //     and B alike.
@@ -78,8 +81,17 @@ struct CfgStrip {
   static constexpr int lookahead(int kmb) { return kmb >= 8 ? 2 : 3; }
   // Bytes of one strip's fp32 partial (kMB x kNB blocks of 16 x 16).
   static constexpr int partial_bytes(int kmb, int knb) { return kmb * knb * 1024; }
+  // A staged through LDS by DMA, as B_T is (whole lines), for 32 rows with
+  // 32-column strips, where both rings fit in LDS (less 1 KiB for the
+  // workgroup's other shared variables).  Measured against A in registers:
+  // 32 x {8192 x 8192, 4096 x 14336, 2048 x 8192} 3 to 5 % faster; with 16
+  // rows it is 1 to 22 % slower (16 x 8192 x 8192 15.2 against 12.8 us).
+  static constexpr bool a_in_lds(int kmb, int knb) {
+    return kmb == 2 && 4 * (lookahead(kmb) + 1) * (knb + kmb) * 16 * kBK <= 159 * 1024;
+  }
   static constexpr int lds_bytes(int kmb, int knb) {
-    const int ring = 4 * (lookahead(kmb) + 1) * knb * 16 * kBK;
+    const int rows = 16 * (knb + (a_in_lds(kmb, knb) ? kmb : 0));
+    const int ring = 4 * (lookahead(kmb) + 1) * rows * kBK;
     const int red = 4 * kmb * knb * 1024;
     return ring > red ? ring : red;
   }
@@ -93,11 +105,13 @@ template <int kMB, int kNB, bool kVec8, bool kExt = false, int kFmt = 0>
 __device__ __forceinline__ void gemm_strip_body(const StripArgs& g, lds_u8* lds) {
   using Cfg = CfgStrip;
   constexpr int L = Cfg::lookahead(kMB);
-  constexpr int R = L + 1;                  // ring stages (LDS for B, VGPR for A)
+  constexpr int R = L + 1;                  // ring stages (LDS for B, VGPR or LDS for A)
   constexpr int kBN = 16 * kNB;             // strip width
   constexpr int kStageB = kBN * Cfg::kBK;   // bytes per wave per stage
   constexpr int kDmaB = kBN / 8;            // B DMA per step (8 rows each)
-  constexpr int kLdA = 2 * kMB;             // A loads per step
+  constexpr bool kADma = Cfg::a_in_lds(kMB, kNB);
+  constexpr int kStageA = 16 * kMB * Cfg::kBK;
+  constexpr int kLdA = 2 * kMB;             // A loads (or DMA) per step
   constexpr int kOps = kDmaB + kLdA;        // vmcnt per step
   static_assert(L * kOps < 64, "vmcnt range");
   const int lane = lane_id();
@@ -138,13 +152,19 @@ __device__ __forceinline__ void gemm_strip_body(const StripArgs& g, lds_u8* lds)
 #pragma unroll
   for (int m = 0; m < kMB; ++m)
     voff_a[m] = (uint32_t)(16 * m + r16) * (uint32_t)g.lda + 16u * gq;
+  // A by DMA: instruction j covers rows 8j .. 8j + 7, lanes as for B_T.
+  uint32_t voff_da[kLdA];
+#pragma unroll
+  for (int j = 0; j < kLdA; ++j)
+    voff_da[j] = (uint32_t)(8 * j + drow) * (uint32_t)g.lda + (uint32_t)dch[0] * 16u;
   const int sx = strip_xor(r16);
   lds_u8* ring = lds + wave * R * kStageB;
+  lds_u8* ring_a = lds + 4 * R * kStageB + wave * R * kStageA;
   const uint32_t rd0 = (uint32_t)(r16 * Cfg::kBK + ((gq ^ sx) * 16));
   const uint32_t rd1 = (uint32_t)(r16 * Cfg::kBK + (((gq + 4) ^ sx) * 16));
 
   i32x4 aq[R][kMB][2];
-  // Step i of the wave into ring slot d: A into registers, B into LDS.
+  // Step i of the wave into ring slot d: A into registers (or LDS), B into LDS.
   auto issue = [&](int i, int d) {
     uint32_t k0 = (uint32_t)(kb0 + i * Cfg::kBK);
     asm volatile("" : "+s"(k0));
@@ -156,12 +176,21 @@ __device__ __forceinline__ void gemm_strip_body(const StripArgs& g, lds_u8* lds)
           rsrc_b, (__attribute__((address_space(3))) void*)(ring + d * kStageB + j * 1024),
           16, (int)(voff_b[j] | ok), (int)k0, 0, kStoreC /* nt */);
     }
-    const uint32_t oob0 = (16 * gq < lim) ? 0u : kOobOffset;
-    const uint32_t oob1 = (64 + 16 * gq < lim) ? 0u : kOobOffset;
+    if constexpr (kADma) {
+      const uint32_t ok = (16 * dch[0] < lim) ? 0u : kOobOffset;
 #pragma unroll
-    for (int m = 0; m < kMB; ++m) {
-      aq[d][m][0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a[m] | oob0, k0, 0);
-      aq[d][m][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a[m] | oob1, k0 + 64, 0);
+      for (int j = 0; j < kLdA; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rsrc_a, (__attribute__((address_space(3))) void*)(ring_a + d * kStageA + j * 1024),
+            16, (int)(voff_da[j] | ok), (int)k0, 0, 0);
+    } else {
+      const uint32_t oob0 = (16 * gq < lim) ? 0u : kOobOffset;
+      const uint32_t oob1 = (64 + 16 * gq < lim) ? 0u : kOobOffset;
+#pragma unroll
+      for (int m = 0; m < kMB; ++m) {
+        aq[d][m][0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a[m] | oob0, k0, 0);
+        aq[d][m][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a[m] | oob1, k0 + 64, 0);
+      }
     }
   };
 
@@ -186,10 +215,18 @@ __device__ __forceinline__ void gemm_strip_body(const StripArgs& g, lds_u8* lds)
         const lds_u8* p = ring + d * kStageB + f * 16 * Cfg::kBK;
         b[f] = join(lds_read16(p + rd0), lds_read16(p + rd1));
       }
+      i32x8 al[kMB];
+      if constexpr (kADma) {
+#pragma unroll
+        for (int m = 0; m < kMB; ++m) {
+          const lds_u8* p = ring_a + d * kStageA + m * 16 * Cfg::kBK;
+          al[m] = join(lds_read16(p + rd0), lds_read16(p + rd1));
+        }
+      }
       wait_lgkmcnt<0>();
 #pragma unroll
       for (int m = 0; m < kMB; ++m) {
-        const i32x8 a = join(aq[d][m][0], aq[d][m][1]);
+        const i32x8 a = kADma ? al[m] : join(aq[d][m][0], aq[d][m][1]);
 #pragma unroll
         for (int f = 0; f < kNB; ++f)
           acc[m][f] = mfma_16x16x128<fmt_b(kFmt), fmt_a(kFmt)>(b[f], a, acc[m][f]);
