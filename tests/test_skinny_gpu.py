@@ -58,6 +58,9 @@ def run_ws(torch, A, B, M, N, K, ldc=None, sa=None, sb=None, variant=SKINNY,
     (1, 300, 16), (16, 8192, 8192), (17, 1000, 272), (33, 4100, 1040),
     (64, 512, 4096), (100, 2050, 528), (128, 8192, 8192), (5, 260, 8192),
     (32, 8192, 8192), (128, 2048, 8192), (20, 16384, 1024), (48, 70, 4112),
+    # 17-32 rows on 32-column strips (A staged through LDS): K tails,
+    # ragged N, many K-slices
+    (24, 3000, 4112), (31, 96, 20000), (29, 5000, 1008),
     # long K: the split-K plan takes two workgroups per CU (8 and 16 slices)
     (128, 8192, 12288), (96, 4096, 28672)])
 def test_skinny_ternary_bit_exact(gpu, oracle, M, N, K, variant):
