@@ -299,7 +299,11 @@ struct StripPlan {
 
 StripPlan plan_strip(int M, int N, int K, int knb, bool unsplit = false) {
   StripPlan p{};
-  p.kmb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+  // 16-row blocks: 1, 2, 3, 4 or 8.  Three for 33-48 rows instead of four
+  // (A loads and MFMA for the rows that exist): same process, bit-identical,
+  // 4-6 % faster (40 x 8192 x 8192 17.74 -> 16.82 us, 48 x 28672 x 4096
+  // 31.69 -> 29.96, 40 x 4096 x 4096 9.68 -> 9.21).
+  p.kmb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 48 ? 3 : M <= 64 ? 4 : 8;
   p.knb = knb;
   const int bn = 16 * knb;
   p.tiles_n = (N + bn - 1) / bn;

@@ -19,6 +19,7 @@ const void* sel_mb(int kmb, F&& f) {
   switch (kmb) {
     case 1: return f(ic<1>{});
     case 2: return f(ic<2>{});
+    case 3: return f(ic<3>{});
     case 4: return f(ic<4>{});
     case 8: return f(ic<8>{});
     default: return nullptr;

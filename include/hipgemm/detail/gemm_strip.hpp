@@ -97,7 +97,8 @@ struct CfgStrip {
   }
 };
 
-// kMB: 16-row blocks of M (M <= 16 kMB).  kNB: 16-column blocks per strip.
+// kMB: 16-row blocks of M (M <= 16 kMB; 1, 2, 3, 4 or 8).  kNB: 16-column
+// blocks per strip.
 // kVec8: 8-byte C stores (N, ldc multiples of 4, C 8-byte aligned; 2-byte
 // output types).  kExt: the extended epilogue of epilogue.hpp, output type
 // and activation chosen at run time.
