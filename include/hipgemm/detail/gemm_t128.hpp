@@ -29,6 +29,19 @@
 // loads.  Steps per tile are padded to an even count >= kStages (padding
 // steps read zeros).
 //
+// K order: the workgroups of XCD x (blockIdx % 8) start each unit at step
+// x * steps / 8 of its range and wrap around (not with MX scales, whose
+// scale words follow the plain order).  Started together at step 0, every
+// workgroup's DMA of a step falls at the same offset of each operand row, and
+// with row strides that are a multiple of 4096 bytes all those rows meet at
+// one offset within 4 KiB -- which measured as an HBM-bound stall; one start
+// per XCD keeps the workgroups of an XCD (which share operand panels in
+// their L2) in step.  Same process, against starting at step 0: 40 x 28672
+// x 4096 +19 %, 40 x 28672 x 8192 +27 %, 16 x 28672 x 4096 +24 %, 64 x
+// 16384 x 8192 +29 %, 96 x 28672 x 4096 +15 %, 4096 x 1536 x 4096 +5 %,
+// 512 x 4096 x 8192, 2048 x 2048 x 8192 and 4000 x 904 x 3584 within 1 %.
+// The fp32 sums run in that rotated order (deterministic per launch shape).
+//
 // LDS layout: 128-byte rows with the slot_xor swizzle in the instruction K
 // order (layout.hpp).  A lane reads K-chunks g and g + 4 of its row
 // (g = lane / 16; lane group g of the MFMA holds K 16g .. 16g + 15 and
@@ -170,6 +183,8 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   };
   Src cur = src_of(t);
   Src nxt = src_of(t + walk.stride);
+  // First step of this workgroup's units (K order, above).
+  const int krot = kMx ? 0 : (int)((blockIdx.x & 7u) * (unsigned)steps / 8u);
 
   // DMA of tile-local step d (d >= steps_pad: step d - steps_pad of the next
   // tile) into `stage`, instruction n (0-3: A rows, 4-7: B rows).  K-chunks
@@ -177,7 +192,11 @@ __device__ __forceinline__ void gemm_t128_body(const GemmArgs& g, lds_u8* lds) {
   auto dma_one = [&](int d, int stage, int n) {
     const bool next = d >= steps_pad;
     const Src& s = next ? nxt : cur;
-    uint32_t k0 = s.k0 + (uint32_t)(next ? d - steps_pad : d) * kStepBytes;
+    const int dd = next ? d - steps_pad : d;  // step of the unit
+    int dr = dd + krot;                        // the step it loads
+    if (dr >= steps) dr -= steps;
+    if (dd >= steps) dr = dd;                  // padding: past the range
+    uint32_t k0 = s.k0 + (uint32_t)dr * kStepBytes;
     asm volatile("" : "+s"(k0));
     const bool ok = (int)(k0 + dchunk * 16) < s.kend && (!k6 || dchunk < 6);
     lds_u8* base = lds + stage * Cfg::kStage;
