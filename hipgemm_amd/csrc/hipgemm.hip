@@ -740,20 +740,22 @@ int hipgemm_select_variant(int M, int N, int K) {
   //    schedule, 64 x 2048 x 4096 9.7 against 10.0 on the split-K one and
   //    14.0 on the 128 x 128 one, 40 x 14336 x 8192 25.4 / 33.1 / 33.9,
   //    64 x 8192 x 8192 21.1 / 24.6 / 21.8.  Except, from 17 rows, where
-  //    even 64-column strips outnumber the CUs (N > 64 x CUs) -- up to 32
-  //    rows only for K <= 3072: the 128 x 128 tiles, one row of them, are
-  //    then ahead (28 x 20480 x 1024 8.9 against 12.6, 24 x 28672 x 2048
-  //    14.2 / 16.0, 52 x 20480 x 3072 19.1 / 28.1, 34 x 24576 x 10240 52.8 /
-  //    60.6, 64 x 28672 x 2048 14.6 / 22.0; but 24 x 28672 x 8192 55.1 /
-  //    43.3, 20 x 32768 x 4096 34.1 / 26.6); above 32 rows for
-  //    K <= 1024 unless 32-column strips fill between half and all of the
-  //    CUs in one K-slice, each wave then taking 2 of the 8 steps (64 x 2048
-  //    x 1024 7.2 against 8.3, 56 x 14336 x 1024 8.5 / 9.4; but 48 x 8192 x
-  //    1024 8.2 / 6.9); and above 40 rows for K > 8192 from N = 3072
-  //    (64 x 4096 x 14336 19.7 / 22.6, 56 x 8192 x 14336 29.7 / 33.8,
-  //    62 x 11008 x 10240 34.3 / 37.6).  A sweep of 584 shapes up to 128
-  //    rows (python -m hipgemm_amd.sweep) put these rules within 0.5 % of
-  //    the best schedule on average, 18 % at worst.
+  //    even 64-column strips outnumber the CUs (N > 64 x CUs): the 128 x 128
+  //    tiles, one row of them, are then ahead (28 x 20480 x 1024 8.9
+  //    against 12.6, 24 x 28672 x 4096 23.4 / 24.9, 28 x 20480 x 6144
+  //    30.8 / 34.5, 32 x 24576 x 8192 39.8 / 43.4, 52 x 20480 x 3072 19.1 /
+  //    28.1, 64 x 28672 x 2048 14.6 / 22.0; at 16 rows the strip keeps
+  //    them: 16 x 28672 x 4096 22.9 / 23.8); above 32 rows for K <= 1024
+  //    unless 32-column strips fill between a quarter and all of the CUs in
+  //    one K-slice (64 x 2048 x 1024 7.2 against 8.3, 56 x 14336 x 1024
+  //    8.5 / 9.4, 44 x 2048 x 1024 7.3 / 7.8; but 48 x 8192 x 1024 8.1 /
+  //    6.5, 40 x 3072 x 1024 8.0 / 7.5); and above 48 rows for K > 8192
+  //    from N = 3072 (64 x 4096 x 14336 19.7 / 22.6, 56 x 8192 x 14336
+  //    29.7 / 33.8, 62 x 11008 x 10240 34.3 / 37.6; 33-48 rows run as
+  //    three 16-row blocks and keep the strip: 44 x 5120 x 12288 21.5 /
+  //    18.5).  Sweeps of 584 shapes up to 128 rows and 630 from 34 to 48
+  //    rows (python -m hipgemm_amd.sweep) put these rules within 0.4 % of
+  //    the best schedule on average up to 64 rows.
   //  * From 65 rows the strip still for a B_T of at most 8 MiB (96 x 2048 x
   //    4096 12.0 against 13.0 on the split-K schedule and 15.1 on the
   //    128 x 128 one, 72 x 1024 x 8192 12.1 / 13.9 / 12.4, 128 x 2048 x
@@ -774,12 +776,12 @@ int hipgemm_select_variant(int M, int N, int K) {
   if (M <= 16) return HIPGEMM_VARIANT_STRIP;
   if (M <= 64) {
     const int cus = cu_count();
-    if (ceil_div(N, 64) > cus && (M > 32 || K <= 3072)) return HIPGEMM_VARIANT_TILE128;
+    if (ceil_div(N, 64) > cus) return HIPGEMM_VARIANT_TILE128;
     if (M > 32 && K <= 1024) {
       const int strips = ceil_div(N, 32);
-      if (strips > cus || 2 * strips <= cus) return HIPGEMM_VARIANT_TILE128;
+      if (strips > cus || 4 * strips <= cus) return HIPGEMM_VARIANT_TILE128;
     }
-    if (M > 40 && K > 8192 && N >= 3072) return HIPGEMM_VARIANT_TILE128;
+    if (M > 48 && K > 8192 && N >= 3072) return HIPGEMM_VARIANT_TILE128;
     return HIPGEMM_VARIANT_STRIP;
   }
   if (M <= CfgSkinny::kMaxM) {

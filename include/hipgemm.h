@@ -86,9 +86,10 @@ enum {
    * ones fill at most half of them (unless M or N >= 8192 and K >= 4096), or
    * for K <= 2048 on at most 128 tiles of 256 x 256, for 64 < M <= 128
    * (except as under STRIP and SKINNY), and for 16 < M <= 64 where N > 64 x
-   * CUs (up to 32 rows with K <= 3072), above 32 rows where K <= 1024
-   * (unless N / 32 lies in (CUs / 2, CUs]), or above 40 rows where K > 8192
-   * and N >= 3072. Splits K into slices when its tiles fill at most a
+   * CUs, above 32 rows where K <= 1024 (unless N / 32 lies in (CUs / 4,
+   * CUs]), or above 48 rows where K > 8192 and N >= 3072. The workgroups
+   * of each XCD start their K walk at their own step (a different order of
+   * the fp32 sums per XCD). Splits K into slices when its tiles fill at most a
    * quarter of the CUs and K has at least 16 steps of 128 bytes, or at most
    * half of them and K has at least 64 steps (CUs / tiles slices: 2, or 3
    * for 65-85 tiles on 256 CUs); a workspace then (hipgemm_workspace_size).
@@ -106,7 +107,8 @@ enum {
    * with a workspace, when the strips alone are fewer than the CUs; at most
    * one workgroup per CU), its 4 waves each a quarter of the K-steps,
    * summed in LDS; B_T streamed by whole-line DMA into LDS, A straight into
-   * registers.  AUTO's choice for M <= 64 except where TILE128 is, and for
+   * registers (through LDS as well for 17-32 rows on 32-column strips).
+   * AUTO's choice for M <= 64 except where TILE128 is, and for
    * 64 < M <= 128 with a B_T of at most 8 MiB.  No reference
    * counterpart. */
   HIPGEMM_VARIANT_STRIP = 6,

@@ -64,11 +64,13 @@ def test_version_and_variants():
     assert hg.select_variant(64, 2048, 2048) == 6
     assert hg.select_variant(48, 1024, 1024) == 5    # K <= 1024, 32 strips
     assert hg.select_variant(48, 8192, 1024) == 6    # ... 256 strips
+    assert hg.select_variant(40, 2048, 1024) == 5    # ... 64 strips: a quarter
+    assert hg.select_variant(40, 3072, 1024) == 6    # ... 96 strips
     assert hg.select_variant(32, 1024, 1024) == 6
     assert hg.select_variant(16, 8192, 8192) == 6
     assert hg.select_variant(16, 28672, 1024) == 6   # 16 rows: strips throughout
     assert hg.select_variant(24, 28672, 2048) == 5
-    assert hg.select_variant(24, 28672, 4096) == 6   # up to 32 rows: K <= 3072 only
+    assert hg.select_variant(24, 28672, 4096) == 5   # from 17 rows, any K
     assert hg.select_variant(40, 28672, 4096) == 5
     assert hg.select_variant(40, 28672, 8192) == 5
     assert hg.select_variant(28, 20480, 1536) == 5   # N > 64 x CUs
@@ -76,10 +78,11 @@ def test_version_and_variants():
     assert hg.select_variant(36, 20480, 12288) == 5
     assert hg.select_variant(36, 16384, 2048) == 6
     assert hg.select_variant(64, 8192, 14336) == 5   # 41-64 rows, long K
-    assert hg.select_variant(48, 8192, 14336) == 5
+    assert hg.select_variant(48, 8192, 14336) == 6   # 33-48 rows: strip
     assert hg.select_variant(40, 8192, 14336) == 6   # 40 rows: strip
     assert hg.select_variant(48, 4096, 8192) == 6    # K = 8192: strip
-    assert hg.select_variant(48, 3072, 10240) == 5
+    assert hg.select_variant(48, 3072, 10240) == 6
+    assert hg.select_variant(52, 3072, 10240) == 5
     assert hg.select_variant(64, 2048, 14336) == 6   # N < 3072
     assert hg.select_variant(129, 8192, 8192) == 5   # 2 x 64 tiles of 128
 

@@ -1,7 +1,7 @@
 """GPU parity of AUTO's picks in the regions its rules name one by one
 (hipgemm_select_variant): up to 64 rows (column strips of 32 or 64 columns,
-one or more K-slices; 128 x 128 tiles for N > 64 x CUs (up to 32 rows with K
-<= 3072) and, above 40 rows, for K > 8192), 65-128 rows (strips for a B_T of
+one or more K-slices; 128 x 128 tiles for N > 64 x CUs from 17 rows and,
+above 48 rows, for K > 8192), 65-128 rows (strips for a B_T of
 at most 8 MiB, the split-K schedule on half-filled K-splits of 3 slices or
 more, else 128 x 128 tiles), and M > 128 where 128 x 128 tiles take under
 two rounds while 256 x 256 ones fill at most half the CUs. Each case checks
@@ -29,11 +29,13 @@ TERNARY = np.array([0xB8, 0x00, 0x38], np.uint8)  # -1, 0, +1
     (40, 14336, 8192, "strip"),     # 64-column strips: 448 of 32 > CUs
     (64, 8192, 8192, "strip"),
     (16, 28672, 8192, "strip"),     # up to 16 rows: strips throughout
-    (32, 28672, 8192, "strip"),     # N > 64 x CUs, but K > 3072
-    (28, 20480, 1536, "tile128"),   # N > 64 x CUs, up to 32 rows K <= 3072
-    (40, 24576, 8192, "tile128"),   # ... any K above 32 rows
-    (48, 8192, 14336, "tile128"),   # above 40 rows, K > 8192
-    (40, 8192, 14336, "strip"),
+    (32, 28672, 8192, "tile128"),   # N > 64 x CUs from 17 rows
+    (28, 20480, 1536, "tile128"),
+    (40, 24576, 8192, "tile128"),
+    (56, 8192, 14336, "tile128"),   # above 48 rows, K > 8192
+    (48, 8192, 14336, "strip"),     # three 16-row blocks
+    (40, 3072, 1024, "strip"),      # K <= 1024, 96 strips
+    (40, 2048, 1024, "tile128"),    # ... 64 strips
     (96, 2048, 4096, "strip"),      # 65-128 rows, B_T of at most 8 MiB
     (128, 6144, 2048, "tile128"),   # half-filled, but 2 slices
     (120, 2560, 4096, "skinny"),    # half-filled, 4 slices
